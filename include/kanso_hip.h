@@ -1,0 +1,218 @@
+/*
+ * kanso_hip.h — C ABI of libkanso_hip.so, the MI355X (gfx950) implementation of
+ * kanso-infer's ragged continuous-batching attention path.
+ *
+ * Every function is `extern "C"`, takes plain pointers and sizes, and returns an
+ * int status (KANSO_OK = 0, negative on error). The message of the last error on
+ * the calling thread is kanso_last_error(). Shapes the kernels cannot represent are
+ * errors, never silent fallbacks (reference: src/metal/paged_attention.rs:34-38).
+ *
+ * Ownership: the caller owns every buffer named in an argument list (device
+ * memory unless stated otherwise). A kanso_ctx owns only its scratch: split-K
+ * partials, the attention work list and a device status word. A context is not
+ * thread-safe; work is enqueued asynchronously on the caller's stream.
+ *
+ * Device-side validation: conditions that depend on device-resident data (a
+ * context length of 0, a slot outside the pool, a block table too short for a
+ * position) cannot be checked on the host without a synchronisation. The kernels
+ * clamp so they never read or write out of bounds, record the condition in the
+ * context's status word, and kanso_check_device_status() reports it.
+ *
+ * Reference interfaces replaced (paths relative to the kanso-infer tree):
+ *   src/metal/paged_attention.rs:12-22    PagedAttentionParams     -> kanso_paged_attention_params
+ *   src/metal/paged_attention.rs:27-32    num_partitions           -> kanso_paged_attention_num_partitions
+ *   src/metal/paged_attention.rs:39-81    validate_...params       -> kanso_validate_paged_attention_params
+ *   src/metal/paged_attention.rs:193-293  encode_paged_attention_v2-> kanso_paged_attention_v2
+ *   src/model.rs:1689-1714 (mixed-batch per-sequence gqa_attention)-> kanso_ragged_paged_attention
+ *   src/engine.rs:376-402 + src/model.rs:64-116 (step packing)    -> kanso_pack_step
+ *   src/kv_cache/kind.rs:348-374 write_kv_slots                   -> kanso_kv_append
+ *   src/kv_cache/kind.rs:379-387 reset_block                      -> kanso_kv_reset_blocks
+ *   src/weights.rs:43-45 LinearWeight::forward on Q8_0 / Q4_K     -> kanso_gemv_q8_0 / kanso_gemv_q4_k
+ */
+#ifndef KANSO_HIP_H
+#define KANSO_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* hipStream_t, declared opaquely so this header does not need the HIP headers.
+ * NULL means the default (null) stream of the current device. */
+typedef struct ihipStream_t* kanso_stream_t;
+
+typedef struct kanso_ctx kanso_ctx;
+
+/* Status codes (reference EngineError variants, src/error.rs:4-11, become codes). */
+enum {
+    KANSO_OK = 0,
+    KANSO_E_INVALID_ARG = -1,   /* null pointer, zero where non-zero is required  */
+    KANSO_E_INVALID_SHAPE = -2, /* shape outside what the kernels represent       */
+    KANSO_E_OUT_OF_BOUNDS = -3, /* index / slot / length outside its buffer       */
+    KANSO_E_HIP = -4,           /* a HIP runtime call failed                      */
+    KANSO_E_DEVICE_CHECK = -5   /* a device-side validation flag was raised       */
+};
+
+/* Bits of the device status word (kanso_check_device_status). */
+enum {
+    KANSO_DEV_EMPTY_CONTEXT = 1u << 0,    /* context_len == 0 (paged_attention.rs:349-355)   */
+    KANSO_DEV_CONTEXT_OVERFLOW = 1u << 1, /* context_len > table capacity (:342-348)         */
+    KANSO_DEV_QUERY_OVERFLOW = 1u << 2,   /* query rows > context_len (model.rs:1488-1493)   */
+    KANSO_DEV_TABLE_SHORT = 1u << 3,      /* block table shorter than needed (engine.rs:387) */
+    KANSO_DEV_SLOT_OOB = 1u << 4,         /* slot >= num_blocks*block_size (kind.rs:130-137) */
+    KANSO_DEV_BLOCK_OOB = 1u << 5         /* physical block id >= num_blocks                 */
+};
+
+/* KV pool element types.
+ *   F32:  pool [num_blocks][block_size][num_kv_heads][head_dim] f32
+ *         (src/kv_cache/storage.rs:70-76).
+ *   INT8: quant [num_blocks][block_size][num_kv_heads][head_dim] i8 and
+ *         scales [num_blocks][block_size][num_kv_heads] f32, one scale per token per
+ *         KV head (src/kv_cache/quantized_storage.rs:14-21, 452-469).
+ *   Q8_0: quant [num_blocks][block_size][num_kv_heads][head_dim] i8 and
+ *         scales [num_blocks][block_size][num_kv_heads][head_dim/32] f16 (IEEE
+ *         binary16 bits), one scale per 32 elements, quantized with the Q8_0 rule
+ *         of src/quant/q8_0.rs:13-32; head_dim must be a multiple of 32.       */
+enum { KANSO_KV_F32 = 0, KANSO_KV_INT8 = 1, KANSO_KV_Q8_0 = 2 };
+
+/* Same fields, order and types as PagedAttentionParams (src/metal/paged_attention.rs:12-22). */
+typedef struct {
+    uint32_t num_seqs;
+    uint32_t num_heads;
+    uint32_t num_kv_heads;
+    uint32_t head_dim;
+    uint32_t block_size;
+    uint32_t max_num_blocks_per_seq;
+    float scale;
+} kanso_paged_attention_params;
+
+/* Parameters of one ragged (mixed prefill + decode) attention call. */
+typedef struct {
+    uint32_t num_seqs;
+    uint32_t num_heads;
+    uint32_t num_kv_heads;
+    uint32_t head_dim;
+    uint32_t block_size;
+    uint32_t max_num_blocks_per_seq; /* row stride of block_tables                 */
+    float scale;
+    uint32_t total_q;    /* T = cu_seqlens[num_seqs]: query rows in q and out       */
+    uint32_t kv_dtype;   /* KANSO_KV_*                                              */
+    uint32_t num_blocks; /* physical blocks in the pool (bounds check of table ids) */
+    uint32_t max_q_len;  /* upper bound of any sequence's query rows (0 = total_q)  */
+} kanso_ragged_attention_params;
+
+/* One planned sequence of a step, as Engine::step plans it (src/engine.rs:221-226). */
+typedef struct {
+    uint32_t start_pos;    /* position of the first query token                    */
+    uint32_t q_len;        /* tokens this step: 1 for decode, chunk_len for prefill */
+    uint32_t table_offset; /* first entry of this sequence's table in table_arena   */
+    uint32_t table_len;    /* entries of the table                                  */
+    uint32_t token_offset; /* this sequence's token history starts at token_arena[token_offset] */
+} kanso_seq_plan;
+
+/* Device outputs of kanso_pack_step (all caller-owned device buffers). */
+typedef struct {
+    int32_t* cu_seqlens;    /* [S+1] prefix sums of q_len                            */
+    int32_t* seq_of_query;  /* [T]   sequence index of every query row                */
+    int32_t* positions;     /* [T]   start_pos + i                                    */
+    int64_t* slot_mapping;  /* [T]   table[pos / bs] * bs + pos % bs                  */
+    uint32_t* tokens;       /* [T]   token_arena[token_offset + pos]                  */
+    uint32_t* block_tables; /* [S * max_blocks] padded by repeating table[needed-1]   */
+    uint32_t* context_lens; /* [S]   start_pos + q_len                                */
+} kanso_packed_step;
+
+const char* kanso_last_error(void);
+
+/* Context on HIP device `device`. */
+int kanso_create(int device, kanso_ctx** out);
+int kanso_destroy(kanso_ctx* ctx);
+
+/* Synchronises `stream`, reads and clears the device status word. Returns
+ * KANSO_E_DEVICE_CHECK (and the bits in *flags) when any was raised. */
+int kanso_check_device_status(kanso_ctx* ctx, kanso_stream_t stream, uint32_t* flags);
+
+/* ceil(max_num_blocks_per_seq * block_size / 256), at least 1
+ * (src/metal/paged_attention.rs:27-32). */
+uint32_t kanso_paged_attention_num_partitions(const kanso_paged_attention_params* p);
+
+/* Host-side shape validation (src/metal/paged_attention.rs:39-81). This build's
+ * limits: GQA group <= 8, head_dim a power of two in [4, 256]. */
+int kanso_validate_paged_attention_params(const kanso_paged_attention_params* p);
+
+/* Decode attention over an F32 pool: q [num_seqs][num_heads][head_dim], one query
+ * per sequence attending its context_lens[s] tokens through block_tables
+ * [num_seqs][max_num_blocks_per_seq]; out [num_seqs][num_heads][head_dim].
+ * Replaces encode_paged_attention_v2 (src/metal/paged_attention.rs:193-203). */
+int kanso_paged_attention_v2(kanso_ctx* ctx, const kanso_paged_attention_params* p,
+                             const float* q, const float* k_cache, const float* v_cache,
+                             const uint32_t* block_tables, const uint32_t* context_lens,
+                             float* out, kanso_stream_t stream);
+
+/* Ragged attention over a mixed batch. Sequence s owns query rows
+ * cu_seqlens[s]..cu_seqlens[s+1] (q_len rows); row i sits at position
+ * context_lens[s] - q_len + i and attends keys 0..=that position (the offset causal
+ * mask of src/model.rs:1510-1527; a decode row attends its whole context).
+ * q and out are [total_q][num_heads][head_dim] f32. k_scales/v_scales are unused
+ * for KANSO_KV_F32. Query head h reads KV head h / (num_heads/num_kv_heads). */
+int kanso_ragged_paged_attention(kanso_ctx* ctx, const kanso_ragged_attention_params* p,
+                                 const float* q, const void* k_pool, const void* v_pool,
+                                 const void* k_scales, const void* v_scales,
+                                 const uint32_t* block_tables, const int32_t* cu_seqlens,
+                                 const uint32_t* context_lens, float* out,
+                                 kanso_stream_t stream);
+
+/* Packs one scheduler step on the device (src/engine.rs:376-402 and the padding
+ * rule of src/model.rs:64-116). `plan` is a device array of num_seqs entries in plan
+ * order; total_q = sum of q_len and max_blocks = max_s ceil((start+q_len)/bs) (at
+ * least 1) are computed by the caller from the same plan and size the outputs. */
+int kanso_pack_step(kanso_ctx* ctx, const kanso_seq_plan* plan, uint32_t num_seqs,
+                    const uint32_t* token_arena, const uint32_t* table_arena,
+                    uint32_t block_size, uint32_t max_blocks, uint32_t total_q,
+                    const kanso_packed_step* out, kanso_stream_t stream);
+
+/* Writes num_tokens rows of K and V ([num_tokens][num_kv_heads][head_dim] f32) into
+ * pool row slot_mapping[t] (slot = block * block_size + offset), quantizing on the
+ * fly for INT8 / Q8_0 (src/kv_cache/kind.rs:348-374, quantized_storage.rs:143-204). */
+int kanso_kv_append(kanso_ctx* ctx, uint32_t kv_dtype, const float* k, const float* v,
+                    const int64_t* slot_mapping, uint32_t num_tokens, uint32_t num_blocks,
+                    uint32_t block_size, uint32_t num_kv_heads, uint32_t head_dim,
+                    void* k_pool, void* v_pool, void* k_scales, void* v_scales,
+                    kanso_stream_t stream);
+
+/* Erases num_reset physical blocks (device array `blocks`) of one pool: F32 and
+ * quant bytes to 0, INT8 scales to 1.0, Q8_0 scales to 0 (src/kv_cache/storage.rs:
+ * 152-176, quantized_storage.rs:35-40). */
+int kanso_kv_reset_blocks(kanso_ctx* ctx, uint32_t kv_dtype, const uint32_t* blocks,
+                          uint32_t num_reset, uint32_t num_blocks, uint32_t block_size,
+                          uint32_t num_kv_heads, uint32_t head_dim, void* k_pool,
+                          void* v_pool, void* k_scales, void* v_scales,
+                          kanso_stream_t stream);
+
+/* y[b][out] = sum_i W[out][i] * x[b][i] with W in GGUF block_q8_0 layout
+ * ([out][in/32] blocks of {f16 d; i8 qs[32]}, 34 B); in % 32 == 0, batch in 1..64.
+ * Dequantization semantics of src/quant/q8_0.rs:35-39 / 51-93. */
+int kanso_gemv_q8_0(kanso_ctx* ctx, const void* w, const float* x, float* y,
+                    uint32_t out_features, uint32_t in_features, uint32_t batch,
+                    kanso_stream_t stream);
+
+/* Same with W in GGUF block_q4_K layout ([out][in/256] blocks of {f16 d; f16 dmin;
+ * u8 scales[12]; u8 qs[128]}, 144 B); in % 256 == 0. Dequantization semantics of
+ * src/quant/q4_k.rs:16-55. */
+int kanso_gemv_q4_k(kanso_ctx* ctx, const void* w, const float* x, float* y,
+                    uint32_t out_features, uint32_t in_features, uint32_t batch,
+                    kanso_stream_t stream);
+
+/* Timing of the library's own kernels with HIP events on the launch stream.
+ * When enabled, every launch of the named kernel is bracketed by events and the
+ * elapsed times are summed. Names: "attention" (stage 1), "reduce", "gemv",
+ * "append", "pack". */
+int kanso_set_profiling(kanso_ctx* ctx, int enabled);
+int kanso_get_kernel_time(kanso_ctx* ctx, const char* name, double* total_ms,
+                          uint64_t* launches);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* KANSO_HIP_H */

@@ -1,0 +1,312 @@
+"""kanso_infer_amd — MI355X (gfx950) implementation of kanso-infer's ragged
+continuous-batching attention path.
+
+The compute lives in libkanso_hip.so (hand-written HIP, C ABI in
+include/kanso_hip.h). This module is the thin host layer over it: device buffers
+and streams are torch tensors / streams (plumbing only), and every call goes
+through the C ABI. It mirrors the reference's own entry points for the path:
+
+  PagedAttentionParams, paged_attention_num_partitions,
+  validate_paged_attention_params, gpu_paged_attention_v2
+      <- src/metal/paged_attention.rs:12-81, 328-382
+  ragged_paged_attention   <- the mixed-batch attention of src/model.rs:1689-1714
+  pack_step                <- Engine::step packing, src/engine.rs:376-402
+  kv_append / kv_reset_blocks <- KvStorageKind::write_kv_slots / reset_block
+  gemv_q8_0 / gemv_q4_k    <- LinearWeight::forward on Q8_0 / Q4_K weights
+
+Errors are raised as EngineError (src/error.rs:4-11), never swallowed: there is
+no CPU fallback, and a missing library is an error.
+"""
+from __future__ import annotations
+
+import ctypes as C
+from dataclasses import dataclass
+
+import numpy as np
+import torch
+
+from . import _capi
+from ._capi import (KANSO_KV_F32, KANSO_KV_INT8, KANSO_KV_Q8_0, PackedStepC,
+                    PagedAttentionParamsC, RaggedAttentionParamsC, SeqPlanC)
+
+__all__ = [
+    "EngineError", "Context", "PagedAttentionParams", "paged_attention_num_partitions",
+    "validate_paged_attention_params", "gpu_paged_attention_v2", "paged_attention_v2",
+    "ragged_paged_attention", "pack_step", "kv_append", "kv_reset_blocks", "gemv_q8_0",
+    "gemv_q4_k", "KANSO_KV_F32", "KANSO_KV_INT8", "KANSO_KV_Q8_0",
+]
+
+
+class EngineError(RuntimeError):
+    """Error of the path (the reference's EngineError::Metal / ::Model, src/error.rs:4-11)."""
+
+    def __init__(self, code: int, message: str):
+        super().__init__(f"[{code}] {message}")
+        self.code = code
+
+
+def _check(rc: int) -> None:
+    if rc != _capi.KANSO_OK:
+        msg = _capi.load().kanso_last_error().decode(errors="replace")
+        raise EngineError(rc, msg)
+
+
+def _ptr(t: torch.Tensor | None) -> int | None:
+    if t is None:
+        return None
+    if not t.is_cuda:
+        raise EngineError(_capi.KANSO_E_INVALID_ARG, "buffers must be device tensors")
+    if not t.is_contiguous():
+        raise EngineError(_capi.KANSO_E_INVALID_ARG, "buffers must be contiguous")
+    return t.data_ptr()
+
+
+def _stream(stream: torch.cuda.Stream | None) -> int:
+    s = stream if stream is not None else torch.cuda.current_stream()
+    return s.cuda_stream
+
+
+class Context:
+    """A kanso_ctx on one device: owns split-K scratch and the device status word."""
+
+    def __init__(self, device: int = 0):
+        self._lib = _capi.load()
+        torch.cuda.set_device(device)
+        h = C.c_void_p()
+        _check(self._lib.kanso_create(device, C.byref(h)))
+        self.handle = h
+        self.device = device
+
+    def close(self) -> None:
+        if getattr(self, "handle", None):
+            self._lib.kanso_destroy(self.handle)
+            self.handle = None
+
+    def __del__(self):  # pragma: no cover - interpreter teardown order varies
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    def __enter__(self):
+        return self
+
+    def __exit__(self, *exc):
+        self.close()
+
+    def check_device_status(self, stream: torch.cuda.Stream | None = None) -> int:
+        """Synchronises and raises EngineError if a kernel flagged bad input."""
+        flags = C.c_uint32(0)
+        _check(self._lib.kanso_check_device_status(self.handle, _stream(stream), C.byref(flags)))
+        return flags.value
+
+    def set_profiling(self, enabled: bool) -> None:
+        _check(self._lib.kanso_set_profiling(self.handle, int(enabled)))
+
+    def kernel_time(self, name: str) -> tuple[float, int]:
+        """(total ms, launches) of a library kernel timed with HIP events."""
+        ms = C.c_double(0.0)
+        n = C.c_uint64(0)
+        _check(self._lib.kanso_get_kernel_time(self.handle, name.encode(), C.byref(ms), C.byref(n)))
+        return ms.value, n.value
+
+
+# ---------------------------------------------------------------- params mirror
+
+
+@dataclass
+class PagedAttentionParams:
+    """src/metal/paged_attention.rs:12-22 (same fields, same order)."""
+    num_seqs: int
+    num_heads: int
+    num_kv_heads: int
+    head_dim: int
+    block_size: int
+    max_num_blocks_per_seq: int
+    scale: float
+
+    def to_c(self) -> PagedAttentionParamsC:
+        return PagedAttentionParamsC(self.num_seqs, self.num_heads, self.num_kv_heads,
+                                     self.head_dim, self.block_size,
+                                     self.max_num_blocks_per_seq, self.scale)
+
+
+def paged_attention_num_partitions(params: PagedAttentionParams) -> int:
+    """src/metal/paged_attention.rs:27-32."""
+    p = params.to_c()
+    return int(_capi.load().kanso_paged_attention_num_partitions(C.byref(p)))
+
+
+def validate_paged_attention_params(params: PagedAttentionParams) -> None:
+    """src/metal/paged_attention.rs:39-81; raises EngineError on an unrepresentable shape."""
+    p = params.to_c()
+    _check(_capi.load().kanso_validate_paged_attention_params(C.byref(p)))
+
+
+# ---------------------------------------------------------------- attention
+
+
+def paged_attention_v2(ctx: Context, params: PagedAttentionParams, q: torch.Tensor,
+                       k_cache: torch.Tensor, v_cache: torch.Tensor, block_tables: torch.Tensor,
+                       context_lens: torch.Tensor, out: torch.Tensor,
+                       stream: torch.cuda.Stream | None = None) -> None:
+    """Device-buffer decode attention (encode_paged_attention_v2, paged_attention.rs:193-293)."""
+    p = params.to_c()
+    _check(ctx._lib.kanso_paged_attention_v2(
+        ctx.handle, C.byref(p), _ptr(q), _ptr(k_cache), _ptr(v_cache), _ptr(block_tables),
+        _ptr(context_lens), _ptr(out), _stream(stream)))
+
+
+def gpu_paged_attention_v2(ctx: Context, q, k_cache, v_cache, block_tables, context_lens,
+                           params: PagedAttentionParams) -> np.ndarray:
+    """Host-array wrapper (gpu_paged_attention_v2, paged_attention.rs:328-382): rejects a
+    context longer than the table capacity and an empty context before any upload,
+    copies to the device, runs, and returns the [seqs, heads, head_dim] output."""
+    capacity = params.max_num_blocks_per_seq * params.block_size
+    lens = np.asarray(context_lens, dtype=np.uint32)
+    for length in lens:
+        if length > capacity:
+            raise EngineError(_capi.KANSO_E_OUT_OF_BOUNDS,
+                              f"paged attention: context_len {length} exceeds block table "
+                              f"capacity {capacity}")
+    if (lens == 0).any():
+        raise EngineError(_capi.KANSO_E_INVALID_SHAPE,
+                          "paged attention: context_len must be non-zero "
+                          "(empty context merges to NaN)")
+    validate_paged_attention_params(params)
+    dev = torch.device("cuda", ctx.device)
+
+    def up(a, dt):
+        return torch.from_numpy(np.ascontiguousarray(np.asarray(a, dtype=dt))).to(dev)
+
+    q_d = up(q, np.float32)
+    k_d = up(k_cache, np.float32)
+    v_d = up(v_cache, np.float32)
+    t_d = up(np.asarray(block_tables, dtype=np.uint32).view(np.int32), np.int32)
+    l_d = up(lens.view(np.int32), np.int32)
+    out = torch.empty(params.num_seqs * params.num_heads * params.head_dim, dtype=torch.float32,
+                      device=dev)
+    paged_attention_v2(ctx, params, q_d, k_d, v_d, t_d, l_d, out)
+    ctx.check_device_status()
+    return out.cpu().numpy()
+
+
+def ragged_paged_attention(ctx: Context, *, q: torch.Tensor, k_pool: torch.Tensor,
+                           v_pool: torch.Tensor, block_tables: torch.Tensor,
+                           cu_seqlens: torch.Tensor, context_lens: torch.Tensor,
+                           out: torch.Tensor, num_heads: int, num_kv_heads: int, head_dim: int,
+                           block_size: int, scale: float, kv_dtype: int = KANSO_KV_F32,
+                           k_scales: torch.Tensor | None = None,
+                           v_scales: torch.Tensor | None = None, num_blocks: int = 0,
+                           max_q_len: int = 0,
+                           stream: torch.cuda.Stream | None = None) -> None:
+    """Mixed prefill + decode attention over the paged pool (kanso_ragged_paged_attention)."""
+    num_seqs = cu_seqlens.numel() - 1
+    max_blocks = block_tables.numel() // max(num_seqs, 1)
+    total_q = q.numel() // (num_heads * head_dim)
+    p = RaggedAttentionParamsC(num_seqs, num_heads, num_kv_heads, head_dim, block_size, max_blocks,
+                               scale, total_q, kv_dtype, num_blocks, max_q_len)
+    _check(ctx._lib.kanso_ragged_paged_attention(
+        ctx.handle, C.byref(p), _ptr(q), _ptr(k_pool), _ptr(v_pool), _ptr(k_scales),
+        _ptr(v_scales), _ptr(block_tables), _ptr(cu_seqlens), _ptr(context_lens), _ptr(out),
+        _stream(stream)))
+
+
+# ---------------------------------------------------------------- packing
+
+
+@dataclass
+class PackedStep:
+    cu_seqlens: torch.Tensor
+    seq_of_query: torch.Tensor
+    positions: torch.Tensor
+    slot_mapping: torch.Tensor
+    tokens: torch.Tensor
+    block_tables: torch.Tensor
+    context_lens: torch.Tensor
+    max_blocks: int
+    total_q: int
+
+
+def plan_shapes(plan: np.ndarray, block_size: int) -> tuple[int, int]:
+    """(total_q, max_blocks) of a plan array with fields start_pos, q_len (host side,
+    the same arithmetic as PaddedDecodeTables::new, src/model.rs:84-88)."""
+    start = plan[:, 0].astype(np.int64)
+    qlen = plan[:, 1].astype(np.int64)
+    ctx = start + qlen
+    max_blocks = int(max(1, ((ctx + block_size - 1) // block_size).max(initial=1)))
+    return int(qlen.sum()), max_blocks
+
+
+def pack_step(ctx: Context, plan: np.ndarray, token_arena: torch.Tensor, table_arena: torch.Tensor,
+              block_size: int, stream: torch.cuda.Stream | None = None) -> PackedStep:
+    """Packs one step on the device. `plan` is an int array [S, 5] of
+    (start_pos, q_len, table_offset, table_len, token_offset) in plan order."""
+    plan = np.ascontiguousarray(np.asarray(plan, dtype=np.uint32))
+    S = plan.shape[0]
+    total_q, max_blocks = plan_shapes(plan, block_size)
+    dev = torch.device("cuda", ctx.device)
+    plan_d = torch.from_numpy(plan.view(np.int32)).to(dev)
+    out = PackedStep(
+        cu_seqlens=torch.empty(S + 1, dtype=torch.int32, device=dev),
+        seq_of_query=torch.empty(total_q, dtype=torch.int32, device=dev),
+        positions=torch.empty(total_q, dtype=torch.int32, device=dev),
+        slot_mapping=torch.empty(total_q, dtype=torch.int64, device=dev),
+        tokens=torch.empty(total_q, dtype=torch.int32, device=dev),
+        block_tables=torch.empty(S * max_blocks, dtype=torch.int32, device=dev),
+        context_lens=torch.empty(S, dtype=torch.int32, device=dev),
+        max_blocks=max_blocks, total_q=total_q)
+    c = PackedStepC(out.cu_seqlens.data_ptr(), out.seq_of_query.data_ptr(),
+                    out.positions.data_ptr(), out.slot_mapping.data_ptr(), out.tokens.data_ptr(),
+                    out.block_tables.data_ptr(), out.context_lens.data_ptr())
+    _check(ctx._lib.kanso_pack_step(ctx.handle, _ptr(plan_d), S, _ptr(token_arena),
+                                    _ptr(table_arena), block_size, max_blocks, total_q,
+                                    C.byref(c), _stream(stream)))
+    out._plan_keepalive = plan_d  # the kernel reads it asynchronously
+    return out
+
+
+# ---------------------------------------------------------------- KV pool
+
+
+def kv_append(ctx: Context, kv_dtype: int, k: torch.Tensor, v: torch.Tensor,
+              slot_mapping: torch.Tensor, num_blocks: int, block_size: int, num_kv_heads: int,
+              head_dim: int, k_pool: torch.Tensor, v_pool: torch.Tensor,
+              k_scales: torch.Tensor | None = None, v_scales: torch.Tensor | None = None,
+              stream: torch.cuda.Stream | None = None) -> None:
+    """Fused append (+ quantize) of [T, Hkv, D] K/V rows into pool row slot_mapping[t]."""
+    T = slot_mapping.numel()
+    _check(ctx._lib.kanso_kv_append(ctx.handle, kv_dtype, _ptr(k), _ptr(v), _ptr(slot_mapping), T,
+                                    num_blocks, block_size, num_kv_heads, head_dim, _ptr(k_pool),
+                                    _ptr(v_pool), _ptr(k_scales), _ptr(v_scales), _stream(stream)))
+
+
+def kv_reset_blocks(ctx: Context, kv_dtype: int, blocks: torch.Tensor, num_blocks: int,
+                    block_size: int, num_kv_heads: int, head_dim: int, k_pool: torch.Tensor,
+                    v_pool: torch.Tensor, k_scales: torch.Tensor | None = None,
+                    v_scales: torch.Tensor | None = None,
+                    stream: torch.cuda.Stream | None = None) -> None:
+    """allocate_zeroed's erase (src/kv_cache/mod.rs:25-35) for a list of blocks."""
+    _check(ctx._lib.kanso_kv_reset_blocks(ctx.handle, kv_dtype, _ptr(blocks), blocks.numel(),
+                                          num_blocks, block_size, num_kv_heads, head_dim,
+                                          _ptr(k_pool), _ptr(v_pool), _ptr(k_scales),
+                                          _ptr(v_scales), _stream(stream)))
+
+
+# ---------------------------------------------------------------- GEMV
+
+
+def gemv_q8_0(ctx: Context, w: torch.Tensor, x: torch.Tensor, y: torch.Tensor, out_features: int,
+              in_features: int, stream: torch.cuda.Stream | None = None) -> None:
+    """y[b, out] = W x[b] with W as GGUF block_q8_0 bytes ([out, in/32] x 34 B)."""
+    batch = x.numel() // in_features
+    _check(ctx._lib.kanso_gemv_q8_0(ctx.handle, _ptr(w), _ptr(x), _ptr(y), out_features,
+                                    in_features, batch, _stream(stream)))
+
+
+def gemv_q4_k(ctx: Context, w: torch.Tensor, x: torch.Tensor, y: torch.Tensor, out_features: int,
+              in_features: int, stream: torch.cuda.Stream | None = None) -> None:
+    """y[b, out] = W x[b] with W as GGUF block_q4_K bytes ([out, in/256] x 144 B)."""
+    batch = x.numel() // in_features
+    _check(ctx._lib.kanso_gemv_q4_k(ctx.handle, _ptr(w), _ptr(x), _ptr(y), out_features,
+                                    in_features, batch, _stream(stream)))

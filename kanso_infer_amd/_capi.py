@@ -1,0 +1,128 @@
+"""ctypes declaration of libkanso_hip.so (include/kanso_hip.h).
+
+torch is imported before the library is loaded: torch ships its own HIP runtime
+(libamdhip64.so.7), and loading it first makes the library bind to that same
+runtime, so torch's device buffers and streams are valid handles for it.
+"""
+from __future__ import annotations
+
+import ctypes as C
+import os
+from pathlib import Path
+
+import torch  # noqa: F401  (must precede the library load, see module docstring)
+
+LIB_PATH = Path(__file__).resolve().parent / "libkanso_hip.so"
+
+KANSO_OK = 0
+KANSO_E_INVALID_ARG = -1
+KANSO_E_INVALID_SHAPE = -2
+KANSO_E_OUT_OF_BOUNDS = -3
+KANSO_E_HIP = -4
+KANSO_E_DEVICE_CHECK = -5
+
+KANSO_DEV_EMPTY_CONTEXT = 1 << 0
+KANSO_DEV_CONTEXT_OVERFLOW = 1 << 1
+KANSO_DEV_QUERY_OVERFLOW = 1 << 2
+KANSO_DEV_TABLE_SHORT = 1 << 3
+KANSO_DEV_SLOT_OOB = 1 << 4
+KANSO_DEV_BLOCK_OOB = 1 << 5
+
+KANSO_KV_F32 = 0
+KANSO_KV_INT8 = 1
+KANSO_KV_Q8_0 = 2
+
+
+class PagedAttentionParamsC(C.Structure):
+    _fields_ = [
+        ("num_seqs", C.c_uint32),
+        ("num_heads", C.c_uint32),
+        ("num_kv_heads", C.c_uint32),
+        ("head_dim", C.c_uint32),
+        ("block_size", C.c_uint32),
+        ("max_num_blocks_per_seq", C.c_uint32),
+        ("scale", C.c_float),
+    ]
+
+
+class RaggedAttentionParamsC(C.Structure):
+    _fields_ = [
+        ("num_seqs", C.c_uint32),
+        ("num_heads", C.c_uint32),
+        ("num_kv_heads", C.c_uint32),
+        ("head_dim", C.c_uint32),
+        ("block_size", C.c_uint32),
+        ("max_num_blocks_per_seq", C.c_uint32),
+        ("scale", C.c_float),
+        ("total_q", C.c_uint32),
+        ("kv_dtype", C.c_uint32),
+        ("num_blocks", C.c_uint32),
+        ("max_q_len", C.c_uint32),
+    ]
+
+
+class SeqPlanC(C.Structure):
+    _fields_ = [
+        ("start_pos", C.c_uint32),
+        ("q_len", C.c_uint32),
+        ("table_offset", C.c_uint32),
+        ("table_len", C.c_uint32),
+        ("token_offset", C.c_uint32),
+    ]
+
+
+class PackedStepC(C.Structure):
+    _fields_ = [
+        ("cu_seqlens", C.c_void_p),
+        ("seq_of_query", C.c_void_p),
+        ("positions", C.c_void_p),
+        ("slot_mapping", C.c_void_p),
+        ("tokens", C.c_void_p),
+        ("block_tables", C.c_void_p),
+        ("context_lens", C.c_void_p),
+    ]
+
+
+# Every symbol the header declares, with its signature.
+_P = C.c_void_p
+_U = C.c_uint32
+_I = C.c_int
+SIGNATURES: dict[str, tuple] = {
+    "kanso_last_error": (C.c_char_p, []),
+    "kanso_create": (_I, [_I, C.POINTER(_P)]),
+    "kanso_destroy": (_I, [_P]),
+    "kanso_check_device_status": (_I, [_P, _P, C.POINTER(_U)]),
+    "kanso_paged_attention_num_partitions": (_U, [C.POINTER(PagedAttentionParamsC)]),
+    "kanso_validate_paged_attention_params": (_I, [C.POINTER(PagedAttentionParamsC)]),
+    "kanso_paged_attention_v2": (_I, [_P, C.POINTER(PagedAttentionParamsC), _P, _P, _P, _P, _P, _P, _P]),
+    "kanso_ragged_paged_attention": (
+        _I, [_P, C.POINTER(RaggedAttentionParamsC), _P, _P, _P, _P, _P, _P, _P, _P, _P, _P]),
+    "kanso_pack_step": (_I, [_P, _P, _U, _P, _P, _U, _U, _U, C.POINTER(PackedStepC), _P]),
+    "kanso_kv_append": (_I, [_P, _U, _P, _P, _P, _U, _U, _U, _U, _U, _P, _P, _P, _P, _P]),
+    "kanso_kv_reset_blocks": (_I, [_P, _U, _P, _U, _U, _U, _U, _U, _P, _P, _P, _P, _P]),
+    "kanso_gemv_q8_0": (_I, [_P, _P, _P, _P, _U, _U, _U, _P]),
+    "kanso_gemv_q4_k": (_I, [_P, _P, _P, _P, _U, _U, _U, _P]),
+    "kanso_set_profiling": (_I, [_P, _I]),
+    "kanso_get_kernel_time": (_I, [_P, C.c_char_p, C.POINTER(C.c_double), C.POINTER(C.c_uint64)]),
+}
+
+_lib: C.CDLL | None = None
+
+
+def load() -> C.CDLL:
+    """Loads libkanso_hip.so; raises if it has not been built (no fallback exists)."""
+    global _lib
+    if _lib is not None:
+        return _lib
+    path = Path(os.environ.get("KANSO_HIP_LIB", LIB_PATH))
+    if not path.exists():
+        raise RuntimeError(
+            f"{path} is missing: build it with `python -m kanso_infer_amd.build` "
+            "(there is no CPU fallback for the HIP path)")
+    lib = C.CDLL(str(path))
+    for name, (res, args) in SIGNATURES.items():
+        fn = getattr(lib, name)
+        fn.restype = res
+        fn.argtypes = args
+    _lib = lib
+    return lib

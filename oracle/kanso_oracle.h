@@ -1,0 +1,137 @@
+/*
+ * kanso_oracle.h — CPU restatement of kanso-infer's attention-path arithmetic.
+ *
+ * TEST INFRASTRUCTURE ONLY. This library is the checker the parity tests,
+ * __graft_entry__.smoke() and bench.py's cpu_baseline leg compare the HIP
+ * library against. No product code links, loads or calls it.
+ *
+ * The reference is Rust (kanso-infer; no toolchain for it exists in this
+ * environment), so each function restates the cited Rust source line by line:
+ * the same loop order, the same f32 operations, no fused multiply-add (the
+ * library is compiled with -ffp-contract=off, as Rust never contracts).
+ *
+ * Pinning (what checks each function besides the HIP comparison) is recorded in
+ * the tests under tests/test_oracle_*.py; the one unpinned item is the Q4_K
+ * quantizer's byte choice (candle's QTensor::quantize is not available), see
+ * oracle_quantize_row_q4_k.
+ */
+#ifndef KANSO_ORACLE_H
+#define KANSO_ORACLE_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#include "../include/kanso_hip.h"
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* ---- attention ---------------------------------------------------------- */
+
+/* cpu_paged_attention (src/metal/paged_attention.rs:84-178), F32 pool. */
+void oracle_paged_attention(const float* q, const float* k_cache, const float* v_cache,
+                            const uint32_t* block_tables, const uint32_t* context_lens,
+                            const kanso_paged_attention_params* p, float* out);
+
+/* Mixed-batch attention of forward_batch_rows (src/model.rs:1689-1714): per
+ * sequence, gather the context (dequantized for INT8 / Q8_0 pools exactly as
+ * gather_dequantized_blocks, quantized_storage.rs:284-383), then per query head
+ * and row: scores with the offset causal limit (model.rs:1510-1527), max, exp,
+ * sum, 1/sum, weighted V — the arithmetic of cpu_paged_attention. nthreads > 1
+ * runs sequences x heads on OpenMP threads (results do not depend on it).
+ * Returns 0, or -1 for an empty / inconsistent sequence (model.rs:1488-1493). */
+int oracle_ragged_attention(const float* q, const void* k_pool, const void* v_pool,
+                            const void* k_scales, const void* v_scales,
+                            const uint32_t* block_tables, const int32_t* cu_seqlens,
+                            const uint32_t* context_lens,
+                            const kanso_ragged_attention_params* p, float* out,
+                            int nthreads);
+
+/* ---- packing ------------------------------------------------------------ */
+
+/* Host packing loop of Engine::step (src/engine.rs:376-402) plus
+ * PaddedDecodeTables::new (src/model.rs:71-111). Outputs as kanso_packed_step but
+ * host arrays. *max_blocks_out receives the padded width. Returns 0, -1 if a
+ * position has no block (engine.rs:387-394). */
+int oracle_pack_step(const kanso_seq_plan* plan, uint32_t num_seqs,
+                     const uint32_t* token_arena, const uint32_t* table_arena,
+                     uint32_t block_size, int32_t* cu_seqlens, int32_t* seq_of_query,
+                     int32_t* positions, int64_t* slot_mapping, uint32_t* tokens,
+                     uint32_t* block_tables, uint32_t* context_lens,
+                     uint32_t* max_blocks_out);
+
+/* ---- KV append / quantization ------------------------------------------ */
+
+/* quantize_head_slice, INT8 arm (src/kv_cache/quantized_storage.rs:452-469). */
+float oracle_quantize_head_int8(const float* x, uint32_t n, int8_t* q);
+
+/* BlockQ8_0::from_f32_slice (src/quant/q8_0.rs:13-32) on 32 values; returns d (f32). */
+float oracle_quantize_q8_0_block(const float* x, int8_t* qs);
+
+/* IEEE binary16 conversions (round to nearest even), used for GGUF scales. */
+uint16_t oracle_f32_to_f16(float x);
+float oracle_f16_to_f32(uint16_t h);
+
+/* write_kv_slots for every pool kind (src/kv_cache/kind.rs:348-374). Returns 0,
+ * -1 when a slot is outside the pool (kind.rs:130-137; nothing is written then). */
+int oracle_kv_append(uint32_t kv_dtype, const float* k, const float* v,
+                     const int64_t* slot_mapping, uint32_t num_tokens, uint32_t num_blocks,
+                     uint32_t block_size, uint32_t num_kv_heads, uint32_t head_dim,
+                     void* k_pool, void* v_pool, void* k_scales, void* v_scales);
+
+/* ---- quantized GEMV ---------------------------------------------------- */
+
+/* scalar_gemv_q8_0 (src/quant/q8_0.rs:69-93) on GGUF blocks {f16 d; i8 qs[32]}
+ * (34 B) and on the reference's own blocks {f32 d; i8 qs[32]} (36 B). batch rows
+ * of x are independent GEMVs. */
+void oracle_gemv_q8_0(const void* w, const float* x, float* y, uint32_t rows,
+                      uint32_t cols, uint32_t batch, int nthreads);
+void oracle_gemv_q8_0_f32d(const void* w, const float* x, float* y, uint32_t rows,
+                           uint32_t cols, uint32_t batch);
+
+/* BlockQ4_K::dequantize (src/quant/q4_k.rs:30-55) on a GGUF block {f16 d; f16 dmin;
+ * u8 scales[12]; u8 qs[128]} (144 B) and on the reference block with f32 d/dmin
+ * (148 B). */
+void oracle_dequant_q4_k(const void* blk, float* out256);
+void oracle_dequant_q4_k_f32d(const void* blk, float* out256);
+void oracle_get_scale_min_k4(uint32_t j, const uint8_t* scales12, uint8_t* sc, uint8_t* m);
+
+/* scalar_gemv_q4_k (src/quant/q4_k.rs:162-186) on GGUF / reference blocks. */
+void oracle_gemv_q4_k(const void* w, const float* x, float* y, uint32_t rows,
+                      uint32_t cols, uint32_t batch, int nthreads);
+void oracle_gemv_q4_k_f32d(const void* w, const float* x, float* y, uint32_t rows,
+                           uint32_t cols, uint32_t batch);
+
+/* Row quantizers used to build synthetic weights (GGUF layouts). Q8_0 is the
+ * q8_0.rs:13-32 rule with d stored as f16. Q4_K is this build's own quantizer
+ * (per 32-element sub-block: min/max to 6-bit scale/min, nibble = round((x+m)/s)),
+ * because the reference takes Q4_K bytes from candle's QTensor::quantize, which is
+ * not available here: its bytes are "parity unpinned"; only dequantization and the
+ * GEMV over given bytes are pinned. */
+void oracle_quantize_row_q8_0(const float* x, uint32_t n, void* blocks);
+void oracle_quantize_row_q4_k(const float* x, uint32_t n, void* blocks);
+
+/* ---- decoder glue (config 5) -------------------------------------------- */
+
+/* Model::rmsnorm (src/model.rs:653-659): x / sqrt(mean(x^2) + eps) * w, rows of n. */
+void oracle_rmsnorm(const float* x, const float* w, float* y, uint32_t rows, uint32_t n,
+                    float eps);
+/* build_rope_table (src/model.rs:698-718): cos/sin [len][head_dim/2]. */
+void oracle_rope_table(uint32_t len, uint32_t head_dim, float theta, float* cos_t,
+                       float* sin_t);
+/* rope_apply (src/model.rs:720-737), in place on [rows][heads][head_dim] with the
+ * table rows of positions[rows]. */
+void oracle_rope_apply(float* x, uint32_t rows, uint32_t heads, uint32_t head_dim,
+                       const int32_t* positions, const float* cos_t, const float* sin_t);
+/* silu(gate) * up (src/model.rs:375-378; metal/ops.rs cpu_silu_gate_multiply). */
+void oracle_silu_mul(const float* gate, const float* up, float* y, uint32_t n);
+/* greedy_token (src/sampler.rs:7-17): first maximum wins. */
+uint32_t oracle_greedy(const float* logits, uint32_t n);
+/* fnv1a_64 (src/bench.rs:20-29): one XOR per u32 token widened to u64. */
+uint64_t oracle_fnv1a_64(const uint32_t* tokens, size_t n);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

@@ -1,0 +1,145 @@
+"""GPU parity of the ragged paged-attention kernels against the oracle (through the
+C ABI), covering the reference's own GPU test matrix (tests/test_paged_attention_v2.rs)
+and the ragged mixed batches of this path."""
+import numpy as np
+import pytest
+import torch
+
+import kanso_infer_amd as K
+import oracle
+from golden_cases import GOLDEN_PATH, REFERENCE_CASES
+from gpu_helpers import (assert_close, dev, fill_pool, host, run_ragged_gpu,
+                         run_ragged_oracle)
+from kanso_infer_amd import workloads
+
+pytestmark = pytest.mark.gpu
+
+
+def params_of(c):
+    return K.PagedAttentionParams(c["num_seqs"], c["num_heads"], c["num_kv_heads"],
+                                  c["head_dim"], c["block_size"], c["max_blocks"], c["scale"])
+
+
+def test_known_answer(ctx):
+    bs, hd = 2, 4
+    k = np.zeros(4 * bs * hd, np.float32)
+    v = np.zeros_like(k)
+    k[2 * bs * hd] = 1.0
+    v[2 * bs * hd] = 10.0
+    k[(2 * bs + 1) * hd + 2] = 1.0
+    v[(2 * bs + 1) * hd + 1] = 20.0
+    k[bs * hd] = 1.0
+    k[bs * hd + 2] = 1.0
+    v[bs * hd + 2] = 30.0
+    p = K.PagedAttentionParams(1, 1, 1, hd, bs, 2, 0.5)
+    out = K.gpu_paged_attention_v2(ctx, [1, 0, 1, 0], k, v, [2, 1], [3], p)
+    assert abs(out[0] - 2.7407) < 1e-3
+    assert abs(out[1] - 5.4814) < 1e-3
+    assert abs(out[2] - 13.5558) < 1e-3
+    assert abs(out[3]) < 1e-6
+
+
+@pytest.mark.parametrize("name", sorted(REFERENCE_CASES))
+def test_reference_matrix(ctx, name):
+    c = REFERENCE_CASES[name]()
+    out = K.gpu_paged_attention_v2(ctx, c["q"], c["k"], c["v"], c["tables"], c["lens"],
+                                   params_of(c))
+    golden = np.load(GOLDEN_PATH)[name]
+    assert_close(out, golden, what=name)
+    # the reference's own GPU-vs-CPU tolerance holds as well
+    assert np.abs(out - golden).max() <= 1e-4, name
+
+
+def test_flat_output_long_context(ctx):
+    # tests/test_paged_attention_v2.rs:558-633: ctx 2048, out stays [seqs, heads, hd]
+    hd, bs, ctx_len = 64, 16, 2048
+    blocks = ctx_len // bs
+    p = K.PagedAttentionParams(1, 4, 4, hd, bs, blocks, 1.0 / 8.0)
+    nb = blocks + 4
+    q = np.full(4 * hd, 0.1, np.float32)
+    k = np.full(nb * bs * 4 * hd, 0.05, np.float32)
+    v = np.full(nb * bs * 4 * hd, 0.02, np.float32)
+    out = K.gpu_paged_attention_v2(ctx, q, k, v, np.arange(blocks), [ctx_len], p)
+    assert out.shape == (4 * hd,)
+    assert np.isfinite(out).all() and (out > 0).all()
+    np.testing.assert_allclose(out, 0.02, rtol=1e-5)
+
+
+def test_rejects_unrepresentable(ctx):
+    p = K.PagedAttentionParams(1, 1, 1, 384, 16, 4, 1.0 / np.sqrt(384))
+    with pytest.raises(K.EngineError):
+        K.gpu_paged_attention_v2(ctx, np.full(384, 0.1), np.full(4 * 16 * 384, 0.1),
+                                 np.full(4 * 16 * 384, 0.1), [0, 1, 2, 3], [8], p)
+    p = K.PagedAttentionParams(1, 1, 1, 4, 2, 2, 0.5)
+    with pytest.raises(K.EngineError):  # empty context
+        K.gpu_paged_attention_v2(ctx, np.ones(4), np.zeros(16), np.zeros(16), [0, 1], [0], p)
+    with pytest.raises(K.EngineError):  # context beyond table capacity
+        K.gpu_paged_attention_v2(ctx, np.ones(4), np.zeros(16), np.zeros(16), [0, 1], [5], p)
+    p = K.PagedAttentionParams(1, 9, 1, 64, 16, 4, 0.125)
+    with pytest.raises(K.EngineError):  # GQA group above 8
+        K.validate_paged_attention_params(p)
+
+
+def test_device_flags_raise(ctx):
+    """A context length the table cannot address is flagged on the device and raised."""
+    hd, bs = 64, 16
+    q = torch.zeros(2 * 4 * hd, device="cuda:0")
+    pool = torch.zeros(8 * bs * 4 * hd, device="cuda:0")
+    tables = dev(np.zeros(2 * 2, np.uint32))
+    lens = dev(np.array([10, 40], np.uint32))  # 40 > capacity 32
+    out = torch.empty_like(q)
+    K.paged_attention_v2(ctx, K.PagedAttentionParams(2, 4, 4, hd, bs, 2, 0.125), q, pool, pool,
+                         tables, lens, out)
+    with pytest.raises(K.EngineError):
+        ctx.check_device_status()
+    ctx.check_device_status()  # cleared
+
+
+@pytest.mark.parametrize("seed", range(4))
+@pytest.mark.parametrize("kv_dtype", [oracle.KV_F32, oracle.KV_INT8, oracle.KV_Q8_0])
+def test_ragged_small(ctx, seed, kv_dtype):
+    shapes = [dict(), dict(num_heads=16, num_kv_heads=4), dict(num_heads=8, num_kv_heads=1,
+                                                              head_dim=128),
+              dict(num_heads=4, num_kv_heads=4, head_dim=32, block_size=8)]
+    b = workloads.small_mixed(seed, **shapes[seed])
+    kp, vp, ks, vs = fill_pool(b, kv_dtype, seed)
+    q = np.random.default_rng(seed + 50).standard_normal(
+        b.total_q * b.num_heads * b.head_dim).astype(np.float32)
+    got = run_ragged_gpu(ctx, b, q, kp, vp, ks, vs, kv_dtype)
+    want = run_ragged_oracle(b, q, kp, vp, ks, vs, kv_dtype)
+    assert_close(got, want, what=f"{b.label} kv {kv_dtype}")
+
+
+@pytest.mark.parametrize("variant", ["config1", "config2_small_pool", "config3_int8",
+                                     "config3_q8_0"])
+def test_baseline_shapes(ctx, variant):
+    """The BASELINE configs at their real shapes (pools sized to what the tables use)."""
+    if variant == "config1":
+        b, kv = workloads.config1_decode(), oracle.KV_F32
+    elif variant == "config2_small_pool":
+        b, kv = workloads.config2_mixed(num_blocks=10000), oracle.KV_F32
+    else:
+        b = workloads.config3_quant_decode()
+        kv = oracle.KV_INT8 if variant.endswith("int8") else oracle.KV_Q8_0
+    kp, vp, ks, vs = fill_pool(b, kv, 7)
+    q = np.random.default_rng(8).standard_normal(
+        b.total_q * b.num_heads * b.head_dim).astype(np.float32)
+    got = run_ragged_gpu(ctx, b, q, kp, vp, ks, vs, kv)
+    want = run_ragged_oracle(b, q, kp, vp, ks, vs, kv)
+    assert_close(got, want, what=variant)
+
+
+def test_ragged_equals_decode_entry(ctx):
+    """The reference-compatible decode entry and the ragged entry agree on decode rows."""
+    b = workloads.config1_decode(seed_offset=3)
+    kp, vp, _, _ = fill_pool(b, oracle.KV_F32, 9)
+    q = np.random.default_rng(10).standard_normal(
+        b.total_q * b.num_heads * b.head_dim).astype(np.float32)
+    ragged = run_ragged_gpu(ctx, b, q, kp, vp)
+    p = K.PagedAttentionParams(b.num_seqs, b.num_heads, b.num_kv_heads, b.head_dim,
+                               b.block_size, b.max_blocks, b.scale)
+    out = torch.empty(q.size, device="cuda:0")
+    K.paged_attention_v2(ctx, p, dev(q), dev(kp), dev(vp), dev(b.block_tables.ravel()),
+                         dev(b.context_lens.astype(np.uint32)), out)
+    ctx.check_device_status()
+    np.testing.assert_array_equal(host(out), ragged)
