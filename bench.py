@@ -1,0 +1,380 @@
+"""Benchmark of the ragged paged-attention path on one MI355X.
+
+    python bench.py [--gpus 1] [--steps 200] [--warmup 20] [--quick]
+
+Headline: one mixed Sarathi step under a 512-token budget,
+SmolLM2-360M attention shape (15 query / 5 KV heads, head_dim 64), 48 decode rows
+(context U[128,4096]) + 4 prefill chunks (U[32,256] rows truncated by the budget,
+prior context U[0,2048]), block size 16, block tables a random scatter over a
+64k-block F32 pool (2.7 GB). A step is one ragged attention call over one such
+batch (work-list build, split-K stage 1, reduce). Eight independent batches with
+their own random tables are rotated, so consecutive steps read different blocks
+of the 2.7 GB pool and the 256 MB Infinity Cache cannot hold a step's 276 MB.
+
+value = query rows / second over the timed steps (inputs resident in HBM).
+roofline: stage-1 attention kernel, algorithmic bytes (K/V once per sequence +
+tables + Q + O + lengths) / its average duration from HIP events recorded on the
+launch stream inside the timed region, against 8 TB/s.
+cpu_baseline: the oracle (C++ restatement of the reference CPU path) on the same
+batch, single-threaded on this host, timed over a bounded number of calls.
+Extra fields: the 64-sequence variant, configs 1 and 3, GEMV and a copy kernel.
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+from pathlib import Path
+
+import numpy as np
+
+ROOT = Path(__file__).resolve().parent
+sys.path.insert(0, str(ROOT))
+
+HBM_PEAK = 8.0e12
+METRIC = "ragged paged-attn tokens/s + % HBM peak; batched decode tok/s at 1 MI355X"
+
+
+def log(msg: str) -> None:
+    print(msg, file=sys.stderr, flush=True)
+
+
+class AttnBench:
+    """Device-resident inputs for a rotation of attention batches over one pool."""
+
+    def __init__(self, ctx, batches, kv_dtype, seed):
+        import torch
+        import kanso_infer_amd as K
+        self.K, self.torch, self.ctx = K, torch, ctx
+        self.batches = batches
+        self.kv_dtype = kv_dtype
+        b0 = batches[0]
+        self.num_blocks = b0.num_blocks
+        rows = b0.num_blocks * b0.block_size * b0.num_kv_heads
+        g = torch.Generator(device="cuda:0")
+        g.manual_seed(seed)
+        dev = torch.device("cuda:0")
+        if kv_dtype == K.KANSO_KV_F32:
+            self.k = torch.randn(rows * b0.head_dim, generator=g, device=dev)
+            self.v = torch.randn(rows * b0.head_dim, generator=g, device=dev)
+            self.ks = self.vs = None
+        else:
+            # quantize N(0,1) rows into the pool with the fused append kernel itself
+            self.k = torch.zeros(rows * b0.head_dim, dtype=torch.int8, device=dev)
+            self.v = torch.zeros_like(self.k)
+            if kv_dtype == K.KANSO_KV_INT8:
+                self.ks = torch.ones(rows, dtype=torch.float32, device=dev)
+            else:
+                self.ks = torch.zeros(rows * b0.head_dim // 32, dtype=torch.float16, device=dev)
+            self.vs = torch.ones_like(self.ks)
+            chunk = 1 << 16
+            tok = b0.num_blocks * b0.block_size
+            width = b0.num_kv_heads * b0.head_dim
+            for t0 in range(0, tok, chunk):
+                n = min(chunk, tok - t0)
+                kk = torch.randn(n * width, generator=g, device=dev)
+                vv = torch.randn(n * width, generator=g, device=dev)
+                slots = torch.arange(t0, t0 + n, dtype=torch.int64, device=dev)
+                K.kv_append(ctx, kv_dtype, kk, vv, slots, b0.num_blocks, b0.block_size,
+                            b0.num_kv_heads, b0.head_dim, self.k, self.v, self.ks, self.vs)
+            ctx.check_device_status()
+        self.dev_batches = []
+        for i, b in enumerate(batches):
+            q = torch.randn(b.total_q * b.num_heads * b.head_dim, generator=g, device=dev)
+            self.dev_batches.append(dict(
+                q=q, out=torch.empty_like(q),
+                tables=torch.from_numpy(b.block_tables.ravel().view(np.int32)).to(dev),
+                cu=torch.from_numpy(b.cu_seqlens).to(dev),
+                lens=torch.from_numpy(b.context_lens.astype(np.int32)).to(dev)))
+        torch.cuda.synchronize()
+
+    def call(self, i):
+        b, d = self.batches[i % len(self.batches)], self.dev_batches[i % len(self.batches)]
+        self.K.ragged_paged_attention(
+            self.ctx, q=d["q"], k_pool=self.k, v_pool=self.v, k_scales=self.ks, v_scales=self.vs,
+            block_tables=d["tables"], cu_seqlens=d["cu"], context_lens=d["lens"], out=d["out"],
+            num_heads=b.num_heads, num_kv_heads=b.num_kv_heads, head_dim=b.head_dim,
+            block_size=b.block_size, scale=b.scale, kv_dtype=self.kv_dtype,
+            num_blocks=self.num_blocks, max_q_len=int(b.q_lens.max()))
+
+    def run(self, steps, warmup):
+        torch = self.torch
+        for i in range(warmup):
+            self.call(i)
+        self.ctx.check_device_status()
+        torch.cuda.synchronize()
+        self.ctx.set_profiling(True)
+        start, stop = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        torch.cuda.synchronize()
+        start.record()
+        for i in range(steps):
+            self.call(i)
+        stop.record()
+        torch.cuda.synchronize()
+        total_ms = start.elapsed_time(stop)
+        k_ms, k_n = self.ctx.kernel_time("attention")
+        r_ms, r_n = self.ctx.kernel_time("reduce")
+        c_ms, c_n = self.ctx.kernel_time("attention_chunk")
+        d_ms, d_n = self.ctx.kernel_time("attention_decode")
+        self.ctx.set_profiling(False)
+        self.ctx.check_device_status()
+        rows = np.mean([b.total_q for b in self.batches])
+        abytes = np.mean([b.algorithmic_bytes(self.kv_dtype) for b in self.batches])
+        ms = total_ms / steps
+        st1 = k_ms / max(k_n, 1)
+        return dict(ms_per_step=ms, tokens_per_s=rows / (ms * 1e-3),
+                    stage1_ms=st1, reduce_ms=r_ms / max(r_n, 1),
+                    chunk_kernel_ms=c_ms / max(c_n, 1), decode_kernel_ms=d_ms / max(d_n, 1),
+                    algorithmic_bytes=int(abytes),
+                    stage1_gbps=abytes / (st1 * 1e-3) / 1e9,
+                    call_gbps=abytes / (ms * 1e-3) / 1e9)
+
+
+def copy_bandwidth(torch, nbytes=2 << 30, iters=10):
+    a = torch.empty(nbytes // 4, dtype=torch.float32, device="cuda:0").normal_()
+    b = torch.empty_like(a)
+    for _ in range(2):
+        b.copy_(a)
+    torch.cuda.synchronize()
+    s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    s.record()
+    for _ in range(iters):
+        b.copy_(a)
+    e.record()
+    torch.cuda.synchronize()
+    ms = s.elapsed_time(e) / iters
+    return 2 * nbytes / (ms * 1e-3) / 1e9
+
+
+def gemv_bench(ctx, torch, K, oracle_mod, quick):
+    """Q8_0 / Q4_K GEMV at the SmolLM2 projection shapes; each timing rotates over
+    weight copies totalling > 1 GB."""
+    dev = torch.device("cuda:0")
+    shapes = [("q", 960, 960), ("kv", 320, 960), ("gate_up", 2560, 960), ("down", 960, 2560)]
+    out = []
+    for kind in ("q8_0", "q4_k"):
+        for name, rows, cols in shapes:
+            cols_eff = cols if kind == "q8_0" or cols % 256 == 0 else 1024
+            label = name if cols_eff == cols else name + "_padded"
+            rng = np.random.default_rng(rows + cols)
+            wf = (rng.standard_normal((rows, cols_eff)) * 0.02).astype(np.float32)
+            if cols_eff != cols:
+                wf[:, cols:] = 0.0
+            w = (oracle_mod.quantize_row_q8_0(wf) if kind == "q8_0"
+                 else oracle_mod.quantize_row_q4_k(wf))
+            wbytes = w.size
+            copies = max(32, int((1.1e9) // wbytes) + 1)
+            arena = torch.from_numpy(w).to(dev).repeat(copies)
+            fn = K.gemv_q8_0 if kind == "q8_0" else K.gemv_q4_k
+            for batch in ([1, 8, 32] if quick else [1, 4, 8, 16, 32]):
+                x = torch.randn(batch * cols_eff, device=dev)
+                y = torch.empty(batch * rows, device=dev)
+                for i in range(4):
+                    fn(ctx, arena[i * wbytes:(i + 1) * wbytes], x, y, rows, cols_eff)
+                torch.cuda.synchronize()
+                ctx.set_profiling(True)
+                n = min(copies, 200)
+                for i in range(n):
+                    fn(ctx, arena[i * wbytes:(i + 1) * wbytes], x, y, rows, cols_eff)
+                g_ms, g_n = ctx.kernel_time("gemv")
+                ctx.set_profiling(False)
+                us = g_ms / max(g_n, 1) * 1e3
+                abytes = wbytes + batch * (cols_eff + rows) * 4
+                out.append(dict(kind=kind, shape=label, out=rows, inp=cols_eff, batch=batch,
+                                us=round(us, 2), gbps=round(abytes / (us * 1e-6) / 1e9, 1),
+                                frac=round(abytes / (us * 1e-6) / HBM_PEAK, 4)))
+            del arena
+            torch.cuda.empty_cache()
+    return out
+
+
+def cpu_baseline(batch, seconds=12.0):
+    """Oracle (C++ restatement of the reference CPU path) on the headline batch,
+    single-threaded, over a pool compacted to exactly the blocks the batch reads."""
+    sys.path.insert(0, str(ROOT / "oracle"))
+    import oracle as oracle_mod
+    ids = np.unique(batch.block_tables)
+    lut = np.zeros(int(ids.max()) + 1, np.uint32)
+    lut[ids] = np.arange(ids.size, dtype=np.uint32)
+    tables = lut[batch.block_tables]
+    rng = np.random.default_rng(1)
+    n = ids.size * batch.block_size * batch.num_kv_heads * batch.head_dim
+    k = rng.standard_normal(n, dtype=np.float32)
+    v = rng.standard_normal(n, dtype=np.float32)
+    q = rng.standard_normal(batch.total_q * batch.num_heads * batch.head_dim, dtype=np.float32)
+    kw = dict(num_heads=batch.num_heads, num_kv_heads=batch.num_kv_heads,
+              head_dim=batch.head_dim, block_size=batch.block_size, scale=batch.scale,
+              num_blocks=int(ids.size))
+    calls, t0 = 0, time.perf_counter()
+    while True:
+        oracle_mod.ragged_attention(q, k, v, tables, batch.cu_seqlens, batch.context_lens,
+                                    nthreads=1, **kw)
+        calls += 1
+        el = time.perf_counter() - t0
+        if el >= seconds or calls >= 100:
+            break
+    per_call = el / calls
+    return dict(value=round(batch.total_q / per_call, 1), unit="tokens/s", cores=1, kind="port",
+                sample=f"{calls} oracle calls on the headline batch ({batch.total_q} query rows, "
+                       f"{batch.num_seqs} sequences), single thread, {el:.1f} s",
+                ms_per_call=round(per_call * 1e3, 2))
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=200)
+    ap.add_argument("--warmup", type=int, default=20)
+    ap.add_argument("--quick", action="store_true", help="headline only: skip extras")
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
+    ap.add_argument("--decode-only", action="store_true",
+                    help="also time the headline batches' decode rows alone")
+    args = ap.parse_args()
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
+        print("bench.py measures one GPU: this path has no multi-GPU component in this build "
+              "(see DESIGN.md for how it would shard); run with --gpus 1", file=sys.stderr)
+        sys.exit(2)
+
+    import torch
+    import kanso_infer_amd as K
+    from kanso_infer_amd import workloads
+
+    ctx = K.Context(0)
+    log("building headline batches (config 2, 64k-block pool)")
+    nb = 65536
+    head = [workloads.config2_mixed(num_blocks=nb, seed_offset=i) for i in range(8)]
+    hb = AttnBench(ctx, head, K.KANSO_KV_F32, seed=2)
+    res = hb.run(args.steps, args.warmup)
+    log(f"config2: {res}")
+
+    extras = {}
+    if args.decode_only:
+        dec = [workloads.config2_mixed(num_chunks=0, num_blocks=nb, seed_offset=i) for i in range(8)]
+        hd = AttnBench.__new__(AttnBench)
+        hd.__dict__.update(hb.__dict__)
+        hd.batches = dec
+        hd.dev_batches = []
+        for b in dec:
+            q = torch.randn(b.total_q * b.num_heads * b.head_dim, device="cuda:0")
+            hd.dev_batches.append(dict(
+                q=q, out=torch.empty_like(q),
+                tables=torch.from_numpy(b.block_tables.ravel().view(np.int32)).cuda(),
+                cu=torch.from_numpy(b.cu_seqlens).cuda(),
+                lens=torch.from_numpy(b.context_lens.astype(np.int32)).cuda()))
+        rd = hd.run(args.steps, args.warmup)
+        extras["config2_decode_rows_only"] = {k: (round(v, 4) if isinstance(v, float) else v)
+                                              for k, v in rd.items()}
+        log(f"config2 decode rows only: {rd}")
+    if not args.quick:
+        s64 = [workloads.config2_mixed(num_decodes=60, num_blocks=nb, seed_offset=100 + i)
+               for i in range(8)]
+        # same pool, different batches: reuse the pool of the headline
+        hb64 = AttnBench.__new__(AttnBench)
+        hb64.__dict__.update(hb.__dict__)
+        hb64.batches = s64
+        hb64.dev_batches = []
+        g = torch.Generator(device="cuda:0")
+        g.manual_seed(64)
+        for b in s64:
+            q = torch.randn(b.total_q * b.num_heads * b.head_dim, generator=g, device="cuda:0")
+            hb64.dev_batches.append(dict(
+                q=q, out=torch.empty_like(q),
+                tables=torch.from_numpy(b.block_tables.ravel().view(np.int32)).cuda(),
+                cu=torch.from_numpy(b.cu_seqlens).cuda(),
+                lens=torch.from_numpy(b.context_lens.astype(np.int32)).cuda()))
+        r64 = hb64.run(args.steps, args.warmup)
+        extras["config2_64seq"] = {k: (round(v, 4) if isinstance(v, float) else v)
+                                   for k, v in r64.items()}
+        extras["config2_64seq"]["hbm_frac_stage1"] = round(r64["stage1_gbps"] * 1e9 / HBM_PEAK, 4)
+        log(f"config2 64-seq: {r64}")
+        del hb64
+        del hb.k, hb.v
+        torch.cuda.empty_cache()
+
+        c1 = [workloads.config1_decode(seed_offset=i) for i in range(8)]
+        # config 1 pools hold only the needed blocks; rotate 8 batches over a shared
+        # large pool instead so timings are not cache-resident
+        for b in c1:
+            b.num_blocks = nb
+        rng = np.random.default_rng(5)
+        for b in c1:
+            need = (b.context_lens + 15) // 16
+            ids = rng.choice(nb, size=int(need.sum()), replace=False).astype(np.uint32)
+            off = 0
+            for s, n_ in enumerate(need):
+                b.block_tables[s, :n_] = ids[off:off + n_]
+                b.block_tables[s, n_:] = ids[off + n_ - 1]
+                off += n_
+        b1 = AttnBench(ctx, c1, K.KANSO_KV_F32, seed=1)
+        r1 = b1.run(args.steps, args.warmup)
+        extras["config1_decode"] = {k: (round(v, 4) if isinstance(v, float) else v)
+                                    for k, v in r1.items()}
+        log(f"config1: {r1}")
+        del b1
+        torch.cuda.empty_cache()
+
+        for kv, name in ((K.KANSO_KV_INT8, "config3_int8"), (K.KANSO_KV_Q8_0, "config3_q8_0")):
+            c3 = [workloads.config3_quant_decode(num_blocks=131072, seed_offset=i) for i in range(8)]
+            b3 = AttnBench(ctx, c3, kv, seed=3)
+            r3 = b3.run(args.steps, args.warmup)
+            r3["hbm_frac_stage1"] = r3["stage1_gbps"] * 1e9 / HBM_PEAK
+            extras[name] = {k: (round(v, 4) if isinstance(v, float) else v) for k, v in r3.items()}
+            log(f"{name}: {r3}")
+            del b3
+            torch.cuda.empty_cache()
+
+        sys.path.insert(0, str(ROOT / "oracle"))
+        import oracle as oracle_mod
+        extras["gemv"] = gemv_bench(ctx, torch, K, oracle_mod, quick=False)
+        extras["copy_kernel_gbps"] = round(copy_bandwidth(torch), 1)
+
+    cpu = None if args.no_cpu else cpu_baseline(head[0])
+    if cpu:
+        log(f"cpu baseline: {cpu}")
+
+    achieved = res["stage1_gbps"] * 1e9
+    line = {
+        "metric": METRIC,
+        "value": round(res["tokens_per_s"], 1),
+        "unit": "tokens/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(res["ms_per_step"], 5),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f32",
+        "data": "synthetic",
+        "config": {
+            "workload": "config2: mixed Sarathi step, 48 decode + 4 prefill-chunk sequences, "
+                        "512-token budget, SmolLM2-360M attention (H15/Hkv5/D64), bs16, "
+                        "F32 KV, random scatter over a 64k-block pool",
+            "query_rows": int(np.mean([b.total_q for b in head])),
+            "sequences": int(np.mean([b.num_seqs for b in head])),
+            "rotation": "8 batches",
+        },
+        "roofline": {
+            "bound": "hbm",
+            "achieved": round(achieved / 1e9, 1),
+            "peak": HBM_PEAK / 1e9,
+            "unit": "GB/s",
+            "frac": round(achieved / HBM_PEAK, 4),
+            "traffic": None,
+            "kernel": "attn_stage1 (split-K ragged paged attention)",
+            "algorithmic_bytes_per_launch": res["algorithmic_bytes"],
+            "avg_launch_ms": round(res["stage1_ms"], 5),
+        },
+        "hbm_frac_whole_call": round(res["call_gbps"] * 1e9 / HBM_PEAK, 4),
+        "reduce_ms": round(res["reduce_ms"], 5),
+        "cpu_baseline": cpu,
+    }
+    line.update(extras)
+    ctx.close()
+    print(json.dumps(line), flush=True)
+
+
+if __name__ == "__main__":
+    main()

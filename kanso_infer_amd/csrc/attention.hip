@@ -3,30 +3,39 @@
 //
 // Reference semantics: cpu_paged_attention (src/metal/paged_attention.rs:84-178) for
 // a decode row, and the offset causal mask of forward_batch_rows (src/model.rs:
-// 1510-1527) for a prefill-chunk row. The Metal kernel's structure
-// (paged_attention_v2.metal:32-205: partitions, (m, d) stats, merge) is kept as a
-// contract; the mapping onto the hardware is this file's own:
+// 1510-1527) for the rows of a prefill chunk: row i of a sequence with q_len rows
+// and context c attends keys 0..=c-q_len+i. The Metal kernel's contract
+// (paged_attention_v2.metal:32-205: partitions, per-partition (m, d) statistics,
+// a merge) is kept; the mapping onto CDNA4 is this file's own:
 //
-//  * One work item = (query row, context partition, KV head). A 256-thread
-//    workgroup (4 wave64s) owns one item at a time and walks a device-built work
-//    list in a grid-stride loop, so no host knowledge of context lengths is needed.
-//  * Inside a wave, LPT = head_dim/4 lanes share one token: each lane loads one
-//    float4 (16 B) of K and of V, so a load instruction moves 64 x 16 B = 1 KB of
-//    fully used, coalesced bytes (four 256 B rows at head_dim 64). A lane loads
-//    NL = 8 tokens per tile, K and V together, before any arithmetic, so 16
-//    independent 16 B loads per lane are in flight.
-//  * Every query head of the GQA group is served from the same K/V registers, so
-//    K/V bytes are read once per (token, KV head), not once per query head.
-//  * Scores live in the log2 domain (scale * log2(e) folded into one multiply) and
-//    the online softmax runs per tile: one max / sum butterfly per tile and head
-//    instead of one per token.
-//  * The four waves of a workgroup split the partition into interleaved tiles and
-//    merge their (m, l, acc) through LDS before one partial is written.
+//  * Work unit = one wave64. A device-built work list holds (rows, partition)
+//    items; every wave of a persistent grid walks it with a grid-wide stride, one
+//    item x KV head at a time. No LDS, no barriers: waves never wait on each other.
+//  * Decode rows (one query row): LPT = head_dim/4 lanes share a token, each lane
+//    loads one 16 B float4 of K and of V, so a load instruction moves 1 KB of fully
+//    used bytes (four 256 B rows at head_dim 64). Tiles of NL tokens per lane are
+//    double-buffered: the next tile's loads are in flight while the current tile
+//    is scored. Every query head of the GQA group is served from the same K/V
+//    registers, so K/V bytes are read once per (token, KV head).
+//  * Prefill-chunk rows: 16 rows x G heads per wave on the matrix cores
+//    (v_mfma_f32_16x16x4f32, full fp32 products). S^T = K Q^T is computed with K as
+//    the A operand (loaded straight from the pool in MFMA layout) and Q^T held in
+//    registers; the C layout of S^T is then exactly the B-operand layout of
+//    O^T = V^T P^T, so probabilities never leave registers and each query's
+//    softmax statistics live in that query's own lanes.
+//  * Block tables: the <= 64 table entries a partition touches are loaded once
+//    into one register per lane; token -> physical block is a lane shuffle.
+//  * Scores live in the log2 domain (scale * log2(e) folded into one multiply);
+//    the online softmax rescales once per tile, not once per token.
+//  * A row whose context fits one partition is normalised and written directly;
+//    only rows split over several partitions go through the reduce kernel.
+//  * Chunk items come first in the work list, so compute-bound MFMA waves and
+//    bandwidth-bound decode waves share the machine instead of running in turn.
 //  * Quantized pools (INT8 per token-head scale, Q8_0 per-32 f16 scale) are
 //    dequantized in registers with the reference's own product (q as f32) * scale.
-//
-// Decode is a bandwidth-bound GEMV-like walk over K/V; it uses no MFMA.
 #include <cmath>
+#include <cstdlib>
+#include <string>
 
 #include "common.hpp"
 
@@ -36,6 +45,8 @@ namespace {
 constexpr int kThreads = 256;
 constexpr int kWaves = kThreads / kWave;
 constexpr float kLog2e = 1.4426950408889634f;
+constexpr int kChunkRows = 16;  // query rows per MFMA chunk item
+constexpr int kKindChunk = 1;
 
 struct AttnArgs {
     const float* q;
@@ -46,14 +57,14 @@ struct AttnArgs {
     const uint32_t* tables;
     const int32_t* cu;
     const uint32_t* ctx_lens;
-    float* part_out;   // [T][H][max_parts][D]
+    float* part_out;     // [T][H][max_parts][D]
     float2* part_stats;  // [T][H][max_parts] (m in log2 units, l)
-    float* out;        // [T][H][D]
-    const int4* items; // {row, part, limit, seq}
-    const uint32_t* n_items;
+    float* out;          // [T][H][D]
     uint32_t* status;
     uint32_t num_seqs, num_heads, num_kv_heads, group, block_size, bs_shift;
     uint32_t max_blocks, num_blocks, part_size, max_parts, total_q, capacity;
+    uint32_t use_mfma;
+    uint32_t pool_bytes, scale_bytes;  // per pool tensor, for buffer resources (< 4 GiB)
     float scale_log2;
 };
 
@@ -65,46 +76,90 @@ __device__ __forceinline__ uint32_t row_limit(int32_t ctx, int32_t q_len, int32_
     return min(static_cast<uint32_t>(lim), cap);
 }
 
-// Single workgroup: validates every sequence, counts its (row, partition) items,
-// scans the counts and writes the work list. Sequences are split into contiguous
-// ranges, one per thread.
-__global__ __launch_bounds__(kThreads) void build_worklist(AttnArgs a, int4* items, uint32_t* n_items) {
-    __shared__ uint32_t scan[kThreads];
-    const uint32_t tid = threadIdx.x;
-    const uint32_t per = (a.num_seqs + kThreads - 1) / kThreads;
-    const uint32_t s0 = min(tid * per, a.num_seqs), s1 = min(s0 + per, a.num_seqs);
+__device__ __forceinline__ uint32_t ceil_div(uint32_t a, uint32_t b) { return (a + b - 1) / b; }
+
+// ---------------------------------------------------------------- work mapping
+//
+// No work list is materialised. Each workgroup copies cu_seqlens / context_lens
+// into LDS and scans the per-sequence item counts of its kernel (chunk items for
+// the MFMA kernel, decode items for the other); a wave maps its work index to a
+// sequence by binary search over that prefix and to (rows, partition) by walking
+// the sequence's rows or 16-row tiles.
+
+constexpr uint32_t kMaxSeqs = 2048;  // sequences per call (LDS-resident tables)
+
+struct SeqTable {
+    int32_t cu[kMaxSeqs + 1];
+    int32_t ctx[kMaxSeqs];
+    uint32_t pre[kMaxSeqs + 1];  // exclusive prefix of this kernel's item counts
+    uint32_t part_sums[kThreads];
+};
+
+__device__ __forceinline__ bool is_chunk_seq(const AttnArgs& a, int32_t ql) { return a.use_mfma && ql > 1; }
+
+// Items of one sequence for this kernel: per 16-row tile (chunk) or per row (decode),
+// ceil(limit / P) partitions of the tile's last row / the row.
+__device__ uint32_t seq_items(const AttnArgs& a, int32_t ql, int32_t ctx, bool chunk) {
     const uint32_t P = a.part_size;
-    uint32_t count = 0, flags = 0;
+    uint32_t n = 0;
+    if (chunk) {
+        for (int32_t i0 = 0; i0 < ql; i0 += kChunkRows)
+            n += ceil_div(row_limit(ctx, ql, min(i0 + kChunkRows, ql) - 1, a.capacity), P);
+    } else {
+        for (int32_t i = 0; i < ql; ++i) n += ceil_div(row_limit(ctx, ql, i, a.capacity), P);
+    }
+    return n;
+}
+
+// Fills the workgroup's SeqTable (all threads participate). Workgroup 0 of the
+// decode kernel also raises the input-validation flags.
+template <bool CHUNK>
+__device__ void load_seq_table(const AttnArgs& a, SeqTable& st) {
+    const uint32_t tid = threadIdx.x, S = a.num_seqs;
+    for (uint32_t s = tid; s <= S; s += kThreads) {
+        st.cu[s] = a.cu[s];
+        if (s < S) st.ctx[s] = static_cast<int32_t>(a.ctx_lens[s]);
+    }
+    __syncthreads();
+    const uint32_t seg = ceil_div(S, kThreads);
+    const uint32_t s0 = min(tid * seg, S), s1 = min(s0 + seg, S);
+    uint32_t run = 0, flags = 0;
     for (uint32_t s = s0; s < s1; ++s) {
-        const int32_t ql = a.cu[s + 1] - a.cu[s];
-        const int32_t ctx = static_cast<int32_t>(a.ctx_lens[s]);
+        const int32_t ql = st.cu[s + 1] - st.cu[s], ctx = st.ctx[s];
         if (ctx == 0) flags |= KANSO_DEV_EMPTY_CONTEXT;
         if (static_cast<uint32_t>(ctx) > a.capacity) flags |= KANSO_DEV_CONTEXT_OVERFLOW;
         if (ql > ctx) flags |= KANSO_DEV_QUERY_OVERFLOW;
-        for (int32_t i = 0; i < ql; ++i) count += (row_limit(ctx, ql, i, a.capacity) + P - 1) / P;
+        const bool chunk = is_chunk_seq(a, ql);
+        run += chunk == CHUNK ? seq_items(a, ql, ctx, chunk) : 0u;
+        st.pre[s + 1] = run;  // inclusive within this thread's segment
     }
-    if (flags) raise_status(a.status, flags);
-    scan[tid] = count;
+    if (!CHUNK && flags && blockIdx.x == 0) raise_status(a.status, flags);
+    st.part_sums[tid] = run;
     __syncthreads();
     for (uint32_t off = 1; off < kThreads; off <<= 1) {
-        const uint32_t v = tid >= off ? scan[tid - off] : 0;
+        const uint32_t v = tid >= off ? st.part_sums[tid - off] : 0;
         __syncthreads();
-        scan[tid] += v;
+        st.part_sums[tid] += v;
         __syncthreads();
     }
-    uint32_t pos = scan[tid] - count;
-    for (uint32_t s = s0; s < s1; ++s) {
-        const int32_t ql = a.cu[s + 1] - a.cu[s];
-        const int32_t ctx = static_cast<int32_t>(a.ctx_lens[s]);
-        for (int32_t i = 0; i < ql; ++i) {
-            const uint32_t lim = row_limit(ctx, ql, i, a.capacity);
-            const uint32_t np = (lim + P - 1) / P;
-            for (uint32_t p = 0; p < np; ++p)
-                items[pos++] = make_int4(a.cu[s] + i, static_cast<int>(p), static_cast<int>(lim), static_cast<int>(s));
-        }
-    }
-    if (tid == kThreads - 1) *n_items = scan[tid];
+    const uint32_t base = st.part_sums[tid] - run;
+    for (uint32_t s = s0; s < s1; ++s) st.pre[s + 1] += base;
+    if (tid == 0) st.pre[0] = 0;
+    __syncthreads();
 }
+
+// Sequence owning item `idx`: the s with pre[s] <= idx < pre[s + 1].
+__device__ __forceinline__ uint32_t find_seq(const SeqTable& st, uint32_t S, uint32_t idx) {
+    uint32_t lo = 0, hi = S;
+    while (hi - lo > 1) {
+        const uint32_t mid = (lo + hi) >> 1;
+        if (st.pre[mid] <= idx) lo = mid;
+        else hi = mid;
+    }
+    return lo;
+}
+
+// ---------------------------------------------------------------- KV loads
 
 template <int KVT>
 struct KvLoader;
@@ -112,16 +167,16 @@ struct KvLoader;
 // F32 pool: one float4 per lane.
 template <>
 struct KvLoader<KANSO_KV_F32> {
-    __device__ __forceinline__ static float4 load(const void* pool, const void*, size_t row, int D, int dl) {
-        return *reinterpret_cast<const float4*>(static_cast<const float*>(pool) + row * D + dl * 4);
+    __device__ __forceinline__ static float4 load(const void* pool, const void*, size_t row, int D, int d0) {
+        return *reinterpret_cast<const float4*>(static_cast<const float*>(pool) + row * D + d0);
     }
 };
 
 // INT8 pool with one f32 scale per (token, KV head): (q as f32) * scale.
 template <>
 struct KvLoader<KANSO_KV_INT8> {
-    __device__ __forceinline__ static float4 load(const void* pool, const void* scales, size_t row, int D, int dl) {
-        const char4 q = *reinterpret_cast<const char4*>(static_cast<const int8_t*>(pool) + row * D + dl * 4);
+    __device__ __forceinline__ static float4 load(const void* pool, const void* scales, size_t row, int D, int d0) {
+        const char4 q = *reinterpret_cast<const char4*>(static_cast<const int8_t*>(pool) + row * D + d0);
         const float sc = static_cast<const float*>(scales)[row];
         return make_float4(static_cast<float>(q.x) * sc, static_cast<float>(q.y) * sc,
                            static_cast<float>(q.z) * sc, static_cast<float>(q.w) * sc);
@@ -131,10 +186,63 @@ struct KvLoader<KANSO_KV_INT8> {
 // Q8_0 pool with one f16 scale per 32 elements: d * (q as f32).
 template <>
 struct KvLoader<KANSO_KV_Q8_0> {
-    __device__ __forceinline__ static float4 load(const void* pool, const void* scales, size_t row, int D, int dl) {
-        const char4 q = *reinterpret_cast<const char4*>(static_cast<const int8_t*>(pool) + row * D + dl * 4);
-        const __half h = static_cast<const __half*>(scales)[row * (D / 32) + (dl * 4) / 32];
-        const float d = __half2float(h);
+    __device__ __forceinline__ static float4 load(const void* pool, const void* scales, size_t row, int D, int d0) {
+        const char4 q = *reinterpret_cast<const char4*>(static_cast<const int8_t*>(pool) + row * D + d0);
+        const float d = __half2float(static_cast<const __half*>(scales)[row * (D / 32) + d0 / 32]);
+        return make_float4(d * static_cast<float>(q.x), d * static_cast<float>(q.y),
+                           d * static_cast<float>(q.z), d * static_cast<float>(q.w));
+    }
+};
+
+// Buffer-resource loads: the pool base and size live in scalar registers, a lane
+// only carries a 32-bit byte offset (one VGPR shared by K and V), and an offset
+// past the pool returns zeros without touching memory, which is how masked tokens
+// are skipped. Used when every pool tensor is below 4 GiB.
+typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
+constexpr uint32_t kOffNone = 0xffffffffu;  // out of range: the load returns 0
+
+struct PoolRsrc {
+    __amdgpu_buffer_rsrc_t k, v, ks, vs;
+};
+
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* p, uint32_t bytes) {
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(p), static_cast<short>(0),
+                                             static_cast<int>(bytes), 0x00020000);
+}
+
+template <int KVT>
+struct KvBuf;
+
+template <>
+struct KvBuf<KANSO_KV_F32> {
+    __device__ __forceinline__ static float4 load(__amdgpu_buffer_rsrc_t pool, __amdgpu_buffer_rsrc_t, uint32_t row,
+                                                  bool ok, int D, int d0) {
+        const uint32_t off = ok ? (row * D + d0) * 4u : kOffNone;
+        return __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(pool, off, 0, 0));
+    }
+};
+
+template <>
+struct KvBuf<KANSO_KV_INT8> {
+    __device__ __forceinline__ static float4 load(__amdgpu_buffer_rsrc_t pool, __amdgpu_buffer_rsrc_t scales,
+                                                  uint32_t row, bool ok, int D, int d0) {
+        const uint32_t w = __builtin_amdgcn_raw_buffer_load_b32(pool, ok ? row * D + d0 : kOffNone, 0, 0);
+        const float sc = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(scales, ok ? row * 4u : kOffNone, 0, 0));
+        const char4 q = __builtin_bit_cast(char4, w);
+        return make_float4(static_cast<float>(q.x) * sc, static_cast<float>(q.y) * sc,
+                           static_cast<float>(q.z) * sc, static_cast<float>(q.w) * sc);
+    }
+};
+
+template <>
+struct KvBuf<KANSO_KV_Q8_0> {
+    __device__ __forceinline__ static float4 load(__amdgpu_buffer_rsrc_t pool, __amdgpu_buffer_rsrc_t scales,
+                                                  uint32_t row, bool ok, int D, int d0) {
+        const uint32_t w = __builtin_amdgcn_raw_buffer_load_b32(pool, ok ? row * D + d0 : kOffNone, 0, 0);
+        const uint16_t hb = __builtin_amdgcn_raw_buffer_load_b16(
+            scales, ok ? (row * (D / 32) + d0 / 32) * 2u : kOffNone, 0, 0);
+        const float d = __half2float(__ushort_as_half(hb));
+        const char4 q = __builtin_bit_cast(char4, w);
         return make_float4(d * static_cast<float>(q.x), d * static_cast<float>(q.y),
                            d * static_cast<float>(q.z), d * static_cast<float>(q.w));
     }
@@ -144,189 +252,536 @@ __device__ __forceinline__ float dot4(float4 a, float4 b) {
     return a.x * b.x + a.y * b.y + a.z * b.z + a.w * b.w;
 }
 
-template <int D, int GMAX, int KVT>
-__global__ __launch_bounds__(kThreads) void attn_stage1(AttnArgs a) {
-    constexpr int LPT = D / 4;          // lanes per token
-    constexpr int TPI = kWave / LPT;    // tokens per load instruction
-    constexpr int NL = 8;               // tokens per lane per tile
-    constexpr int TT = TPI * NL;        // tokens per wave tile
-    __shared__ float sm_acc[kWaves][GMAX][D];
-    __shared__ float sm_m[kWaves][GMAX];
-    __shared__ float sm_l[kWaves][GMAX];
-
-    const int lane = threadIdx.x & (kWave - 1);
-    const int wv = threadIdx.x / kWave;
-    const int ts = lane / LPT;
-    const int dl = lane % LPT;
-    const uint32_t G = a.group;
-    const uint32_t n_work = *a.n_items * a.num_kv_heads;
-
-    for (uint32_t w = blockIdx.x; w < n_work; w += gridDim.x) {
-        const int4 it = a.items[w / a.num_kv_heads];
-        const uint32_t kvh = w % a.num_kv_heads;
-        const uint32_t row = static_cast<uint32_t>(it.x), part = static_cast<uint32_t>(it.y);
-        const uint32_t limit = static_cast<uint32_t>(it.z), seq = static_cast<uint32_t>(it.w);
-        const uint32_t t_begin = part * a.part_size;
-        const uint32_t t_end = min(t_begin + a.part_size, limit);
-
-        float4 qv[GMAX], acc[GMAX];
-        float m[GMAX], l[GMAX];
-#pragma unroll
-        for (int g = 0; g < GMAX; ++g) {
-            qv[g] = make_float4(0.f, 0.f, 0.f, 0.f);
-            acc[g] = make_float4(0.f, 0.f, 0.f, 0.f);
-            m[g] = -INFINITY;
-            l[g] = 0.f;
-            if (g < static_cast<int>(G))
-                qv[g] = *reinterpret_cast<const float4*>(
-                    a.q + (static_cast<size_t>(row) * a.num_heads + kvh * G + g) * D + dl * 4);
-        }
-        const uint32_t* table = a.tables + static_cast<size_t>(seq) * a.max_blocks;
-
-        for (uint32_t tile0 = t_begin + wv * TT; tile0 < t_end; tile0 += kWaves * TT) {
-            float4 kx[NL], vx[NL];
-            bool ok[NL];
-#pragma unroll
-            for (int i = 0; i < NL; ++i) {
-                const uint32_t t = tile0 + i * TPI + ts;
-                ok[i] = t < t_end;
-                kx[i] = make_float4(0.f, 0.f, 0.f, 0.f);
-                vx[i] = kx[i];
-                if (ok[i]) {
-                    const uint32_t blk = a.bs_shift < 32 ? (t >> a.bs_shift) : t / a.block_size;
-                    const uint32_t off = t - blk * a.block_size;
-                    uint32_t phys = table[blk];
-                    if (phys >= a.num_blocks) {
-                        raise_status(a.status, KANSO_DEV_BLOCK_OOB);
-                        phys = 0;
-                    }
-                    const size_t r = (static_cast<size_t>(phys) * a.block_size + off) * a.num_kv_heads + kvh;
-                    kx[i] = KvLoader<KVT>::load(a.k_pool, a.k_scales, r, D, dl);
-                    vx[i] = KvLoader<KVT>::load(a.v_pool, a.v_scales, r, D, dl);
-                }
-            }
-#pragma unroll
-            for (int g = 0; g < GMAX; ++g) {
-                if (g >= static_cast<int>(G)) break;
-                float sc[NL];
-                float mt = -INFINITY;
-#pragma unroll
-                for (int i = 0; i < NL; ++i) {
-                    float d = dot4(qv[g], kx[i]);
-#pragma unroll
-                    for (int o = 1; o < LPT; o <<= 1) d += wave_xor(d, o);
-                    sc[i] = ok[i] ? d * a.scale_log2 : -INFINITY;
-                    mt = fmaxf(mt, sc[i]);
-                }
-#pragma unroll
-                for (int o = LPT; o < kWave; o <<= 1) mt = fmaxf(mt, wave_xor(mt, o));
-                const float mn = fmaxf(m[g], mt);
-                const float alpha = exp2f(m[g] - mn);
-                float ps = 0.f;
-                float4 pv = make_float4(0.f, 0.f, 0.f, 0.f);
-#pragma unroll
-                for (int i = 0; i < NL; ++i) {
-                    const float p = exp2f(sc[i] - mn);
-                    ps += p;
-                    pv.x += p * vx[i].x;
-                    pv.y += p * vx[i].y;
-                    pv.z += p * vx[i].z;
-                    pv.w += p * vx[i].w;
-                }
-#pragma unroll
-                for (int o = LPT; o < kWave; o <<= 1) ps += wave_xor(ps, o);
-                l[g] = l[g] * alpha + ps;
-                acc[g].x = acc[g].x * alpha + pv.x;
-                acc[g].y = acc[g].y * alpha + pv.y;
-                acc[g].z = acc[g].z * alpha + pv.z;
-                acc[g].w = acc[g].w * alpha + pv.w;
-                m[g] = mn;
-            }
-        }
-
-        // Sum the token groups of the wave; lanes of group 0 then hold the wave's acc.
-#pragma unroll
-        for (int g = 0; g < GMAX; ++g) {
-            if (g >= static_cast<int>(G)) break;
-#pragma unroll
-            for (int o = LPT; o < kWave; o <<= 1) {
-                acc[g].x += wave_xor(acc[g].x, o);
-                acc[g].y += wave_xor(acc[g].y, o);
-                acc[g].z += wave_xor(acc[g].z, o);
-                acc[g].w += wave_xor(acc[g].w, o);
-            }
-            if (ts == 0) *reinterpret_cast<float4*>(&sm_acc[wv][g][dl * 4]) = acc[g];
-            if (lane == 0) {
-                sm_m[wv][g] = m[g];
-                sm_l[wv][g] = l[g];
-            }
-        }
-        __syncthreads();
-        for (uint32_t e = threadIdx.x; e < G * D; e += kThreads) {
-            const uint32_t g = e / D, d = e % D;
-            float M = -INFINITY;
-#pragma unroll
-            for (int x = 0; x < kWaves; ++x) M = fmaxf(M, sm_m[x][g]);
-            float o = 0.f, L = 0.f;
-#pragma unroll
-            for (int x = 0; x < kWaves; ++x) {
-                const float f = exp2f(sm_m[x][g] - M);  // 0 for a wave with no tile
-                o += sm_acc[x][g][d] * f;
-                L += sm_l[x][g] * f;
-            }
-            const size_t slot = (static_cast<size_t>(row) * a.num_heads + kvh * G + g) * a.max_parts + part;
-            a.part_out[slot * D + d] = o;
-            if (d == 0) a.part_stats[slot] = make_float2(M, L);
-        }
-        __syncthreads();
-    }
-}
-
-// One wave per (row, query head): merge the row's partitions,
-// out = sum_p acc_p 2^(m_p - M) / sum_p l_p 2^(m_p - M)
-// (paged_attention_v2.metal:154-205), 1/denominator = 0 for an empty row.
-template <int D>
-__global__ __launch_bounds__(kThreads) void attn_reduce(AttnArgs a) {
-    constexpr int PER = (D + kWave - 1) / kWave;
-    const int lane = threadIdx.x & (kWave - 1);
-    const uint32_t gw = blockIdx.x * kWaves + threadIdx.x / kWave;
-    if (gw >= a.total_q * a.num_heads) return;
-    const uint32_t row = gw / a.num_heads, h = gw % a.num_heads;
-    // Sequence of this row: last s with cu[s] <= row.
-    uint32_t lo = 0, hi = a.num_seqs;
-    while (hi - lo > 1) {
-        const uint32_t mid = (lo + hi) / 2;
-        if (static_cast<uint32_t>(a.cu[mid]) <= row) lo = mid;
-        else hi = mid;
-    }
-    const int32_t ql = a.cu[lo + 1] - a.cu[lo];
-    const uint32_t lim = row_limit(static_cast<int32_t>(a.ctx_lens[lo]), ql,
-                                   static_cast<int32_t>(row) - a.cu[lo], a.capacity);
-    const uint32_t np = (lim + a.part_size - 1) / a.part_size;
-    const size_t base = (static_cast<size_t>(row) * a.num_heads + h) * a.max_parts;
+// Merge of `np` partials of one (row, head) for head-dim elements [d0, d0 + 4*n4):
+// out = sum_p acc_p 2^(m_p - M) / sum_p l_p 2^(m_p - M) (paged_attention_v2.metal:
+// 154-205), 1/denominator = 0 for an empty row.
+template <int D, int N4>
+__device__ __forceinline__ void merge_partials(const AttnArgs& a, size_t head, uint32_t np, int d0) {
+    const size_t base = head * a.max_parts;
     float M = -INFINITY;
     for (uint32_t p = 0; p < np; ++p) M = fmaxf(M, a.part_stats[base + p].x);
-    float o[PER];
+    float4 o[N4];
 #pragma unroll
-    for (int k = 0; k < PER; ++k) o[k] = 0.f;
+    for (int k = 0; k < N4; ++k) o[k] = make_float4(0.f, 0.f, 0.f, 0.f);
     float L = 0.f;
     for (uint32_t p = 0; p < np; ++p) {
         const float2 st = a.part_stats[base + p];
-        const float f = exp2f(st.x - M);
+        const float f = fast_exp2(st.x - M);
         L += st.y * f;
-        const float* src = a.part_out + (base + p) * D;
+        const float4* src = reinterpret_cast<const float4*>(a.part_out + (base + p) * D + d0);
 #pragma unroll
-        for (int k = 0; k < PER; ++k) {
-            const int d = lane + k * kWave;
-            if (d < D) o[k] += src[d] * f;
+        for (int k = 0; k < N4; ++k) {
+            const float4 v = src[k];
+            o[k].x += v.x * f;
+            o[k].y += v.y * f;
+            o[k].z += v.z * f;
+            o[k].w += v.w * f;
         }
     }
     const float inv = L > 0.f ? 1.0f / L : 0.f;
-    float* dst = a.out + (static_cast<size_t>(row) * a.num_heads + h) * D;
 #pragma unroll
-    for (int k = 0; k < PER; ++k) {
-        const int d = lane + k * kWave;
-        if (d < D) dst[d] = o[k] * inv;
+    for (int k = 0; k < N4; ++k)
+        *reinterpret_cast<float4*>(a.out + head * D + d0 + 4 * k) =
+            make_float4(o[k].x * inv, o[k].y * inv, o[k].z * inv, o[k].w * inv);
+}
+
+__device__ __forceinline__ float comp(const float4& v, int i) {
+    return i == 0 ? v.x : i == 1 ? v.y : i == 2 ? v.z : v.w;
+}
+
+// Partition geometry of one (row set, partition): keys [t_begin, t_end), the block
+// ids they touch loaded one per lane (lane j holds table[blk0 + j]).
+struct PartView {
+    uint32_t t_begin, t_end, blk0;
+    int tab;
+};
+
+__device__ __forceinline__ uint32_t block_of(const AttnArgs& a, uint32_t t) {
+    return a.bs_shift < 32 ? (t >> a.bs_shift) : t / a.block_size;
+}
+
+__device__ __forceinline__ PartView load_part(const AttnArgs& a, uint32_t seq, uint32_t t_begin,
+                                              uint32_t t_end, int lane) {
+    PartView pv;
+    pv.t_begin = t_begin;
+    pv.t_end = t_end;
+    pv.blk0 = block_of(a, t_begin);
+    const uint32_t nblk = block_of(a, t_end - 1) - pv.blk0 + 1;  // <= 64 by choice of P
+    uint32_t phys = 0;
+    if (static_cast<uint32_t>(lane) < nblk) {
+        phys = a.tables[static_cast<size_t>(seq) * a.max_blocks + pv.blk0 + lane];
+        if (phys >= a.num_blocks) {
+            raise_status(a.status, KANSO_DEV_BLOCK_OOB);
+            phys = 0;
+        }
+    }
+    pv.tab = static_cast<int>(phys);
+    return pv;
+}
+
+// Pool row (block * bs + offset) * Hkv + kv_head of token t (t inside the view).
+__device__ __forceinline__ size_t pool_row(const AttnArgs& a, const PartView& pv, uint32_t t, uint32_t kvh) {
+    const uint32_t blk = block_of(a, t);
+    const uint32_t phys = static_cast<uint32_t>(__shfl(pv.tab, static_cast<int>(blk - pv.blk0), kWave));
+    return (static_cast<size_t>(phys) * a.block_size + (t - blk * a.block_size)) * a.num_kv_heads + kvh;
+}
+
+// ---------------------------------------------------------------- decode rows
+
+template <int D, int KVT, int NL>
+struct DecodeTile {
+    float4 k[NL], v[NL];
+};
+
+template <int D, int KVT, int NL, bool BUF>
+__device__ __forceinline__ void decode_load(const AttnArgs& a, const PoolRsrc& rs, const PartView& pv,
+                                            uint32_t tile0, uint32_t kvh, int ts, int dl,
+                                            DecodeTile<D, KVT, NL>& tl) {
+    constexpr int TPI = kWave / (D / 4);
+#pragma unroll
+    for (int i = 0; i < NL; ++i) {
+        const uint32_t t = tile0 + i * TPI + ts;
+        const bool ok = t < pv.t_end;
+        if constexpr (BUF) {
+            const uint32_t r = static_cast<uint32_t>(pool_row(a, pv, ok ? t : tile0, kvh));
+            tl.k[i] = KvBuf<KVT>::load(rs.k, rs.ks, r, ok, D, dl * 4);
+            tl.v[i] = KvBuf<KVT>::load(rs.v, rs.vs, r, ok, D, dl * 4);
+        } else {
+            const size_t r = pool_row(a, pv, ok ? t : tile0, kvh);  // masked: re-read a valid row
+            tl.k[i] = KvLoader<KVT>::load(a.k_pool, a.k_scales, r, D, dl * 4);
+            tl.v[i] = KvLoader<KVT>::load(a.v_pool, a.v_scales, r, D, dl * 4);
+        }
+    }
+}
+
+template <int D, int GMAX, int KVT, int NL>
+__device__ __forceinline__ void decode_compute(const AttnArgs& a, const PartView& pv, uint32_t tile0,
+                                               int ts, const float4 (&qv)[GMAX], float4 (&acc)[GMAX],
+                                               float (&m)[GMAX], float (&l)[GMAX],
+                                               const DecodeTile<D, KVT, NL>& tl) {
+    constexpr int LPT = D / 4;
+    constexpr int TPI = kWave / LPT;
+    const uint32_t G = a.group;
+#pragma unroll
+    for (int g = 0; g < GMAX; ++g) {
+        if (g >= static_cast<int>(G)) break;
+        float sc[NL];
+        float mt = -INFINITY;
+#pragma unroll
+        for (int i = 0; i < NL; ++i) {
+            const float d = group_sum<LPT>(dot4(qv[g], tl.k[i]));
+            const bool ok = tile0 + i * TPI + ts < pv.t_end;
+            sc[i] = ok ? d * a.scale_log2 : -INFINITY;
+            mt = fmaxf(mt, sc[i]);
+        }
+#pragma unroll
+        for (int o = LPT; o < kWave; o <<= 1) mt = fmaxf(mt, wave_xor(mt, o));
+        const float mn = fmaxf(m[g], mt);  // finite: every tile holds a live token
+        const float alpha = fast_exp2(m[g] - mn);
+        float ps = 0.f;
+        float4 pv4 = make_float4(0.f, 0.f, 0.f, 0.f);
+#pragma unroll
+        for (int i = 0; i < NL; ++i) {
+            const float p = fast_exp2(sc[i] - mn);
+            ps += p;
+            pv4.x += p * tl.v[i].x;
+            pv4.y += p * tl.v[i].y;
+            pv4.z += p * tl.v[i].z;
+            pv4.w += p * tl.v[i].w;
+        }
+#pragma unroll
+        for (int o = LPT; o < kWave; o <<= 1) ps += wave_xor(ps, o);
+        l[g] = l[g] * alpha + ps;
+        acc[g].x = acc[g].x * alpha + pv4.x;
+        acc[g].y = acc[g].y * alpha + pv4.y;
+        acc[g].z = acc[g].z * alpha + pv4.z;
+        acc[g].w = acc[g].w * alpha + pv4.w;
+        m[g] = mn;
+    }
+}
+
+template <int D, int GMAX, int KVT, int NL, bool DB, bool BUF>
+__device__ void decode_item(const AttnArgs& a, const PoolRsrc& rs, uint32_t row, uint32_t part, uint32_t seq,
+                            uint32_t kvh, int lane) {
+    constexpr int LPT = D / 4;
+    constexpr int TT = (kWave / LPT) * NL;
+    const int ts = lane / LPT, dl = lane % LPT;
+    const uint32_t G = a.group;
+    const int32_t ql = a.cu[seq + 1] - a.cu[seq];
+    const uint32_t limit = row_limit(static_cast<int32_t>(a.ctx_lens[seq]), ql,
+                                     static_cast<int32_t>(row) - a.cu[seq], a.capacity);
+    const uint32_t t_begin = part * a.part_size;
+    const uint32_t t_end = min(t_begin + a.part_size, limit);
+    const PartView pv = load_part(a, seq, t_begin, t_end, lane);
+
+    float4 qv[GMAX], acc[GMAX];
+    float m[GMAX], l[GMAX];
+#pragma unroll
+    for (int g = 0; g < GMAX; ++g) {
+        qv[g] = make_float4(0.f, 0.f, 0.f, 0.f);
+        acc[g] = make_float4(0.f, 0.f, 0.f, 0.f);
+        m[g] = -INFINITY;
+        l[g] = 0.f;
+        if (g < static_cast<int>(G))
+            qv[g] = *reinterpret_cast<const float4*>(
+                a.q + (static_cast<size_t>(row) * a.num_heads + kvh * G + g) * D + dl * 4);
+    }
+
+    if constexpr (DB) {
+        // Double-buffered: the next tile's loads are in flight during this tile's math.
+        DecodeTile<D, KVT, NL> ta, tb;
+        decode_load<D, KVT, NL, BUF>(a, rs, pv, t_begin, kvh, ts, dl, ta);
+        for (uint32_t t0 = t_begin; t0 < t_end; t0 += 2 * TT) {
+            const bool has_b = t0 + TT < t_end;
+            if (has_b) decode_load<D, KVT, NL, BUF>(a, rs, pv, t0 + TT, kvh, ts, dl, tb);
+            decode_compute<D, GMAX, KVT, NL>(a, pv, t0, ts, qv, acc, m, l, ta);
+            if (t0 + 2 * TT < t_end) decode_load<D, KVT, NL, BUF>(a, rs, pv, t0 + 2 * TT, kvh, ts, dl, ta);
+            if (has_b) decode_compute<D, GMAX, KVT, NL>(a, pv, t0 + TT, ts, qv, acc, m, l, tb);
+        }
+    } else {
+        // Single-buffered: fewer registers, more resident waves carry the loads.
+        for (uint32_t t0 = t_begin; t0 < t_end; t0 += TT) {
+            DecodeTile<D, KVT, NL> tl;
+            decode_load<D, KVT, NL, BUF>(a, rs, pv, t0, kvh, ts, dl, tl);
+            decode_compute<D, GMAX, KVT, NL>(a, pv, t0, ts, qv, acc, m, l, tl);
+        }
+    }
+
+    const bool single = t_begin == 0 && t_end == limit;  // whole context in this partition
+#pragma unroll
+    for (int g = 0; g < GMAX; ++g) {
+        if (g >= static_cast<int>(G)) break;
+#pragma unroll
+        for (int o = LPT; o < kWave; o <<= 1) {
+            acc[g].x += wave_xor(acc[g].x, o);
+            acc[g].y += wave_xor(acc[g].y, o);
+            acc[g].z += wave_xor(acc[g].z, o);
+            acc[g].w += wave_xor(acc[g].w, o);
+        }
+        const size_t head = static_cast<size_t>(row) * a.num_heads + kvh * G + g;
+        if (single) {
+            const float inv = l[g] > 0.f ? 1.0f / l[g] : 0.f;
+            if (ts == 0)
+                *reinterpret_cast<float4*>(a.out + head * D + dl * 4) =
+                    make_float4(acc[g].x * inv, acc[g].y * inv, acc[g].z * inv, acc[g].w * inv);
+            continue;
+        }
+        const size_t slot = head * a.max_parts + part;
+        if (ts == 0) *reinterpret_cast<float4*>(a.part_out + slot * D + dl * 4) = acc[g];
+        if (lane == 0) a.part_stats[slot] = make_float2(m[g], l[g]);
+    }
+}
+
+// ---------------------------------------------------------------- chunk rows (MFMA)
+
+typedef float floatx4 __attribute__((ext_vector_type(4)));
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+
+// Split of f32 values into bf16 hi + lo (x - hi is exact in f32): a product is
+// then ah*bh + ah*bl + al*bh on the bf16 matrix cores with f32 accumulation, about
+// 2^-16 relative error per product against the exact f32 product.
+struct Bf16Split {
+    bf16x8 hi, lo;
+};
+
+__device__ __forceinline__ Bf16Split split8(const float (&x)[8]) {
+    Bf16Split r;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+        const __bf16 h = static_cast<__bf16>(x[j]);
+        r.hi[j] = h;
+        r.lo[j] = static_cast<__bf16>(x[j] - static_cast<float>(h));
+    }
+    return r;
+}
+
+__device__ __forceinline__ floatx4 mfma3(const Bf16Split& a, const Bf16Split& b, floatx4 c) {
+    c = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a.hi, b.hi, c, 0, 0, 0);
+    c = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a.hi, b.lo, c, 0, 0, 0);
+    c = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a.lo, b.hi, c, 0, 0, 0);
+    return c;
+}
+
+// One 32-key tile of a chunk item, raw f32 after dequantization. With k = lane/16
+// and m = lane%16:
+//   k[b][s][h]: K[key t0 + 16b + m][d = 32s + 8k + 4h .. +3]   (A operand of S^T)
+//   v[4b + r]:  V[key t0 + 16b + 4k + r][d = 4m .. 4m+3]       (A operand of O^T)
+template <int KVT>
+struct ChunkTile {
+    float4 k[2][2][2];
+    float4 v[8];
+};
+
+template <int KVT>
+__device__ __forceinline__ void chunk_load(const AttnArgs& a, const PartView& pv, uint32_t t0,
+                                           uint32_t kvh, int lane, ChunkTile<KVT>& tl) {
+    constexpr int D = 64;
+    const int kq = lane >> 4, m = lane & 15;
+#pragma unroll
+    for (int b = 0; b < 2; ++b) {
+        uint32_t tk = t0 + 16 * b + m;
+        if (tk >= pv.t_end) tk = t0;
+        const size_t rk = pool_row(a, pv, tk, kvh);
+#pragma unroll
+        for (int sd = 0; sd < 2; ++sd)
+#pragma unroll
+            for (int h = 0; h < 2; ++h)
+                tl.k[b][sd][h] = KvLoader<KVT>::load(a.k_pool, a.k_scales, rk, D, 32 * sd + 8 * kq + 4 * h);
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            uint32_t tv = t0 + 16 * b + 4 * kq + r;
+            if (tv >= pv.t_end) tv = t0;
+            tl.v[4 * b + r] = KvLoader<KVT>::load(a.v_pool, a.v_scales, pool_row(a, pv, tv, kvh), D, 4 * m);
+        }
+    }
+}
+
+template <int GMAX, int KVT>
+__device__ __forceinline__ void chunk_compute(const AttnArgs& a, const PartView& pv, uint32_t t0, int lane,
+                                              uint32_t lim, const Bf16Split (&qs)[GMAX][2],
+                                              floatx4 (&o)[GMAX][4], float (&m)[GMAX], float (&l)[GMAX],
+                                              const ChunkTile<KVT>& tl) {
+    const uint32_t G = a.group;
+    // bf16 operands of this tile, shared by every query head of the group.
+    Bf16Split ks[2][2], vs[4];
+#pragma unroll
+    for (int b = 0; b < 2; ++b)
+#pragma unroll
+        for (int sd = 0; sd < 2; ++sd) {
+            const float x[8] = {tl.k[b][sd][0].x, tl.k[b][sd][0].y, tl.k[b][sd][0].z, tl.k[b][sd][0].w,
+                                tl.k[b][sd][1].x, tl.k[b][sd][1].y, tl.k[b][sd][1].z, tl.k[b][sd][1].w};
+            ks[b][sd] = split8(x);
+        }
+#pragma unroll
+    for (int nb = 0; nb < 4; ++nb) {
+        float x[8];
+#pragma unroll
+        for (int j = 0; j < 8; ++j) x[j] = comp(tl.v[j], nb);
+        vs[nb] = split8(x);
+    }
+    const uint32_t kbase = t0 + 4 * (lane >> 4);  // key of s[b][r] is kbase + 16b + r
+#pragma unroll
+    for (int g = 0; g < GMAX; ++g) {
+        if (g >= static_cast<int>(G)) break;
+        float sc[8];
+        float mt = -INFINITY;
+#pragma unroll
+        for (int b = 0; b < 2; ++b) {
+            floatx4 st = {0.f, 0.f, 0.f, 0.f};
+            st = mfma3(ks[b][0], qs[g][0], st);
+            st = mfma3(ks[b][1], qs[g][1], st);
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                const uint32_t key = kbase + 16 * b + r;
+                sc[4 * b + r] = (key < lim && key < pv.t_end) ? st[r] * a.scale_log2 : -INFINITY;
+                mt = fmaxf(mt, sc[4 * b + r]);
+            }
+        }
+        mt = fmaxf(mt, wave_xor(mt, 16));
+        mt = fmaxf(mt, wave_xor(mt, 32));
+        const float mn = fmaxf(m[g], mt);
+        const bool live = mn != -INFINITY;
+        const float alpha = live ? fast_exp2(m[g] - mn) : 1.0f;
+        float p[8];
+        float ps = 0.f;
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+            p[j] = live ? fast_exp2(sc[j] - mn) : 0.f;
+            ps += p[j];
+        }
+        ps += wave_xor(ps, 16);
+        ps += wave_xor(ps, 32);
+        l[g] = l[g] * alpha + ps;
+        m[g] = mn;
+        const Bf16Split pp = split8(p);
+#pragma unroll
+        for (int nb = 0; nb < 4; ++nb) {
+            o[g][nb] *= alpha;
+            o[g][nb] = mfma3(vs[nb], pp, o[g][nb]);
+        }
+    }
+}
+
+template <int GMAX, int KVT>
+__device__ void chunk_item(const AttnArgs& a, uint32_t row0, uint32_t part, int nrows, uint32_t seq,
+                           uint32_t kvh, int lane) {
+    constexpr int D = 64;
+    const uint32_t G = a.group;
+    const int32_t ql = a.cu[seq + 1] - a.cu[seq];
+    const int32_t ctx = static_cast<int32_t>(a.ctx_lens[seq]);
+    const int32_t li0 = static_cast<int32_t>(row0) - a.cu[seq];
+    const int qi = lane & 15;  // this lane's query row within the tile
+    const bool qlive = qi < nrows;
+    const uint32_t lim = qlive ? row_limit(ctx, ql, li0 + qi, a.capacity) : 0;
+    const uint32_t lim_max = row_limit(ctx, ql, li0 + nrows - 1, a.capacity);
+    const uint32_t t_begin = part * a.part_size;
+    const uint32_t t_end = min(t_begin + a.part_size, lim_max);
+    const PartView pv = load_part(a, seq, t_begin, t_end, lane);
+
+    Bf16Split qs[GMAX][2];  // Q[query qi][d = 32s + 8k + j] as bf16 hi / lo (B operand of S^T)
+    floatx4 o[GMAX][4];
+    float m[GMAX], l[GMAX];
+    const uint32_t qrow = row0 + (qlive ? qi : 0);
+#pragma unroll
+    for (int g = 0; g < GMAX; ++g) {
+        m[g] = -INFINITY;
+        l[g] = 0.f;
+#pragma unroll
+        for (int nb = 0; nb < 4; ++nb) o[g][nb] = floatx4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int sd = 0; sd < 2; ++sd) {
+            float x[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+            if (g < static_cast<int>(G) && qlive) {
+                const float* src = a.q + (static_cast<size_t>(qrow) * a.num_heads + kvh * G + g) * D +
+                                   32 * sd + 8 * (lane >> 4);
+                const float4 x0 = *reinterpret_cast<const float4*>(src);
+                const float4 x1 = *reinterpret_cast<const float4*>(src + 4);
+                x[0] = x0.x; x[1] = x0.y; x[2] = x0.z; x[3] = x0.w;
+                x[4] = x1.x; x[5] = x1.y; x[6] = x1.z; x[7] = x1.w;
+            }
+            qs[g][sd] = split8(x);
+        }
+    }
+
+    // Two 32-key tiles in flight: the next tile's loads overlap this tile's MFMAs.
+    ChunkTile<KVT> ta, tb;
+    chunk_load<KVT>(a, pv, t_begin, kvh, lane, ta);
+    for (uint32_t t0 = t_begin; t0 < t_end; t0 += 64) {
+        const bool has_b = t0 + 32 < t_end;
+        if (has_b) chunk_load<KVT>(a, pv, t0 + 32, kvh, lane, tb);
+        chunk_compute<GMAX, KVT>(a, pv, t0, lane, lim, qs, o, m, l, ta);
+        if (t0 + 64 < t_end) chunk_load<KVT>(a, pv, t0 + 64, kvh, lane, ta);
+        if (has_b) chunk_compute<GMAX, KVT>(a, pv, t0 + 32, lane, lim, qs, o, m, l, tb);
+    }
+
+    // Lane holds O^T[d = 16(lane/16) + 4r + nb][query qi] in o[g][nb][r].
+    const uint32_t np = ceil_div(lim, a.part_size);
+    const bool writer = qlive && part < np;
+    const bool single = np == 1;
+    const int qq = lane >> 4;
+#pragma unroll
+    for (int g = 0; g < GMAX; ++g) {
+        if (g >= static_cast<int>(G)) break;
+        const size_t head = static_cast<size_t>(qrow) * a.num_heads + kvh * G + g;
+        if (writer) {
+            const float inv = single ? (l[g] > 0.f ? 1.0f / l[g] : 0.f) : 1.0f;
+            float* dst = single ? a.out + head * D : a.part_out + (head * a.max_parts + part) * D;
+#pragma unroll
+            for (int r = 0; r < 4; ++r)
+                *reinterpret_cast<float4*>(dst + 16 * qq + 4 * r) =
+                    make_float4(o[g][0][r] * inv, o[g][1][r] * inv, o[g][2][r] * inv, o[g][3][r] * inv);
+            if (!single && qq == 0) a.part_stats[head * a.max_parts + part] = make_float2(m[g], l[g]);
+        }
+    }
+}
+
+// ---------------------------------------------------------------- kernels
+
+// Rows with no key (an empty context, or more query rows than context) get zeros,
+// cpu_paged_attention's output for an empty context. Grid-stride over sequences.
+__device__ void zero_empty_rows(const AttnArgs& a, const SeqTable& st, uint32_t D) {
+    const uint32_t n_threads = gridDim.x * kThreads;
+    for (uint32_t s = blockIdx.x * kThreads + threadIdx.x; s < a.num_seqs; s += n_threads) {
+        const int32_t ql = st.cu[s + 1] - st.cu[s];
+        for (int32_t i = 0; i < ql; ++i)
+            if (row_limit(st.ctx[s], ql, i, a.capacity) == 0) {
+                float* row = a.out + static_cast<size_t>(st.cu[s] + i) * a.num_heads * D;
+                for (uint32_t e = 0; e < a.num_heads * D; ++e) row[e] = 0.f;
+            }
+    }
+}
+
+// Decode items (one query row x partition x KV head), persistent grid-stride.
+// WAVES = resident waves per SIMD the register budget is capped for.
+template <int D, int GMAX, int KVT, int NL, bool DB, int WAVES, bool BUF>
+__global__ __launch_bounds__(kThreads, WAVES) void attn_decode(AttnArgs a) {
+    __shared__ SeqTable st;
+    PoolRsrc rs;
+    if constexpr (BUF) {
+        rs.k = make_rsrc(a.k_pool, a.pool_bytes);
+        rs.v = make_rsrc(a.v_pool, a.pool_bytes);
+        rs.ks = make_rsrc(a.k_scales, a.scale_bytes);
+        rs.vs = make_rsrc(a.v_scales, a.scale_bytes);
+    }
+    load_seq_table<false>(a, st);
+    zero_empty_rows(a, st, D);
+    const int lane = threadIdx.x & (kWave - 1);
+    const uint32_t wave = blockIdx.x * kWaves + threadIdx.x / kWave;
+    const uint32_t n_waves = gridDim.x * kWaves;
+    const uint32_t n_work = st.pre[a.num_seqs] * a.num_kv_heads;
+    for (uint32_t w = wave; w < n_work; w += n_waves) {
+        const uint32_t item = w / a.num_kv_heads, kvh = w % a.num_kv_heads;
+        const uint32_t s = find_seq(st, a.num_seqs, item);
+        uint32_t local = item - st.pre[s];
+        const int32_t ql = st.cu[s + 1] - st.cu[s];
+        int32_t i = 0;
+        if (ql > 1) {  // rows of a multi-row sequence without the MFMA path
+            for (; i < ql; ++i) {
+                const uint32_t np = ceil_div(row_limit(st.ctx[s], ql, i, a.capacity), a.part_size);
+                if (local < np) break;
+                local -= np;
+            }
+        }
+        decode_item<D, GMAX, KVT, NL, DB, BUF>(a, rs, static_cast<uint32_t>(st.cu[s] + i), local, s, kvh, lane);
+    }
+}
+
+// Prefill-chunk items (16 rows x partition x KV head) on the matrix cores.
+template <int KVT>
+__global__ __launch_bounds__(kThreads) void attn_chunk(AttnArgs a) {
+    __shared__ SeqTable st;
+    load_seq_table<true>(a, st);
+    const int lane = threadIdx.x & (kWave - 1);
+    const uint32_t wave = blockIdx.x * kWaves + threadIdx.x / kWave;
+    const uint32_t n_waves = gridDim.x * kWaves;
+    const uint32_t n_work = st.pre[a.num_seqs] * a.num_kv_heads;
+    for (uint32_t w = wave; w < n_work; w += n_waves) {
+        const uint32_t item = w / a.num_kv_heads, kvh = w % a.num_kv_heads;
+        const uint32_t s = find_seq(st, a.num_seqs, item);
+        uint32_t local = item - st.pre[s];
+        const int32_t ql = st.cu[s + 1] - st.cu[s];
+        int32_t i0 = 0;
+        for (; i0 < ql; i0 += kChunkRows) {
+            const int32_t last = min(i0 + kChunkRows, ql) - 1;
+            const uint32_t np = ceil_div(row_limit(st.ctx[s], ql, last, a.capacity), a.part_size);
+            if (local < np) break;
+            local -= np;
+        }
+        chunk_item<4, KVT>(a, static_cast<uint32_t>(st.cu[s] + i0), local, min(kChunkRows, ql - i0), s,
+                           kvh, lane);
+    }
+}
+
+// One wave per (row, query head) in a grid-stride loop: rows split over several
+// partitions are merged (a kernel boundary orders them after every partial);
+// single-partition rows were written by stage 1.
+template <int D>
+__global__ __launch_bounds__(kThreads) void attn_reduce(AttnArgs a) {
+    __shared__ SeqTable st;
+    const uint32_t tid = threadIdx.x;
+    for (uint32_t s = tid; s <= a.num_seqs; s += kThreads) {
+        st.cu[s] = a.cu[s];
+        if (s < a.num_seqs) st.ctx[s] = static_cast<int32_t>(a.ctx_lens[s]);
+    }
+    __syncthreads();
+    constexpr int LPT = D / 4 < kWave ? D / 4 : kWave;  // lanes holding 4 elements each
+    constexpr int N4 = D / 4 / LPT;
+    const int lane = threadIdx.x & (kWave - 1);
+    const uint32_t n_waves = gridDim.x * kWaves;
+    const uint32_t n_work = a.total_q * a.num_heads;
+    for (uint32_t w = blockIdx.x * kWaves + threadIdx.x / kWave; w < n_work; w += n_waves) {
+        const uint32_t row = w / a.num_heads, h = w % a.num_heads;
+        uint32_t lo = 0, hi = a.num_seqs;  // last s with cu[s] <= row
+        while (hi - lo > 1) {
+            const uint32_t mid = (lo + hi) >> 1;
+            if (static_cast<uint32_t>(st.cu[mid]) <= row) lo = mid;
+            else hi = mid;
+        }
+        const int32_t ql = st.cu[lo + 1] - st.cu[lo];
+        const uint32_t lim = row_limit(st.ctx[lo], ql, static_cast<int32_t>(row) - st.cu[lo], a.capacity);
+        const uint32_t np = ceil_div(lim, a.part_size);
+        if (np <= 1) continue;
+        if (lane < LPT) merge_partials<D, N4>(a, static_cast<size_t>(row) * a.num_heads + h, np, lane * 4 * N4);
     }
 }
 
@@ -337,34 +792,73 @@ __global__ void iota_cu(int32_t* cu, uint32_t n) {
 
 using Stage1Fn = void (*)(AttnArgs);
 
+// Decode kernel variant: tokens per lane per tile, double buffering and the
+// resident-wave target the register budget is capped for. KANSO_DECODE_VARIANT
+// selects one for experiments: "8d2" (default), "8s4", "4d4", "4s6".
+enum DecodeVariant { kV8d2, kV8s4, kV4d4, kV4s6 };
+DecodeVariant decode_variant() {
+    static const DecodeVariant v = [] {
+        const char* e = std::getenv("KANSO_DECODE_VARIANT");
+        if (!e) return kV8d2;
+        const std::string s(e);
+        if (s == "8s4") return kV8s4;
+        if (s == "4d4") return kV4d4;
+        if (s == "4s6") return kV4s6;
+        return kV8d2;
+    }();
+    return v;
+}
+
+template <int D, int GMAX, int KVT, bool BUF>
+Stage1Fn pick_variant() {
+    if constexpr (D == 64 && BUF) {
+        switch (decode_variant()) {
+            case kV8s4: return attn_decode<D, GMAX, KVT, 8, false, 4, BUF>;
+            case kV4d4: return attn_decode<D, GMAX, KVT, 4, true, 4, BUF>;
+            case kV4s6: return attn_decode<D, GMAX, KVT, 4, false, 6, BUF>;
+            default: break;
+        }
+    }
+    return attn_decode<D, GMAX, KVT, 8, true, 2, BUF>;
+}
+
 template <int D, int KVT>
-Stage1Fn pick_group(uint32_t G) {
-    return G <= 4 ? attn_stage1<D, 4, KVT> : attn_stage1<D, 8, KVT>;
+Stage1Fn pick_group(uint32_t G, bool buf) {
+    if (D == 64 && G == 3)  // SmolLM2 (15 / 5 heads)
+        return buf ? pick_variant<D, 3, KVT, true>() : pick_variant<D, 3, KVT, false>();
+    if (G <= 4) return buf ? pick_variant<D, 4, KVT, true>() : pick_variant<D, 4, KVT, false>();
+    return buf ? pick_variant<D, 8, KVT, true>() : pick_variant<D, 8, KVT, false>();
 }
 
 template <int KVT>
-Stage1Fn pick_stage1(uint32_t D, uint32_t G) {
+Stage1Fn pick_decode(uint32_t D, uint32_t G, bool buf) {
     switch (D) {
-        case 4: return KVT == KANSO_KV_F32 || KVT == KANSO_KV_INT8 ? pick_group<4, KVT>(G) : nullptr;
-        case 8: return KVT == KANSO_KV_F32 || KVT == KANSO_KV_INT8 ? pick_group<8, KVT>(G) : nullptr;
-        case 16: return KVT == KANSO_KV_F32 || KVT == KANSO_KV_INT8 ? pick_group<16, KVT>(G) : nullptr;
-        case 32: return pick_group<32, KVT>(G);
-        case 64: return pick_group<64, KVT>(G);
-        case 128: return pick_group<128, KVT>(G);
-        case 256: return pick_group<256, KVT>(G);
+        case 4: return KVT != KANSO_KV_Q8_0 ? pick_group<4, KVT>(G, buf) : nullptr;
+        case 8: return KVT != KANSO_KV_Q8_0 ? pick_group<8, KVT>(G, buf) : nullptr;
+        case 16: return KVT != KANSO_KV_Q8_0 ? pick_group<16, KVT>(G, buf) : nullptr;
+        case 32: return pick_group<32, KVT>(G, buf);
+        case 64: return pick_group<64, KVT>(G, buf);
+        case 128: return pick_group<128, KVT>(G, buf);
+        case 256: return pick_group<256, KVT>(G, buf);
         default: return nullptr;
     }
 }
 
-Stage1Fn pick_stage1_kv(uint32_t kv, uint32_t D, uint32_t G) {
-    if (kv == KANSO_KV_F32) return pick_stage1<KANSO_KV_F32>(D, G);
-    if (kv == KANSO_KV_INT8) return pick_stage1<KANSO_KV_INT8>(D, G);
-    if (kv == KANSO_KV_Q8_0) return pick_stage1<KANSO_KV_Q8_0>(D, G);
+Stage1Fn pick_decode_kv(uint32_t kv, uint32_t D, uint32_t G, bool buf) {
+    if (kv == KANSO_KV_F32) return pick_decode<KANSO_KV_F32>(D, G, buf);
+    if (kv == KANSO_KV_INT8) return pick_decode<KANSO_KV_INT8>(D, G, buf);
+    if (kv == KANSO_KV_Q8_0) return pick_decode<KANSO_KV_Q8_0>(D, G, buf);
     return nullptr;
 }
 
-using ReduceFn = void (*)(AttnArgs);
-ReduceFn pick_reduce(uint32_t D) {
+Stage1Fn pick_chunk_kv(uint32_t kv) {
+    if (kv == KANSO_KV_F32) return attn_chunk<KANSO_KV_F32>;
+    if (kv == KANSO_KV_INT8) return attn_chunk<KANSO_KV_INT8>;
+    if (kv == KANSO_KV_Q8_0) return attn_chunk<KANSO_KV_Q8_0>;
+    return nullptr;
+}
+
+Stage1Fn pick_reduce(uint32_t D) {
     switch (D) {
         case 4: return attn_reduce<4>;
         case 8: return attn_reduce<8>;
@@ -386,11 +880,15 @@ bool head_dim_supported(uint32_t d) {
 }
 
 // Partition size: 256 tokens (the reference's PARTITION_SIZE) unless that leaves
-// too few work items to fill the chip, then halved down to 64.
-uint32_t choose_partition(const kanso_ctx* ctx, uint32_t rows, uint32_t kv_heads, uint32_t capacity) {
+// fewer items than waves the grid keeps resident, then halved down to 64. Capped so
+// a partition touches at most 63 table entries (one register lane each) and kept a
+// power of two (a multiple of the 32-key MFMA tile).
+uint32_t choose_partition(const kanso_ctx* ctx, uint32_t rows, uint32_t kv_heads, uint32_t capacity,
+                          uint32_t block_size) {
     uint32_t P = kRefPartition;
-    const uint64_t target = static_cast<uint64_t>(ctx->num_cus) * 4;
+    const uint64_t target = static_cast<uint64_t>(ctx->num_cus) * 8;
     while (P > 64 && static_cast<uint64_t>(rows) * kv_heads * ((capacity + P - 1) / P) < target) P /= 2;
+    while (P > 32 && P > 62u * block_size) P /= 2;
     return P;
 }
 
@@ -402,6 +900,10 @@ int run_ragged(kanso_ctx* ctx, const kanso_ragged_attention_params* p, const flo
     if (!q || !kp || !vp || !tables || !cu || !ctx_lens || !out) {
         set_error("%s: null buffer", who);
         return KANSO_E_INVALID_ARG;
+    }
+    if (S > kMaxSeqs) {
+        set_error("%s: %u sequences exceed the per-call limit %u", who, S, kMaxSeqs);
+        return KANSO_E_INVALID_SHAPE;
     }
     if (S == 0 || H == 0 || HKV == 0 || p->total_q == 0) {
         set_error("%s: empty shape (seqs %u, heads %u, kv heads %u, rows %u)", who, S, H, HKV, p->total_q);
@@ -444,7 +946,7 @@ int run_ragged(kanso_ctx* ctx, const kanso_ragged_attention_params* p, const flo
     }
     const uint32_t capacity = static_cast<uint32_t>(cap64);
     const uint32_t T = p->total_q;
-    const uint32_t P = choose_partition(ctx, T, HKV, capacity);
+    const uint32_t P = choose_partition(ctx, T, HKV, capacity, p->block_size);
     const uint32_t max_parts = (capacity + P - 1) / P;
     const uint64_t partial_elems = static_cast<uint64_t>(T) * H * max_parts * D;
     if (partial_elems > (1ull << 31)) {
@@ -453,10 +955,9 @@ int run_ragged(kanso_ctx* ctx, const kanso_ragged_attention_params* p, const flo
         return KANSO_E_INVALID_SHAPE;
     }
 
-    // Scratch: [n_items][items T*max_parts int4][stats T*H*max_parts float2][partials].
-    const size_t off_items = 256;
-    const size_t off_stats = align_up(off_items + static_cast<size_t>(T) * max_parts * sizeof(int4), 256);
-    const size_t off_part = align_up(off_stats + static_cast<size_t>(T) * H * max_parts * sizeof(float2), 256);
+    // Scratch: [stats T*H*max_parts float2][partials T*H*max_parts*D f32].
+    const size_t off_stats = 0;
+    const size_t off_part = align_up(static_cast<size_t>(T) * H * max_parts * sizeof(float2), 256);
     const size_t total = off_part + partial_elems * sizeof(float);
     int rc = ensure_scratch(ctx, total);
     if (rc) return rc;
@@ -474,8 +975,6 @@ int run_ragged(kanso_ctx* ctx, const kanso_ragged_attention_params* p, const flo
     a.part_out = reinterpret_cast<float*>(base + off_part);
     a.part_stats = reinterpret_cast<float2*>(base + off_stats);
     a.out = out;
-    a.items = reinterpret_cast<const int4*>(base + off_items);
-    a.n_items = reinterpret_cast<const uint32_t*>(base);
     a.status = ctx->status;
     a.num_seqs = S;
     a.num_heads = H;
@@ -492,25 +991,68 @@ int run_ragged(kanso_ctx* ctx, const kanso_ragged_attention_params* p, const flo
     a.total_q = T;
     a.capacity = capacity;
     a.scale_log2 = p->scale * kLog2e;
+    // MFMA chunk items exist only when some sequence has more than one query row.
+    const uint32_t max_q = p->max_q_len ? p->max_q_len : T;
+    a.use_mfma = (D == 64 && G <= 4 && max_q > 1) ? 1u : 0u;
 
-    Stage1Fn stage1 = pick_stage1_kv(p->kv_dtype, D, G);
-    ReduceFn reduce = pick_reduce(D);
-    if (!stage1 || !reduce) {
+    // Buffer-resource loads need the pool size and every pool tensor below 4 GiB.
+    const uint64_t elem = p->kv_dtype == KANSO_KV_F32 ? 4 : 1;
+    const uint64_t rows = static_cast<uint64_t>(p->num_blocks) * p->block_size * HKV;
+    const uint64_t pool_bytes = rows * D * elem;
+    const uint64_t scale_bytes = p->kv_dtype == KANSO_KV_INT8 ? rows * 4
+                                 : p->kv_dtype == KANSO_KV_Q8_0 ? rows * (D / 32) * 2 : 0;
+    const bool buf = p->num_blocks != 0 && pool_bytes < (1ull << 32);
+    a.pool_bytes = buf ? static_cast<uint32_t>(pool_bytes) : 0u;
+    a.scale_bytes = buf ? static_cast<uint32_t>(scale_bytes) : 0u;
+    Stage1Fn decode = pick_decode_kv(p->kv_dtype, D, G, buf);
+    Stage1Fn chunk = a.use_mfma ? pick_chunk_kv(p->kv_dtype) : nullptr;
+    Stage1Fn reduce = pick_reduce(D);
+    if (!decode || !reduce || (a.use_mfma && !chunk)) {
         set_error("%s: no kernel for head_dim %u / kv_dtype %u", who, D, p->kv_dtype);
         return KANSO_E_INVALID_SHAPE;
     }
 
-    hipEvent_t ev;
-    hipLaunchKernelGGL(build_worklist, dim3(1), dim3(kThreads), 0, stream, a,
-                       reinterpret_cast<int4*>(base + off_items), reinterpret_cast<uint32_t*>(base));
-    KANSO_LAUNCH_CHECK();
-    const uint64_t max_work = static_cast<uint64_t>(T) * max_parts * HKV;
-    const uint32_t grid = static_cast<uint32_t>(std::min<uint64_t>(max_work, static_cast<uint64_t>(ctx->num_cus) * 4));
+    // Persistent grids; every wave strides over its kernel's items, so no grid
+    // depends on device data. Prefill-chunk items (MFMA, compute-bound) run on the
+    // context's side stream concurrently with the decode items (bandwidth-bound):
+    // fork and join are event waits, so the caller's stream order is preserved.
+    hipEvent_t ev, ev_dec, ev_chk;
+    const uint64_t max_waves = (static_cast<uint64_t>(T) * max_parts * HKV + kWaves - 1) / kWaves;
+    const uint32_t dgrid = static_cast<uint32_t>(
+        std::max<uint64_t>(1, std::min<uint64_t>(max_waves, static_cast<uint64_t>(ctx->num_cus) * 2)));
+    const uint32_t cgrid = static_cast<uint32_t>(
+        std::max<uint64_t>(1, std::min<uint64_t>(max_waves, static_cast<uint64_t>(ctx->num_cus))));
     if ((rc = prof_begin(ctx, "attention", stream, &ev))) return rc;
-    hipLaunchKernelGGL(stage1, dim3(grid), dim3(kThreads), 0, stream, a);
+    static const bool serial = [] {
+        const char* e = std::getenv("KANSO_ATTN_SERIAL");
+        return e && *e == '1';
+    }();
+    if (chunk && serial) {  // experiments: chunk kernel before the decode kernel, one stream
+        if ((rc = prof_begin(ctx, "attention_chunk", stream, &ev_chk))) return rc;
+        hipLaunchKernelGGL(chunk, dim3(cgrid), dim3(kThreads), 0, stream, a);
+        KANSO_LAUNCH_CHECK();
+        if ((rc = prof_end(ctx, "attention_chunk", stream, ev_chk))) return rc;
+        chunk = nullptr;
+    }
+    if (chunk) {
+        KANSO_HIP_TRY(hipEventRecord(ctx->ev_fork, stream));
+        KANSO_HIP_TRY(hipStreamWaitEvent(ctx->side, ctx->ev_fork, 0));
+        if ((rc = prof_begin(ctx, "attention_chunk", ctx->side, &ev_chk))) return rc;
+        hipLaunchKernelGGL(chunk, dim3(cgrid), dim3(kThreads), 0, ctx->side, a);
+        KANSO_LAUNCH_CHECK();
+        if ((rc = prof_end(ctx, "attention_chunk", ctx->side, ev_chk))) return rc;
+    }
+    if ((rc = prof_begin(ctx, "attention_decode", stream, &ev_dec))) return rc;
+    hipLaunchKernelGGL(decode, dim3(dgrid), dim3(kThreads), 0, stream, a);
     KANSO_LAUNCH_CHECK();
+    if ((rc = prof_end(ctx, "attention_decode", stream, ev_dec))) return rc;
+    if (chunk) {
+        KANSO_HIP_TRY(hipEventRecord(ctx->ev_join, ctx->side));
+        KANSO_HIP_TRY(hipStreamWaitEvent(stream, ctx->ev_join, 0));
+    }
     if ((rc = prof_end(ctx, "attention", stream, ev))) return rc;
-    const uint32_t rgrid = (T * H + kWaves - 1) / kWaves;
+    const uint32_t rgrid = static_cast<uint32_t>(std::max<uint64_t>(
+        1, std::min<uint64_t>((static_cast<uint64_t>(T) * H + kWaves - 1) / kWaves, ctx->num_cus * 8)));
     if ((rc = prof_begin(ctx, "reduce", stream, &ev))) return rc;
     hipLaunchKernelGGL(reduce, dim3(rgrid), dim3(kThreads), 0, stream, a);
     KANSO_LAUNCH_CHECK();

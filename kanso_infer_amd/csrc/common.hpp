@@ -34,9 +34,18 @@ struct kanso_ctx {
     int device = 0;
     int num_cus = 256;
     uint32_t* status = nullptr;  // device status word (KANSO_DEV_* bits)
+    // Side stream (default priority) for work that overlaps the caller's stream,
+    // forked and joined with the two events.
+    hipStream_t side = nullptr;
+    hipEvent_t ev_fork = nullptr, ev_join = nullptr;
     // Grow-only scratch: split-K partials, work list, small index arrays.
     void* scratch = nullptr;
     size_t scratch_bytes = 0;
+    // Attention arrival counters (zero between calls), grow-only.
+    uint32_t* counters = nullptr;
+    size_t counters_n = 0;
+    // Events reused by the profiling hooks.
+    std::vector<hipEvent_t> event_pool;
     // Grow-only auxiliary buffer for small per-call index arrays.
     void* aux = nullptr;
     size_t aux_bytes = 0;
@@ -61,6 +70,8 @@ namespace kanso {
 // enqueued earlier, so growth waits for the device before freeing the old buffer.
 int ensure_scratch(kanso_ctx* ctx, size_t bytes);
 int ensure_aux(kanso_ctx* ctx, size_t bytes);
+// Makes ctx->counters at least n entries, all zero.
+int ensure_counters(kanso_ctx* ctx, size_t n);
 
 // Profiling hooks around one kernel launch (no-ops unless ctx->profiling).
 int prof_begin(kanso_ctx* ctx, const char* name, hipStream_t stream, hipEvent_t* start);
@@ -86,6 +97,35 @@ inline size_t align_up(size_t x, size_t a) { return (x + a - 1) / a * a; }
 constexpr int kWave = 64;
 
 __device__ __forceinline__ float wave_xor(float v, int mask) { return __shfl_xor(v, mask, kWave); }
+
+// DPP lane permutations inside a 16-lane row (no LDS traffic, no address registers).
+template <int CTRL>
+__device__ __forceinline__ float dpp(float v) {
+    return __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v), CTRL, 0xf, 0xf, true));
+}
+constexpr int kDppQuadSwap1 = 0xB1;   // quad_perm [1,0,3,2]: lane ^ 1
+constexpr int kDppQuadSwap2 = 0x4E;   // quad_perm [2,3,0,1]: lane ^ 2
+constexpr int kDppHalfMirror = 0x141;  // lane i <-> 7 - i within 8 lanes
+constexpr int kDppRowMirror = 0x140;   // lane i <-> 15 - i within 16 lanes
+
+// Sum over aligned groups of N lanes (N = 1, 2, 4, 8, 16, 32, 64); every lane of a
+// group ends with the group's total. Within a row the partners are lane ^ 1,
+// lane ^ 2, the mirror of 8 and the mirror of 16 (a butterfly whose pairings span
+// the group); across rows a lane shuffle.
+template <int N>
+__device__ __forceinline__ float group_sum(float v) {
+    if constexpr (N >= 2) v += dpp<kDppQuadSwap1>(v);
+    if constexpr (N >= 4) v += dpp<kDppQuadSwap2>(v);
+    if constexpr (N >= 8) v += dpp<kDppHalfMirror>(v);
+    if constexpr (N >= 16) v += dpp<kDppRowMirror>(v);
+    if constexpr (N >= 32) v += wave_xor(v, 16);
+    if constexpr (N >= 64) v += wave_xor(v, 32);
+    return v;
+}
+
+// 2^x on the transcendental unit (v_exp_f32); results below the f32 normal range
+// flush to 0, which only ever affects probabilities that are already negligible.
+__device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
 
 __device__ __forceinline__ void raise_status(uint32_t* status, uint32_t bits) {
     atomicOr(status, bits);

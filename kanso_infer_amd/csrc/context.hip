@@ -46,11 +46,37 @@ int ensure_aux(kanso_ctx* ctx, size_t bytes) {
     return KANSO_OK;
 }
 
+int ensure_counters(kanso_ctx* ctx, size_t n) {
+    if (n <= ctx->counters_n) return KANSO_OK;
+    const size_t want = align_up(n + n / 2, 4096);
+    if (ctx->counters) {
+        KANSO_HIP_TRY(hipDeviceSynchronize());
+        KANSO_HIP_TRY(hipFree(ctx->counters));
+        ctx->counters = nullptr;
+        ctx->counters_n = 0;
+    }
+    KANSO_HIP_TRY(hipMalloc(&ctx->counters, want * sizeof(uint32_t)));
+    KANSO_HIP_TRY(hipMemset(ctx->counters, 0, want * sizeof(uint32_t)));
+    ctx->counters_n = want;
+    return KANSO_OK;
+}
+
+static int pooled_event(kanso_ctx* ctx, hipEvent_t* ev) {
+    if (!ctx->event_pool.empty()) {
+        *ev = ctx->event_pool.back();
+        ctx->event_pool.pop_back();
+        return KANSO_OK;
+    }
+    KANSO_HIP_TRY(hipEventCreate(ev));
+    return KANSO_OK;
+}
+
 int prof_begin(kanso_ctx* ctx, const char* name, hipStream_t stream, hipEvent_t* start) {
     (void)name;
     *start = nullptr;
     if (!ctx->profiling) return KANSO_OK;
-    KANSO_HIP_TRY(hipEventCreate(start));
+    int rc = pooled_event(ctx, start);
+    if (rc) return rc;
     KANSO_HIP_TRY(hipEventRecord(*start, stream));
     return KANSO_OK;
 }
@@ -58,7 +84,8 @@ int prof_begin(kanso_ctx* ctx, const char* name, hipStream_t stream, hipEvent_t*
 int prof_end(kanso_ctx* ctx, const char* name, hipStream_t stream, hipEvent_t start) {
     if (!ctx->profiling || !start) return KANSO_OK;
     hipEvent_t stop;
-    KANSO_HIP_TRY(hipEventCreate(&stop));
+    int rc = pooled_event(ctx, &stop);
+    if (rc) return rc;
     KANSO_HIP_TRY(hipEventRecord(stop, stream));
     ctx->pending.push_back(ProfileRecord{name, start, stop});
     return KANSO_OK;
@@ -78,8 +105,8 @@ static int resolve_profiles(kanso_ctx* ctx) {
         }
         tot->ms += ms;
         tot->launches += 1;
-        (void)hipEventDestroy(rec.start);
-        (void)hipEventDestroy(rec.stop);
+        ctx->event_pool.push_back(rec.start);
+        ctx->event_pool.push_back(rec.stop);
     }
     ctx->pending.clear();
     return KANSO_OK;
@@ -117,6 +144,13 @@ int kanso_create(int device, kanso_ctx** out) {
         delete ctx;
         return KANSO_E_HIP;
     }
+    if (hipStreamCreateWithFlags(&ctx->side, hipStreamNonBlocking) != hipSuccess ||
+        hipEventCreateWithFlags(&ctx->ev_fork, hipEventDisableTiming) != hipSuccess ||
+        hipEventCreateWithFlags(&ctx->ev_join, hipEventDisableTiming) != hipSuccess) {
+        set_error("kanso_create: side stream / event creation failed");
+        kanso_destroy(ctx);
+        return KANSO_E_HIP;
+    }
     *out = ctx;
     return KANSO_OK;
 }
@@ -132,6 +166,11 @@ int kanso_destroy(kanso_ctx* ctx) {
     if (ctx->scratch) (void)hipFree(ctx->scratch);
     if (ctx->aux) (void)hipFree(ctx->aux);
     if (ctx->status) (void)hipFree(ctx->status);
+    for (hipEvent_t e : ctx->event_pool) (void)hipEventDestroy(e);
+    if (ctx->counters) (void)hipFree(ctx->counters);
+    if (ctx->ev_fork) (void)hipEventDestroy(ctx->ev_fork);
+    if (ctx->ev_join) (void)hipEventDestroy(ctx->ev_join);
+    if (ctx->side) (void)hipStreamDestroy(ctx->side);
     delete ctx;
     return KANSO_OK;
 }
