@@ -35,7 +35,6 @@
 //    dequantized in registers with the reference's own product (q as f32) * scale.
 #include <cmath>
 #include <cstdlib>
-#include <string>
 
 #include "common.hpp"
 
@@ -45,8 +44,7 @@ namespace {
 constexpr int kThreads = 256;
 constexpr int kWaves = kThreads / kWave;
 constexpr float kLog2e = 1.4426950408889634f;
-constexpr int kChunkRows = 16;  // query rows per MFMA chunk item
-constexpr int kKindChunk = 1;
+constexpr int kChunkBlockRows = 64;  // query rows per MFMA chunk workgroup item (4 waves x 16)
 
 struct AttnArgs {
     const float* q;
@@ -63,6 +61,7 @@ struct AttnArgs {
     uint32_t* status;
     uint32_t num_seqs, num_heads, num_kv_heads, group, block_size, bs_shift;
     uint32_t max_blocks, num_blocks, part_size, max_parts, total_q, capacity;
+    uint32_t chunk_part;  // partition size of MFMA chunk rows (>= part_size)
     uint32_t use_mfma;
     uint32_t pool_bytes, scale_bytes;  // per pool tensor, for buffer resources (< 4 GiB)
     float scale_log2;
@@ -97,14 +96,20 @@ struct SeqTable {
 
 __device__ __forceinline__ bool is_chunk_seq(const AttnArgs& a, int32_t ql) { return a.use_mfma && ql > 1; }
 
+// Partition size of a sequence's rows: MFMA chunk rows use larger partitions (their
+// work items are already 64 rows wide), decode rows the split-K partition.
+__device__ __forceinline__ uint32_t part_of(const AttnArgs& a, int32_t ql) {
+    return is_chunk_seq(a, ql) ? a.chunk_part : a.part_size;
+}
+
 // Items of one sequence for this kernel: per 16-row tile (chunk) or per row (decode),
 // ceil(limit / P) partitions of the tile's last row / the row.
 __device__ uint32_t seq_items(const AttnArgs& a, int32_t ql, int32_t ctx, bool chunk) {
-    const uint32_t P = a.part_size;
+    const uint32_t P = chunk ? a.chunk_part : a.part_size;
     uint32_t n = 0;
     if (chunk) {
-        for (int32_t i0 = 0; i0 < ql; i0 += kChunkRows)
-            n += ceil_div(row_limit(ctx, ql, min(i0 + kChunkRows, ql) - 1, a.capacity), P);
+        for (int32_t i0 = 0; i0 < ql; i0 += kChunkBlockRows)
+            n += ceil_div(row_limit(ctx, ql, min(i0 + kChunkBlockRows, ql) - 1, a.capacity), P);
     } else {
         for (int32_t i = 0; i < ql; ++i) n += ceil_div(row_limit(ctx, ql, i, a.capacity), P);
     }
@@ -502,128 +507,167 @@ __device__ __forceinline__ floatx4 mfma3(const Bf16Split& a, const Bf16Split& b,
     return c;
 }
 
-// One 32-key tile of a chunk item, raw f32 after dequantization. With k = lane/16
-// and m = lane%16:
-//   k[b][s][h]: K[key t0 + 16b + m][d = 32s + 8k + 4h .. +3]   (A operand of S^T)
-//   v[4b + r]:  V[key t0 + 16b + 4k + r][d = 4m .. 4m+3]       (A operand of O^T)
-template <int KVT>
-struct ChunkTile {
-    float4 k[2][2][2];
-    float4 v[8];
+// ---- chunk workgroup: 4 waves x 16 query rows share every K/V tile
+//
+// A 32-key tile is loaded once per workgroup with coalesced 16 B loads (each
+// thread: 2 float4 of K, 2 of V), split to bf16 hi / lo once, and stored in LDS
+// already in MFMA operand order, so a wave fetches an operand with one
+// ds_read_b128 per plane. Raw tiles are prefetched two ahead in registers.
+constexpr int kChunkWaveRows = 16;
+static_assert(kChunkBlockRows == kChunkWaveRows * kWaves, "one 16-row slice per wave");
+constexpr int kChunkKeys = 32;
+
+// LDS image of one tile. K: [b][sd][kq][m] holds K[key 16b + m][d = 32sd + 8kq .. +7]
+// (A operand of S^T); V: [nb][kq][m] holds V[key 16b + 4kq + r][d = 4m + nb] at
+// element j = 4b + r (A operand of O^T). hi and lo planes each.
+struct ChunkStage {
+    bf16x8 k_hi[2][2][4][16], k_lo[2][2][4][16];
+    bf16x8 v_hi[4][4][16], v_lo[4][4][16];
+};
+
+struct RawTile {
+    float4 k[2], v[2];  // float4 f = tid + 256 j: key f / 16, d0 = 4 (f % 16)
 };
 
 template <int KVT>
-__device__ __forceinline__ void chunk_load(const AttnArgs& a, const PartView& pv, uint32_t t0,
-                                           uint32_t kvh, int lane, ChunkTile<KVT>& tl) {
+__device__ __forceinline__ void chunk_load_raw(const AttnArgs& a, const PoolRsrc& rs, const PartView& pv,
+                                               uint32_t t0, uint32_t kvh, RawTile& rt) {
     constexpr int D = 64;
-    const int kq = lane >> 4, m = lane & 15;
 #pragma unroll
-    for (int b = 0; b < 2; ++b) {
-        uint32_t tk = t0 + 16 * b + m;
-        if (tk >= pv.t_end) tk = t0;
-        const size_t rk = pool_row(a, pv, tk, kvh);
+    for (int j = 0; j < 2; ++j) {
+        const uint32_t f = threadIdx.x + kThreads * j;
+        const uint32_t t = t0 + f / 16;
+        const bool ok = t < pv.t_end;
+        const uint32_t r = static_cast<uint32_t>(pool_row(a, pv, ok ? t : t0, kvh));
+        rt.k[j] = KvBuf<KVT>::load(rs.k, rs.ks, r, ok, D, 4 * (f % 16));
+        rt.v[j] = KvBuf<KVT>::load(rs.v, rs.vs, r, ok, D, 4 * (f % 16));
+    }
+}
+
+__device__ __forceinline__ void chunk_store(const RawTile& rt, ChunkStage& st) {
 #pragma unroll
-        for (int sd = 0; sd < 2; ++sd)
+    for (int j = 0; j < 2; ++j) {
+        const uint32_t f = threadIdx.x + kThreads * j;
+        const uint32_t key = f / 16, d0 = 4 * (f % 16);
+        // K: 4 consecutive d of one key -> half of a 16 B operand entry.
+        {
+            const uint32_t b = key / 16, m = key % 16, sd = d0 / 32, kq = (d0 % 32) / 8, j0 = d0 % 8;
+            const float x[4] = {rt.k[j].x, rt.k[j].y, rt.k[j].z, rt.k[j].w};
+            __bf16* hi = reinterpret_cast<__bf16*>(&st.k_hi[b][sd][kq][m]) + j0;
+            __bf16* lo = reinterpret_cast<__bf16*>(&st.k_lo[b][sd][kq][m]) + j0;
 #pragma unroll
-            for (int h = 0; h < 2; ++h)
-                tl.k[b][sd][h] = KvLoader<KVT>::load(a.k_pool, a.k_scales, rk, D, 32 * sd + 8 * kq + 4 * h);
+            for (int c = 0; c < 4; ++c) {
+                const __bf16 h = static_cast<__bf16>(x[c]);
+                hi[c] = h;
+                lo[c] = static_cast<__bf16>(x[c] - static_cast<float>(h));
+            }
+        }
+        // V: the 4 values land in the 4 d-blocks nb = c (transpose to d-major).
+        {
+            const uint32_t b = key / 16, kq = (key % 16) / 4, r = key % 4, m = d0 / 4;
+            const float x[4] = {rt.v[j].x, rt.v[j].y, rt.v[j].z, rt.v[j].w};
 #pragma unroll
-        for (int r = 0; r < 4; ++r) {
-            uint32_t tv = t0 + 16 * b + 4 * kq + r;
-            if (tv >= pv.t_end) tv = t0;
-            tl.v[4 * b + r] = KvLoader<KVT>::load(a.v_pool, a.v_scales, pool_row(a, pv, tv, kvh), D, 4 * m);
+            for (int c = 0; c < 4; ++c) {
+                const __bf16 h = static_cast<__bf16>(x[c]);
+                reinterpret_cast<__bf16*>(&st.v_hi[c][kq][m])[4 * b + r] = h;
+                reinterpret_cast<__bf16*>(&st.v_lo[c][kq][m])[4 * b + r] =
+                    static_cast<__bf16>(x[c] - static_cast<float>(h));
+            }
         }
     }
 }
 
-template <int GMAX, int KVT>
-__device__ __forceinline__ void chunk_compute(const AttnArgs& a, const PartView& pv, uint32_t t0, int lane,
-                                              uint32_t lim, const Bf16Split (&qs)[GMAX][2],
-                                              floatx4 (&o)[GMAX][4], float (&m)[GMAX], float (&l)[GMAX],
-                                              const ChunkTile<KVT>& tl) {
-    const uint32_t G = a.group;
-    // bf16 operands of this tile, shared by every query head of the group.
-    Bf16Split ks[2][2], vs[4];
+// One tile for this wave's 16 rows x G heads. Operands are fetched from LDS one key
+// block (S^T) or one d-block (O^T) at a time, so only the scores / probabilities of
+// the G heads stay live across the tile.
+template <int G>
+__device__ __forceinline__ void chunk_compute(const AttnArgs& a, const ChunkStage& st, uint32_t t0,
+                                              uint32_t t_end, int lane, uint32_t lim,
+                                              const Bf16Split (&qs)[G][2], floatx4 (&o)[G][4],
+                                              float (&m)[G], float (&l)[G]) {
+    const int kq = lane >> 4, mm = lane & 15;
+    const uint32_t kbase = t0 + 4 * kq;  // key of score (b, r) is kbase + 16b + r
+    float sc[G][8];
 #pragma unroll
-    for (int b = 0; b < 2; ++b)
+    for (int b = 0; b < 2; ++b) {
+        Bf16Split k0, k1;
+        k0.hi = st.k_hi[b][0][kq][mm];
+        k0.lo = st.k_lo[b][0][kq][mm];
+        k1.hi = st.k_hi[b][1][kq][mm];
+        k1.lo = st.k_lo[b][1][kq][mm];
 #pragma unroll
-        for (int sd = 0; sd < 2; ++sd) {
-            const float x[8] = {tl.k[b][sd][0].x, tl.k[b][sd][0].y, tl.k[b][sd][0].z, tl.k[b][sd][0].w,
-                                tl.k[b][sd][1].x, tl.k[b][sd][1].y, tl.k[b][sd][1].z, tl.k[b][sd][1].w};
-            ks[b][sd] = split8(x);
-        }
-#pragma unroll
-    for (int nb = 0; nb < 4; ++nb) {
-        float x[8];
-#pragma unroll
-        for (int j = 0; j < 8; ++j) x[j] = comp(tl.v[j], nb);
-        vs[nb] = split8(x);
-    }
-    const uint32_t kbase = t0 + 4 * (lane >> 4);  // key of s[b][r] is kbase + 16b + r
-#pragma unroll
-    for (int g = 0; g < GMAX; ++g) {
-        if (g >= static_cast<int>(G)) break;
-        float sc[8];
-        float mt = -INFINITY;
-#pragma unroll
-        for (int b = 0; b < 2; ++b) {
-            floatx4 st = {0.f, 0.f, 0.f, 0.f};
-            st = mfma3(ks[b][0], qs[g][0], st);
-            st = mfma3(ks[b][1], qs[g][1], st);
+        for (int g = 0; g < G; ++g) {
+            floatx4 s4 = {0.f, 0.f, 0.f, 0.f};
+            s4 = mfma3(k0, qs[g][0], s4);
+            s4 = mfma3(k1, qs[g][1], s4);
 #pragma unroll
             for (int r = 0; r < 4; ++r) {
                 const uint32_t key = kbase + 16 * b + r;
-                sc[4 * b + r] = (key < lim && key < pv.t_end) ? st[r] * a.scale_log2 : -INFINITY;
-                mt = fmaxf(mt, sc[4 * b + r]);
+                sc[g][4 * b + r] = (key < lim && key < t_end) ? s4[r] * a.scale_log2 : -INFINITY;
             }
         }
+    }
+    Bf16Split pp[G];
+#pragma unroll
+    for (int g = 0; g < G; ++g) {
+        float mt = -INFINITY;
+#pragma unroll
+        for (int j = 0; j < 8; ++j) mt = fmaxf(mt, sc[g][j]);
         mt = fmaxf(mt, wave_xor(mt, 16));
         mt = fmaxf(mt, wave_xor(mt, 32));
         const float mn = fmaxf(m[g], mt);
         const bool live = mn != -INFINITY;
         const float alpha = live ? fast_exp2(m[g] - mn) : 1.0f;
-        float p[8];
         float ps = 0.f;
 #pragma unroll
         for (int j = 0; j < 8; ++j) {
-            p[j] = live ? fast_exp2(sc[j] - mn) : 0.f;
-            ps += p[j];
+            sc[g][j] = live ? fast_exp2(sc[g][j] - mn) : 0.f;
+            ps += sc[g][j];
         }
         ps += wave_xor(ps, 16);
         ps += wave_xor(ps, 32);
         l[g] = l[g] * alpha + ps;
         m[g] = mn;
-        const Bf16Split pp = split8(p);
+        pp[g] = split8(sc[g]);
 #pragma unroll
-        for (int nb = 0; nb < 4; ++nb) {
-            o[g][nb] *= alpha;
-            o[g][nb] = mfma3(vs[nb], pp, o[g][nb]);
-        }
+        for (int nb = 0; nb < 4; ++nb) o[g][nb] *= alpha;
+    }
+#pragma unroll
+    for (int nb = 0; nb < 4; ++nb) {
+        Bf16Split v;
+        v.hi = st.v_hi[nb][kq][mm];
+        v.lo = st.v_lo[nb][kq][mm];
+#pragma unroll
+        for (int g = 0; g < G; ++g) o[g][nb] = mfma3(v, pp[g], o[g][nb]);
     }
 }
 
-template <int GMAX, int KVT>
-__device__ void chunk_item(const AttnArgs& a, uint32_t row0, uint32_t part, int nrows, uint32_t seq,
-                           uint32_t kvh, int lane) {
+// One workgroup item: 64 query rows (wave w: rows 16w .. 16w + 15 of the block) of
+// one sequence, one key partition, one KV head.
+template <int G, int KVT>
+__device__ void chunk_block(const AttnArgs& a, const PoolRsrc& rs, ChunkStage (&stage)[2], uint32_t row0,
+                            uint32_t part, int nrows_blk, uint32_t seq, uint32_t kvh) {
     constexpr int D = 64;
-    const uint32_t G = a.group;
+    const int lane = threadIdx.x & (kWave - 1), wv = threadIdx.x / kWave;
     const int32_t ql = a.cu[seq + 1] - a.cu[seq];
     const int32_t ctx = static_cast<int32_t>(a.ctx_lens[seq]);
     const int32_t li0 = static_cast<int32_t>(row0) - a.cu[seq];
-    const int qi = lane & 15;  // this lane's query row within the tile
+    const int nrows = min(kChunkWaveRows, nrows_blk - kChunkWaveRows * wv);  // this wave's rows (may be <= 0)
+    const int qi = lane & 15;
     const bool qlive = qi < nrows;
-    const uint32_t lim = qlive ? row_limit(ctx, ql, li0 + qi, a.capacity) : 0;
-    const uint32_t lim_max = row_limit(ctx, ql, li0 + nrows - 1, a.capacity);
-    const uint32_t t_begin = part * a.part_size;
-    const uint32_t t_end = min(t_begin + a.part_size, lim_max);
+    const uint32_t wrow0 = row0 + kChunkWaveRows * wv;
+    const uint32_t lim = qlive ? row_limit(ctx, ql, li0 + kChunkWaveRows * wv + qi, a.capacity) : 0;
+    const uint32_t lim_max = row_limit(ctx, ql, li0 + nrows_blk - 1, a.capacity);  // last row of the block
+    const uint32_t t_begin = part * a.chunk_part;
+    const uint32_t t_end = min(t_begin + a.chunk_part, lim_max);
     const PartView pv = load_part(a, seq, t_begin, t_end, lane);
 
-    Bf16Split qs[GMAX][2];  // Q[query qi][d = 32s + 8k + j] as bf16 hi / lo (B operand of S^T)
-    floatx4 o[GMAX][4];
-    float m[GMAX], l[GMAX];
-    const uint32_t qrow = row0 + (qlive ? qi : 0);
+    Bf16Split qs[G][2];  // Q[query qi][d = 32 sd + 8 kq + j] as bf16 hi / lo (B operand of S^T)
+    floatx4 o[G][4];
+    float m[G], l[G];
+    const uint32_t qrow = wrow0 + (qlive ? qi : 0);
 #pragma unroll
-    for (int g = 0; g < GMAX; ++g) {
+    for (int g = 0; g < G; ++g) {
         m[g] = -INFINITY;
         l[g] = 0.f;
 #pragma unroll
@@ -631,7 +675,7 @@ __device__ void chunk_item(const AttnArgs& a, uint32_t row0, uint32_t part, int 
 #pragma unroll
         for (int sd = 0; sd < 2; ++sd) {
             float x[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
-            if (g < static_cast<int>(G) && qlive) {
+            if (qlive) {
                 const float* src = a.q + (static_cast<size_t>(qrow) * a.num_heads + kvh * G + g) * D +
                                    32 * sd + 8 * (lane >> 4);
                 const float4 x0 = *reinterpret_cast<const float4*>(src);
@@ -643,25 +687,31 @@ __device__ void chunk_item(const AttnArgs& a, uint32_t row0, uint32_t part, int 
         }
     }
 
-    // Two 32-key tiles in flight: the next tile's loads overlap this tile's MFMAs.
-    ChunkTile<KVT> ta, tb;
-    chunk_load<KVT>(a, pv, t_begin, kvh, lane, ta);
-    for (uint32_t t0 = t_begin; t0 < t_end; t0 += 64) {
-        const bool has_b = t0 + 32 < t_end;
-        if (has_b) chunk_load<KVT>(a, pv, t0 + 32, kvh, lane, tb);
-        chunk_compute<GMAX, KVT>(a, pv, t0, lane, lim, qs, o, m, l, ta);
-        if (t0 + 64 < t_end) chunk_load<KVT>(a, pv, t0 + 64, kvh, lane, ta);
-        if (has_b) chunk_compute<GMAX, KVT>(a, pv, t0 + 32, lane, lim, qs, o, m, l, tb);
+    const uint32_t n_tiles = ceil_div(t_end - t_begin, kChunkKeys);
+    RawTile ra, rb;
+    chunk_load_raw<KVT>(a, rs, pv, t_begin, kvh, ra);
+    if (n_tiles > 1) chunk_load_raw<KVT>(a, rs, pv, t_begin + kChunkKeys, kvh, rb);
+    chunk_store(ra, stage[0]);
+    __syncthreads();
+    for (uint32_t i = 0; i < n_tiles; ++i) {
+        // rb holds tile i + 1 (in flight); ra is free for tile i + 2.
+        if (i + 2 < n_tiles) chunk_load_raw<KVT>(a, rs, pv, t_begin + kChunkKeys * (i + 2), kvh, ra);
+        if (nrows > 0)
+            chunk_compute<G>(a, stage[i & 1], t_begin + kChunkKeys * i, t_end, lane, lim, qs, o, m, l);
+        if (i + 1 < n_tiles) chunk_store(rb, stage[(i + 1) & 1]);
+        __syncthreads();
+        const RawTile t = ra;
+        ra = rb;
+        rb = t;
     }
 
     // Lane holds O^T[d = 16(lane/16) + 4r + nb][query qi] in o[g][nb][r].
-    const uint32_t np = ceil_div(lim, a.part_size);
+    const uint32_t np = ceil_div(lim, a.chunk_part);
     const bool writer = qlive && part < np;
     const bool single = np == 1;
     const int qq = lane >> 4;
 #pragma unroll
-    for (int g = 0; g < GMAX; ++g) {
-        if (g >= static_cast<int>(G)) break;
+    for (int g = 0; g < G; ++g) {
         const size_t head = static_cast<size_t>(qrow) * a.num_heads + kvh * G + g;
         if (writer) {
             const float inv = single ? (l[g] > 0.f ? 1.0f / l[g] : 0.f) : 1.0f;
@@ -691,10 +741,14 @@ __device__ void zero_empty_rows(const AttnArgs& a, const SeqTable& st, uint32_t 
     }
 }
 
-// Decode items (one query row x partition x KV head), persistent grid-stride.
-// WAVES = resident waves per SIMD the register budget is capped for.
-template <int D, int GMAX, int KVT, int NL, bool DB, int WAVES, bool BUF>
-__global__ __launch_bounds__(kThreads, WAVES) void attn_decode(AttnArgs a) {
+// The attention kernel: one persistent launch. Workgroups [0, n_chunk_wg) take the
+// prefill-chunk items (64 rows x partition x KV head, grid-stride over those
+// workgroups); the waves of the other workgroups take the decode items (one row x
+// partition x KV head) round-robin. Compute-bound MFMA work and bandwidth-bound
+// decode work therefore run side by side on different CUs. With no chunk items (or
+// more chunk items than workgroups) every wave also takes decode items.
+template <int D, int GMAX, int KVT, bool BUF, int GC>
+__global__ __launch_bounds__(kThreads, 2) void attn_main(AttnArgs a) {
     __shared__ SeqTable st;
     PoolRsrc rs;
     if constexpr (BUF) {
@@ -703,11 +757,41 @@ __global__ __launch_bounds__(kThreads, WAVES) void attn_decode(AttnArgs a) {
         rs.ks = make_rsrc(a.k_scales, a.scale_bytes);
         rs.vs = make_rsrc(a.v_scales, a.scale_bytes);
     }
+    uint32_t n_chunk_wg = 0;
+    if constexpr (GC > 0) {
+        __shared__ ChunkStage stage[2];
+        if (a.use_mfma) {
+            load_seq_table<true>(a, st);
+            const uint32_t n_chunk = st.pre[a.num_seqs] * a.num_kv_heads;
+            n_chunk_wg = n_chunk < gridDim.x ? n_chunk : 0u;  // 0: all workgroups do both
+            const uint32_t stride = n_chunk_wg ? n_chunk_wg : gridDim.x;
+            if (n_chunk_wg == 0 || blockIdx.x < n_chunk_wg) {
+                for (uint32_t w = blockIdx.x; w < n_chunk; w += stride) {
+                    const uint32_t item = w / a.num_kv_heads, kvh = w % a.num_kv_heads;
+                    const uint32_t s = find_seq(st, a.num_seqs, item);
+                    uint32_t local = item - st.pre[s];
+                    const int32_t ql = st.cu[s + 1] - st.cu[s];
+                    int32_t i0 = 0;
+                    for (; i0 < ql; i0 += kChunkBlockRows) {
+                        const int32_t last = min(i0 + kChunkBlockRows, ql) - 1;
+                        const uint32_t np = ceil_div(row_limit(st.ctx[s], ql, last, a.capacity), a.chunk_part);
+                        if (local < np) break;
+                        local -= np;
+                    }
+                    chunk_block<GC, KVT>(a, rs, stage, static_cast<uint32_t>(st.cu[s] + i0), local,
+                                         min(kChunkBlockRows, ql - i0), s, kvh);
+                    __syncthreads();  // the next item's prologue reuses the stages
+                }
+                if (n_chunk_wg) return;  // chunk workgroup: done
+            }
+            __syncthreads();  // the decode tables below overwrite the chunk tables
+        }
+    }
     load_seq_table<false>(a, st);
     zero_empty_rows(a, st, D);
     const int lane = threadIdx.x & (kWave - 1);
-    const uint32_t wave = blockIdx.x * kWaves + threadIdx.x / kWave;
-    const uint32_t n_waves = gridDim.x * kWaves;
+    const uint32_t wave = (blockIdx.x - n_chunk_wg) * kWaves + threadIdx.x / kWave;
+    const uint32_t n_waves = (gridDim.x - n_chunk_wg) * kWaves;
     const uint32_t n_work = st.pre[a.num_seqs] * a.num_kv_heads;
     for (uint32_t w = wave; w < n_work; w += n_waves) {
         const uint32_t item = w / a.num_kv_heads, kvh = w % a.num_kv_heads;
@@ -722,33 +806,7 @@ __global__ __launch_bounds__(kThreads, WAVES) void attn_decode(AttnArgs a) {
                 local -= np;
             }
         }
-        decode_item<D, GMAX, KVT, NL, DB, BUF>(a, rs, static_cast<uint32_t>(st.cu[s] + i), local, s, kvh, lane);
-    }
-}
-
-// Prefill-chunk items (16 rows x partition x KV head) on the matrix cores.
-template <int KVT>
-__global__ __launch_bounds__(kThreads) void attn_chunk(AttnArgs a) {
-    __shared__ SeqTable st;
-    load_seq_table<true>(a, st);
-    const int lane = threadIdx.x & (kWave - 1);
-    const uint32_t wave = blockIdx.x * kWaves + threadIdx.x / kWave;
-    const uint32_t n_waves = gridDim.x * kWaves;
-    const uint32_t n_work = st.pre[a.num_seqs] * a.num_kv_heads;
-    for (uint32_t w = wave; w < n_work; w += n_waves) {
-        const uint32_t item = w / a.num_kv_heads, kvh = w % a.num_kv_heads;
-        const uint32_t s = find_seq(st, a.num_seqs, item);
-        uint32_t local = item - st.pre[s];
-        const int32_t ql = st.cu[s + 1] - st.cu[s];
-        int32_t i0 = 0;
-        for (; i0 < ql; i0 += kChunkRows) {
-            const int32_t last = min(i0 + kChunkRows, ql) - 1;
-            const uint32_t np = ceil_div(row_limit(st.ctx[s], ql, last, a.capacity), a.part_size);
-            if (local < np) break;
-            local -= np;
-        }
-        chunk_item<4, KVT>(a, static_cast<uint32_t>(st.cu[s] + i0), local, min(kChunkRows, ql - i0), s,
-                           kvh, lane);
+        decode_item<D, GMAX, KVT, 8, true, BUF>(a, rs, static_cast<uint32_t>(st.cu[s] + i), local, s, kvh, lane);
     }
 }
 
@@ -764,12 +822,15 @@ __global__ __launch_bounds__(kThreads) void attn_reduce(AttnArgs a) {
         if (s < a.num_seqs) st.ctx[s] = static_cast<int32_t>(a.ctx_lens[s]);
     }
     __syncthreads();
-    constexpr int LPT = D / 4 < kWave ? D / 4 : kWave;  // lanes holding 4 elements each
+    // LPT lanes hold 4*N4 elements each; a wave merges PAIRS (row, head) pairs at once.
+    constexpr int LPT = D / 4 < kWave ? D / 4 : kWave;
     constexpr int N4 = D / 4 / LPT;
+    constexpr int PAIRS = kWave / LPT;
     const int lane = threadIdx.x & (kWave - 1);
-    const uint32_t n_waves = gridDim.x * kWaves;
+    const uint32_t slot = static_cast<uint32_t>(lane / LPT), sub = static_cast<uint32_t>(lane % LPT);
+    const uint32_t n_groups = gridDim.x * kWaves * PAIRS;
     const uint32_t n_work = a.total_q * a.num_heads;
-    for (uint32_t w = blockIdx.x * kWaves + threadIdx.x / kWave; w < n_work; w += n_waves) {
+    for (uint32_t w = (blockIdx.x * kWaves + threadIdx.x / kWave) * PAIRS + slot; w < n_work; w += n_groups) {
         const uint32_t row = w / a.num_heads, h = w % a.num_heads;
         uint32_t lo = 0, hi = a.num_seqs;  // last s with cu[s] <= row
         while (hi - lo > 1) {
@@ -779,9 +840,8 @@ __global__ __launch_bounds__(kThreads) void attn_reduce(AttnArgs a) {
         }
         const int32_t ql = st.cu[lo + 1] - st.cu[lo];
         const uint32_t lim = row_limit(st.ctx[lo], ql, static_cast<int32_t>(row) - st.cu[lo], a.capacity);
-        const uint32_t np = ceil_div(lim, a.part_size);
-        if (np <= 1) continue;
-        if (lane < LPT) merge_partials<D, N4>(a, static_cast<size_t>(row) * a.num_heads + h, np, lane * 4 * N4);
+        const uint32_t np = ceil_div(lim, part_of(a, ql));
+        if (np > 1) merge_partials<D, N4>(a, static_cast<size_t>(row) * a.num_heads + h, np, sub * 4 * N4);
     }
 }
 
@@ -792,42 +852,26 @@ __global__ void iota_cu(int32_t* cu, uint32_t n) {
 
 using Stage1Fn = void (*)(AttnArgs);
 
-// Decode kernel variant: tokens per lane per tile, double buffering and the
-// resident-wave target the register budget is capped for. KANSO_DECODE_VARIANT
-// selects one for experiments: "8d2" (default), "8s4", "4d4", "4s6".
-enum DecodeVariant { kV8d2, kV8s4, kV4d4, kV4s6 };
-DecodeVariant decode_variant() {
-    static const DecodeVariant v = [] {
-        const char* e = std::getenv("KANSO_DECODE_VARIANT");
-        if (!e) return kV8d2;
-        const std::string s(e);
-        if (s == "8s4") return kV8s4;
-        if (s == "4d4") return kV4d4;
-        if (s == "4s6") return kV4s6;
-        return kV8d2;
-    }();
-    return v;
-}
-
 template <int D, int GMAX, int KVT, bool BUF>
-Stage1Fn pick_variant() {
+Stage1Fn pick_main_g(uint32_t G) {
     if constexpr (D == 64 && BUF) {
-        switch (decode_variant()) {
-            case kV8s4: return attn_decode<D, GMAX, KVT, 8, false, 4, BUF>;
-            case kV4d4: return attn_decode<D, GMAX, KVT, 4, true, 4, BUF>;
-            case kV4s6: return attn_decode<D, GMAX, KVT, 4, false, 6, BUF>;
+        switch (G) {  // the MFMA chunk path needs the exact group size
+            case 1: return attn_main<D, GMAX, KVT, BUF, 1>;
+            case 2: return attn_main<D, GMAX, KVT, BUF, 2>;
+            case 3: return attn_main<D, GMAX, KVT, BUF, 3>;
+            case 4: return attn_main<D, GMAX, KVT, BUF, 4>;
             default: break;
         }
     }
-    return attn_decode<D, GMAX, KVT, 8, true, 2, BUF>;
+    return attn_main<D, GMAX, KVT, BUF, 0>;
 }
 
 template <int D, int KVT>
 Stage1Fn pick_group(uint32_t G, bool buf) {
     if (D == 64 && G == 3)  // SmolLM2 (15 / 5 heads)
-        return buf ? pick_variant<D, 3, KVT, true>() : pick_variant<D, 3, KVT, false>();
-    if (G <= 4) return buf ? pick_variant<D, 4, KVT, true>() : pick_variant<D, 4, KVT, false>();
-    return buf ? pick_variant<D, 8, KVT, true>() : pick_variant<D, 8, KVT, false>();
+        return buf ? pick_main_g<D, 3, KVT, true>(G) : pick_main_g<D, 3, KVT, false>(G);
+    if (G <= 4) return buf ? pick_main_g<D, 4, KVT, true>(G) : pick_main_g<D, 4, KVT, false>(G);
+    return buf ? pick_main_g<D, 8, KVT, true>(G) : pick_main_g<D, 8, KVT, false>(G);
 }
 
 template <int KVT>
@@ -844,17 +888,10 @@ Stage1Fn pick_decode(uint32_t D, uint32_t G, bool buf) {
     }
 }
 
-Stage1Fn pick_decode_kv(uint32_t kv, uint32_t D, uint32_t G, bool buf) {
+Stage1Fn pick_main_kv(uint32_t kv, uint32_t D, uint32_t G, bool buf) {
     if (kv == KANSO_KV_F32) return pick_decode<KANSO_KV_F32>(D, G, buf);
     if (kv == KANSO_KV_INT8) return pick_decode<KANSO_KV_INT8>(D, G, buf);
     if (kv == KANSO_KV_Q8_0) return pick_decode<KANSO_KV_Q8_0>(D, G, buf);
-    return nullptr;
-}
-
-Stage1Fn pick_chunk_kv(uint32_t kv) {
-    if (kv == KANSO_KV_F32) return attn_chunk<KANSO_KV_F32>;
-    if (kv == KANSO_KV_INT8) return attn_chunk<KANSO_KV_INT8>;
-    if (kv == KANSO_KV_Q8_0) return attn_chunk<KANSO_KV_Q8_0>;
     return nullptr;
 }
 
@@ -987,13 +1024,13 @@ int run_ragged(kanso_ctx* ctx, const kanso_ragged_attention_params* p, const flo
     a.max_blocks = p->max_num_blocks_per_seq;
     a.num_blocks = p->num_blocks ? p->num_blocks : 0xffffffffu;
     a.part_size = P;
+    uint32_t cp = 256;
+    while (cp > P && cp > 62u * p->block_size) cp /= 2;
+    a.chunk_part = std::max(cp, P);
     a.max_parts = max_parts;
     a.total_q = T;
     a.capacity = capacity;
     a.scale_log2 = p->scale * kLog2e;
-    // MFMA chunk items exist only when some sequence has more than one query row.
-    const uint32_t max_q = p->max_q_len ? p->max_q_len : T;
-    a.use_mfma = (D == 64 && G <= 4 && max_q > 1) ? 1u : 0u;
 
     // Buffer-resource loads need the pool size and every pool tensor below 4 GiB.
     const uint64_t elem = p->kv_dtype == KANSO_KV_F32 ? 4 : 1;
@@ -1004,55 +1041,31 @@ int run_ragged(kanso_ctx* ctx, const kanso_ragged_attention_params* p, const flo
     const bool buf = p->num_blocks != 0 && pool_bytes < (1ull << 32);
     a.pool_bytes = buf ? static_cast<uint32_t>(pool_bytes) : 0u;
     a.scale_bytes = buf ? static_cast<uint32_t>(scale_bytes) : 0u;
-    Stage1Fn decode = pick_decode_kv(p->kv_dtype, D, G, buf);
-    Stage1Fn chunk = a.use_mfma ? pick_chunk_kv(p->kv_dtype) : nullptr;
+    // MFMA chunk items exist only when some sequence has more than one query row; the
+    // chunk kernel reads the pool through buffer resources (pool below 4 GiB).
+    const uint32_t max_q = p->max_q_len ? p->max_q_len : T;
+    a.use_mfma = (D == 64 && G <= 4 && max_q > 1 && buf) ? 1u : 0u;
+    Stage1Fn main_fn = pick_main_kv(p->kv_dtype, D, G, buf);
     Stage1Fn reduce = pick_reduce(D);
-    if (!decode || !reduce || (a.use_mfma && !chunk)) {
+    if (!main_fn || !reduce) {
         set_error("%s: no kernel for head_dim %u / kv_dtype %u", who, D, p->kv_dtype);
         return KANSO_E_INVALID_SHAPE;
     }
 
-    // Persistent grids; every wave strides over its kernel's items, so no grid
-    // depends on device data. Prefill-chunk items (MFMA, compute-bound) run on the
-    // context's side stream concurrently with the decode items (bandwidth-bound):
-    // fork and join are event waits, so the caller's stream order is preserved.
-    hipEvent_t ev, ev_dec, ev_chk;
+    // One persistent launch: two workgroups (eight waves) per CU; nothing in the grid
+    // depends on device data.
+    hipEvent_t ev;
     const uint64_t max_waves = (static_cast<uint64_t>(T) * max_parts * HKV + kWaves - 1) / kWaves;
-    const uint32_t dgrid = static_cast<uint32_t>(
-        std::max<uint64_t>(1, std::min<uint64_t>(max_waves, static_cast<uint64_t>(ctx->num_cus) * 2)));
-    const uint32_t cgrid = static_cast<uint32_t>(
-        std::max<uint64_t>(1, std::min<uint64_t>(max_waves, static_cast<uint64_t>(ctx->num_cus))));
+    const uint32_t grid = static_cast<uint32_t>(
+        std::max<uint64_t>(1, std::min<uint64_t>(std::max<uint64_t>(max_waves, a.use_mfma ? ctx->num_cus : 1),
+                                                 static_cast<uint64_t>(ctx->num_cus) * 2)));
     if ((rc = prof_begin(ctx, "attention", stream, &ev))) return rc;
-    static const bool serial = [] {
-        const char* e = std::getenv("KANSO_ATTN_SERIAL");
-        return e && *e == '1';
-    }();
-    if (chunk && serial) {  // experiments: chunk kernel before the decode kernel, one stream
-        if ((rc = prof_begin(ctx, "attention_chunk", stream, &ev_chk))) return rc;
-        hipLaunchKernelGGL(chunk, dim3(cgrid), dim3(kThreads), 0, stream, a);
-        KANSO_LAUNCH_CHECK();
-        if ((rc = prof_end(ctx, "attention_chunk", stream, ev_chk))) return rc;
-        chunk = nullptr;
-    }
-    if (chunk) {
-        KANSO_HIP_TRY(hipEventRecord(ctx->ev_fork, stream));
-        KANSO_HIP_TRY(hipStreamWaitEvent(ctx->side, ctx->ev_fork, 0));
-        if ((rc = prof_begin(ctx, "attention_chunk", ctx->side, &ev_chk))) return rc;
-        hipLaunchKernelGGL(chunk, dim3(cgrid), dim3(kThreads), 0, ctx->side, a);
-        KANSO_LAUNCH_CHECK();
-        if ((rc = prof_end(ctx, "attention_chunk", ctx->side, ev_chk))) return rc;
-    }
-    if ((rc = prof_begin(ctx, "attention_decode", stream, &ev_dec))) return rc;
-    hipLaunchKernelGGL(decode, dim3(dgrid), dim3(kThreads), 0, stream, a);
+    hipLaunchKernelGGL(main_fn, dim3(grid), dim3(kThreads), 0, stream, a);
     KANSO_LAUNCH_CHECK();
-    if ((rc = prof_end(ctx, "attention_decode", stream, ev_dec))) return rc;
-    if (chunk) {
-        KANSO_HIP_TRY(hipEventRecord(ctx->ev_join, ctx->side));
-        KANSO_HIP_TRY(hipStreamWaitEvent(stream, ctx->ev_join, 0));
-    }
     if ((rc = prof_end(ctx, "attention", stream, ev))) return rc;
+    const uint64_t pairs_per_wg = static_cast<uint64_t>(kWaves) * (kWave / std::min<uint32_t>(D / 4, kWave));
     const uint32_t rgrid = static_cast<uint32_t>(std::max<uint64_t>(
-        1, std::min<uint64_t>((static_cast<uint64_t>(T) * H + kWaves - 1) / kWaves, ctx->num_cus * 8)));
+        1, std::min<uint64_t>((static_cast<uint64_t>(T) * H + pairs_per_wg - 1) / pairs_per_wg, ctx->num_cus * 8)));
     if ((rc = prof_begin(ctx, "reduce", stream, &ev))) return rc;
     hipLaunchKernelGGL(reduce, dim3(rgrid), dim3(kThreads), 0, stream, a);
     KANSO_LAUNCH_CHECK();

@@ -34,16 +34,9 @@ struct kanso_ctx {
     int device = 0;
     int num_cus = 256;
     uint32_t* status = nullptr;  // device status word (KANSO_DEV_* bits)
-    // Side stream (default priority) for work that overlaps the caller's stream,
-    // forked and joined with the two events.
-    hipStream_t side = nullptr;
-    hipEvent_t ev_fork = nullptr, ev_join = nullptr;
     // Grow-only scratch: split-K partials, work list, small index arrays.
     void* scratch = nullptr;
     size_t scratch_bytes = 0;
-    // Attention arrival counters (zero between calls), grow-only.
-    uint32_t* counters = nullptr;
-    size_t counters_n = 0;
     // Events reused by the profiling hooks.
     std::vector<hipEvent_t> event_pool;
     // Grow-only auxiliary buffer for small per-call index arrays.
@@ -70,8 +63,6 @@ namespace kanso {
 // enqueued earlier, so growth waits for the device before freeing the old buffer.
 int ensure_scratch(kanso_ctx* ctx, size_t bytes);
 int ensure_aux(kanso_ctx* ctx, size_t bytes);
-// Makes ctx->counters at least n entries, all zero.
-int ensure_counters(kanso_ctx* ctx, size_t n);
 
 // Profiling hooks around one kernel launch (no-ops unless ctx->profiling).
 int prof_begin(kanso_ctx* ctx, const char* name, hipStream_t stream, hipEvent_t* start);

@@ -46,21 +46,6 @@ int ensure_aux(kanso_ctx* ctx, size_t bytes) {
     return KANSO_OK;
 }
 
-int ensure_counters(kanso_ctx* ctx, size_t n) {
-    if (n <= ctx->counters_n) return KANSO_OK;
-    const size_t want = align_up(n + n / 2, 4096);
-    if (ctx->counters) {
-        KANSO_HIP_TRY(hipDeviceSynchronize());
-        KANSO_HIP_TRY(hipFree(ctx->counters));
-        ctx->counters = nullptr;
-        ctx->counters_n = 0;
-    }
-    KANSO_HIP_TRY(hipMalloc(&ctx->counters, want * sizeof(uint32_t)));
-    KANSO_HIP_TRY(hipMemset(ctx->counters, 0, want * sizeof(uint32_t)));
-    ctx->counters_n = want;
-    return KANSO_OK;
-}
-
 static int pooled_event(kanso_ctx* ctx, hipEvent_t* ev) {
     if (!ctx->event_pool.empty()) {
         *ev = ctx->event_pool.back();
@@ -144,13 +129,7 @@ int kanso_create(int device, kanso_ctx** out) {
         delete ctx;
         return KANSO_E_HIP;
     }
-    if (hipStreamCreateWithFlags(&ctx->side, hipStreamNonBlocking) != hipSuccess ||
-        hipEventCreateWithFlags(&ctx->ev_fork, hipEventDisableTiming) != hipSuccess ||
-        hipEventCreateWithFlags(&ctx->ev_join, hipEventDisableTiming) != hipSuccess) {
-        set_error("kanso_create: side stream / event creation failed");
-        kanso_destroy(ctx);
-        return KANSO_E_HIP;
-    }
+
     *out = ctx;
     return KANSO_OK;
 }
@@ -167,10 +146,7 @@ int kanso_destroy(kanso_ctx* ctx) {
     if (ctx->aux) (void)hipFree(ctx->aux);
     if (ctx->status) (void)hipFree(ctx->status);
     for (hipEvent_t e : ctx->event_pool) (void)hipEventDestroy(e);
-    if (ctx->counters) (void)hipFree(ctx->counters);
-    if (ctx->ev_fork) (void)hipEventDestroy(ctx->ev_fork);
-    if (ctx->ev_join) (void)hipEventDestroy(ctx->ev_join);
-    if (ctx->side) (void)hipStreamDestroy(ctx->side);
+
     delete ctx;
     return KANSO_OK;
 }
