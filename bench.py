@@ -12,7 +12,7 @@ their own random tables are rotated, so consecutive steps read different blocks
 of the 2.7 GB pool and the 256 MB Infinity Cache cannot hold a step's 276 MB.
 
 value = query rows / second over the timed steps (inputs resident in HBM).
-roofline: stage-1 attention kernel, algorithmic bytes (K/V once per sequence +
+roofline: the attention kernel (attn_main), algorithmic bytes (K/V once per sequence +
 tables + Q + O + lengths) / its average duration from HIP events recorded on the
 launch stream inside the timed region, against 8 TB/s.
 cpu_baseline: the oracle (C++ restatement of the reference CPU path) on the same
@@ -117,8 +117,6 @@ class AttnBench:
         total_ms = start.elapsed_time(stop)
         k_ms, k_n = self.ctx.kernel_time("attention")
         r_ms, r_n = self.ctx.kernel_time("reduce")
-        c_ms, c_n = self.ctx.kernel_time("attention_chunk")
-        d_ms, d_n = self.ctx.kernel_time("attention_decode")
         self.ctx.set_profiling(False)
         self.ctx.check_device_status()
         rows = np.mean([b.total_q for b in self.batches])
@@ -127,7 +125,6 @@ class AttnBench:
         st1 = k_ms / max(k_n, 1)
         return dict(ms_per_step=ms, tokens_per_s=rows / (ms * 1e-3),
                     stage1_ms=st1, reduce_ms=r_ms / max(r_n, 1),
-                    chunk_kernel_ms=c_ms / max(c_n, 1), decode_kernel_ms=d_ms / max(d_n, 1),
                     algorithmic_bytes=int(abytes),
                     stage1_gbps=abytes / (st1 * 1e-3) / 1e9,
                     call_gbps=abytes / (ms * 1e-3) / 1e9)
@@ -397,7 +394,8 @@ def main():
             "frac": round(achieved / HBM_PEAK, 4),
             "traffic": profiled_traffic(),
             "traffic_source": "profiles/attention_config2_hbm_traffic.md (all kernels of one call)",
-            "kernel": "attn_stage1 (split-K ragged paged attention)",
+            "kernel": "attn_main (persistent ragged paged attention: MFMA prefill-chunk "
+                      "workgroups + split-K decode waves)",
             "algorithmic_bytes_per_launch": res["algorithmic_bytes"],
             "avg_launch_ms": round(res["stage1_ms"], 5),
         },

@@ -260,29 +260,55 @@ __device__ __forceinline__ float dot4(float4 a, float4 b) {
 // Merge of `np` partials of one (row, head) for head-dim elements [d0, d0 + 4*n4):
 // out = sum_p acc_p 2^(m_p - M) / sum_p l_p 2^(m_p - M) (paged_attention_v2.metal:
 // 154-205), 1/denominator = 0 for an empty row.
-template <int D, int N4>
-__device__ __forceinline__ void merge_partials(const AttnArgs& a, size_t head, uint32_t np, int d0) {
+// Merge of one (row, head)'s partitions by the LPT lanes of its group (lane `sub`
+// holds output elements [4*N4*sub, 4*N4*(sub+1))). Partition statistics are read one
+// per lane and reduced across the group; partial vectors are fetched four at a time
+// so their loads overlap.
+template <int D, int N4, int LPT>
+__device__ __forceinline__ void merge_partials(const AttnArgs& a, size_t head, uint32_t np, uint32_t sub,
+                                               int lane) {
     const size_t base = head * a.max_parts;
     float M = -INFINITY;
-    for (uint32_t p = 0; p < np; ++p) M = fmaxf(M, a.part_stats[base + p].x);
+    for (uint32_t p = sub; p < np; p += LPT) M = fmaxf(M, a.part_stats[base + p].x);
+    M = group_max<LPT>(M);
     float4 o[N4];
 #pragma unroll
     for (int k = 0; k < N4; ++k) o[k] = make_float4(0.f, 0.f, 0.f, 0.f);
     float L = 0.f;
-    for (uint32_t p = 0; p < np; ++p) {
-        const float2 st = a.part_stats[base + p];
-        const float f = fast_exp2(st.x - M);
-        L += st.y * f;
-        const float4* src = reinterpret_cast<const float4*>(a.part_out + (base + p) * D + d0);
+    const int gbase = lane - static_cast<int>(sub);
+    const int d0 = static_cast<int>(sub) * 4 * N4;
+    for (uint32_t p0 = 0; p0 < np; p0 += LPT) {
+        float f = 0.f;
+        if (p0 + sub < np) {
+            const float2 st = a.part_stats[base + p0 + sub];
+            f = fast_exp2(st.x - M);
+            L += st.y * f;
+        }
+        const uint32_t cnt = np - p0 < LPT ? np - p0 : LPT;
+        for (uint32_t j = 0; j < cnt; j += 4) {
+            float4 v[4][N4];
+            float fj[4];
 #pragma unroll
-        for (int k = 0; k < N4; ++k) {
-            const float4 v = src[k];
-            o[k].x += v.x * f;
-            o[k].y += v.y * f;
-            o[k].z += v.z * f;
-            o[k].w += v.w * f;
+            for (int u = 0; u < 4; ++u) {
+                const uint32_t jj = j + u < cnt ? j + u : cnt - 1;
+                fj[u] = __shfl(f, gbase + static_cast<int>(jj), kWave);
+                if (j + u >= cnt) fj[u] = 0.f;
+                const float4* src = reinterpret_cast<const float4*>(a.part_out + (base + p0 + jj) * D + d0);
+#pragma unroll
+                for (int k = 0; k < N4; ++k) v[u][k] = src[k];
+            }
+#pragma unroll
+            for (int u = 0; u < 4; ++u)
+#pragma unroll
+                for (int k = 0; k < N4; ++k) {
+                    o[k].x += v[u][k].x * fj[u];
+                    o[k].y += v[u][k].y * fj[u];
+                    o[k].z += v[u][k].z * fj[u];
+                    o[k].w += v[u][k].w * fj[u];
+                }
         }
     }
+    L = group_sum<LPT>(L);
     const float inv = L > 0.f ? 1.0f / L : 0.f;
 #pragma unroll
     for (int k = 0; k < N4; ++k)
@@ -841,7 +867,7 @@ __global__ __launch_bounds__(kThreads) void attn_reduce(AttnArgs a) {
         const int32_t ql = st.cu[lo + 1] - st.cu[lo];
         const uint32_t lim = row_limit(st.ctx[lo], ql, static_cast<int32_t>(row) - st.cu[lo], a.capacity);
         const uint32_t np = ceil_div(lim, part_of(a, ql));
-        if (np > 1) merge_partials<D, N4>(a, static_cast<size_t>(row) * a.num_heads + h, np, sub * 4 * N4);
+        if (np > 1) merge_partials<D, N4, LPT>(a, static_cast<size_t>(row) * a.num_heads + h, np, sub, lane);
     }
 }
 
@@ -1056,9 +1082,12 @@ int run_ragged(kanso_ctx* ctx, const kanso_ragged_attention_params* p, const flo
     // depends on device data.
     hipEvent_t ev;
     const uint64_t max_waves = (static_cast<uint64_t>(T) * max_parts * HKV + kWaves - 1) / kWaves;
-    const uint32_t grid = static_cast<uint32_t>(
+    uint32_t grid = static_cast<uint32_t>(
         std::max<uint64_t>(1, std::min<uint64_t>(std::max<uint64_t>(max_waves, a.use_mfma ? ctx->num_cus : 1),
                                                  static_cast<uint64_t>(ctx->num_cus) * 2)));
+    // Chunk workgroups hold their slots only briefly; extra decode workgroups are
+    // dispatched into the slots they free, keeping bytes in flight.
+    if (a.use_mfma) grid += ctx->num_cus / 2;
     if ((rc = prof_begin(ctx, "attention", stream, &ev))) return rc;
     hipLaunchKernelGGL(main_fn, dim3(grid), dim3(kThreads), 0, stream, a);
     KANSO_LAUNCH_CHECK();

@@ -114,6 +114,18 @@ __device__ __forceinline__ float group_sum(float v) {
     return v;
 }
 
+// Maximum over aligned groups of N lanes, like group_sum.
+template <int N>
+__device__ __forceinline__ float group_max(float v) {
+    if constexpr (N >= 2) v = fmaxf(v, dpp<kDppQuadSwap1>(v));
+    if constexpr (N >= 4) v = fmaxf(v, dpp<kDppQuadSwap2>(v));
+    if constexpr (N >= 8) v = fmaxf(v, dpp<kDppHalfMirror>(v));
+    if constexpr (N >= 16) v = fmaxf(v, dpp<kDppRowMirror>(v));
+    if constexpr (N >= 32) v = fmaxf(v, wave_xor(v, 16));
+    if constexpr (N >= 64) v = fmaxf(v, wave_xor(v, 32));
+    return v;
+}
+
 // 2^x on the transcendental unit (v_exp_f32); results below the f32 normal range
 // flush to 0, which only ever affects probabilities that are already negligible.
 __device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
