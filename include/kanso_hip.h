@@ -62,7 +62,9 @@ enum {
     KANSO_DEV_QUERY_OVERFLOW = 1u << 2,   /* query rows > context_len (model.rs:1488-1493)   */
     KANSO_DEV_TABLE_SHORT = 1u << 3,      /* block table shorter than needed (engine.rs:387) */
     KANSO_DEV_SLOT_OOB = 1u << 4,         /* slot >= num_blocks*block_size (kind.rs:130-137) */
-    KANSO_DEV_BLOCK_OOB = 1u << 5         /* physical block id >= num_blocks                 */
+    KANSO_DEV_BLOCK_OOB = 1u << 5,        /* physical block id >= num_blocks                 */
+    KANSO_DEV_POSITION_OOB = 1u << 6,     /* position beyond the RoPE table                  */
+    KANSO_DEV_TOKEN_OOB = 1u << 7         /* token id >= vocab size                          */
 };
 
 /* KV pool element types.
@@ -191,8 +193,9 @@ int kanso_kv_reset_blocks(kanso_ctx* ctx, uint32_t kv_dtype, const uint32_t* blo
                           kanso_stream_t stream);
 
 /* y[b][out] = sum_i W[out][i] * x[b][i] with W in GGUF block_q8_0 layout
- * ([out][in/32] blocks of {f16 d; i8 qs[32]}, 34 B); in % 32 == 0, batch in 1..64.
- * Dequantization semantics of src/quant/q8_0.rs:35-39 / 51-93. */
+ * ([out][in/32] blocks of {f16 d; i8 qs[32]}, 34 B); in % 32 == 0, batch >= 1.
+ * Dequantization semantics of src/quant/q8_0.rs:35-39 / 51-93; bf16 matrix cores
+ * with x split into bf16 hi + lo, f32 accumulation. */
 int kanso_gemv_q8_0(kanso_ctx* ctx, const void* w, const float* x, float* y,
                     uint32_t out_features, uint32_t in_features, uint32_t batch,
                     kanso_stream_t stream);
@@ -203,6 +206,84 @@ int kanso_gemv_q8_0(kanso_ctx* ctx, const void* w, const float* x, float* y,
 int kanso_gemv_q4_k(kanso_ctx* ctx, const void* w, const float* x, float* y,
                     uint32_t out_features, uint32_t in_features, uint32_t batch,
                     kanso_stream_t stream);
+
+/* ---- packed Q8_0 weights and the decoder-layer operations ----------------
+ *
+ * Packed Q8_0: the GGUF block_q8_0 bytes re-laid for the matrix cores, one 544 B
+ * tile per (16-row group, 32-column block): qs[4][16][8] (row r's bytes 8j..8j+7
+ * of the block at offset 128 j + 8 r) followed by d[16] (f16). The group count is
+ * rounded up to an even number (pairs of groups); rows past the matrix are zero.
+ * No reference counterpart: it is this build's device layout of the weights that
+ * LinearWeight::forward (src/weights.rs:43-45) reads as GGUF blocks. */
+
+/* Bytes of a packed matrix of `rows` rows (groups rounded up to a multiple of 2). */
+size_t kanso_q8_0_packed_bytes(uint32_t rows, uint32_t in_features);
+
+/* Re-lays a GGUF Q8_0 matrix [rows][in/32] into packed groups: source group g
+ * (rows 16g..16g+15) becomes destination group g * group_stride + group_offset.
+ * Stride 1 / offsets concatenate matrices (Q, K, V); stride 2 interleaves two
+ * (gate at offset 0, up at offset 1). Destination groups not written keep their
+ * bytes, so the caller zero-fills the buffer first. */
+int kanso_q8_0_pack(kanso_ctx* ctx, const void* gguf, uint32_t rows, uint32_t in_features,
+                    void* packed, uint32_t group_stride, uint32_t group_offset,
+                    kanso_stream_t stream);
+
+/* y[t][out] = W x[t] over a packed matrix (same arithmetic as kanso_gemv_q8_0). */
+int kanso_gemm_q8_0(kanso_ctx* ctx, const void* packed, const float* x, float* y,
+                    uint32_t out_features, uint32_t in_features, uint32_t num_tokens,
+                    kanso_stream_t stream);
+
+/* y[t][out] += W x[t]: the O and down projections with the residual add
+ * (src/model.rs:1716-1721: hidden = hidden + linear(...)). */
+int kanso_gemm_q8_0_residual(kanso_ctx* ctx, const void* packed, const float* x, float* y,
+                             uint32_t out_features, uint32_t in_features,
+                             uint32_t num_tokens, kanso_stream_t stream);
+
+/* out[t][:] = row tokens[t] of a packed Q8_0 embedding table, dequantized
+ * (Model::embed, src/model.rs:425-431; BlockQ8_0::dequantize, src/quant/q8_0.rs:35-39).
+ * Ids >= vocab raise KANSO_DEV_TOKEN_OOB and read row 0. */
+int kanso_embed_q8_0(kanso_ctx* ctx, const void* packed_table, uint32_t vocab, uint32_t hidden,
+                     const uint32_t* tokens, uint32_t num_tokens, float* out,
+                     kanso_stream_t stream);
+
+typedef struct {
+    uint32_t num_tokens;
+    uint32_t hidden;
+    uint32_t num_heads;
+    uint32_t num_kv_heads;
+    uint32_t head_dim;   /* 64 */
+    uint32_t max_pos;    /* rows of the cos / sin tables                          */
+    float eps;           /* RMSNorm epsilon                                        */
+    uint32_t num_blocks; /* F32 pool geometry, for the slot bounds check           */
+    uint32_t block_size;
+} kanso_qkv_params;
+
+/* One layer's attention prologue for num_tokens rows of x [T][hidden]:
+ * RMSNorm(x) * norm_w (src/model.rs:653-659), the Q/K/V projections of the packed
+ * row-concatenation [Wq; Wk; Wv] (project_qkv, :437-475), rotate-half RoPE on Q
+ * and K with cos/sin rows positions[t] of [max_pos][head_dim/2] tables
+ * (rope_apply, :720-737), Q to q_out [T][num_heads][64], K and V written to F32
+ * pool row slot_mapping[t] (write_kv_slots, src/kv_cache/storage.rs:219-254). */
+int kanso_qkv_rope_append(kanso_ctx* ctx, const kanso_qkv_params* p, const void* packed_qkv,
+                          const float* x, const float* norm_w, const int32_t* positions,
+                          const int64_t* slot_mapping, const float* cos_table,
+                          const float* sin_table, float* q_out, float* k_pool, float* v_pool,
+                          kanso_stream_t stream);
+
+/* h[t][j] = silu(g) * u with g, u the gate / up projections of RMSNorm(x[t]) *
+ * norm_w (forward_mlp_block, src/model.rs:367-380); packed_gate_up interleaves the
+ * gate and up groups (kanso_q8_0_pack stride 2). intermediate % 16 == 0. */
+int kanso_gate_up_swiglu(kanso_ctx* ctx, const void* packed_gate_up, const float* x,
+                         const float* norm_w, float eps, uint32_t num_tokens, uint32_t hidden,
+                         uint32_t intermediate, float* h, kanso_stream_t stream);
+
+/* Final RMSNorm (norm_w may be NULL to skip it) of rows x[rows[i]] (rows NULL:
+ * x[i]), the lm_head projection and greedy_token (src/sampler.rs:7-17: the first
+ * maximum wins; NaN never wins): tokens[i] = argmax. logits [num_rows][vocab] is
+ * written when non-NULL (src/model.rs:1729-1738). */
+int kanso_lm_head_argmax(kanso_ctx* ctx, const void* packed, const float* x, const int32_t* rows,
+                         const float* norm_w, float eps, uint32_t num_rows, uint32_t hidden,
+                         uint32_t vocab, float* logits, uint32_t* tokens, kanso_stream_t stream);
 
 /* Timing of the library's own kernels with HIP events on the launch stream.
  * When enabled, every launch of the named kernel is bracketed by events and the

@@ -13,6 +13,10 @@ through the C ABI. It mirrors the reference's own entry points for the path:
   pack_step                <- Engine::step packing, src/engine.rs:376-402
   kv_append / kv_reset_blocks <- KvStorageKind::write_kv_slots / reset_block
   gemv_q8_0 / gemv_q4_k    <- LinearWeight::forward on Q8_0 / Q4_K weights
+  q8_0_pack, gemm_q8_0, gemm_q8_0_residual, embed_q8_0, qkv_rope_append,
+  gate_up_swiglu, lm_head_argmax
+                           <- the layer body of Model::forward_batch_rows
+                              (src/model.rs:1569-1739) on packed Q8_0 weights
 
 Errors are raised as EngineError (src/error.rs:4-11), never swallowed: there is
 no CPU fallback, and a missing library is an error.
@@ -33,7 +37,9 @@ __all__ = [
     "EngineError", "Context", "PagedAttentionParams", "paged_attention_num_partitions",
     "validate_paged_attention_params", "gpu_paged_attention_v2", "paged_attention_v2",
     "ragged_paged_attention", "pack_step", "kv_append", "kv_reset_blocks", "gemv_q8_0",
-    "gemv_q4_k", "KANSO_KV_F32", "KANSO_KV_INT8", "KANSO_KV_Q8_0",
+    "gemv_q4_k", "KANSO_KV_F32", "KANSO_KV_INT8", "KANSO_KV_Q8_0", "q8_0_packed_bytes",
+    "q8_0_pack", "gemm_q8_0", "gemm_q8_0_residual", "embed_q8_0", "qkv_rope_append",
+    "gate_up_swiglu", "lm_head_argmax",
 ]
 
 
@@ -310,3 +316,91 @@ def gemv_q4_k(ctx: Context, w: torch.Tensor, x: torch.Tensor, y: torch.Tensor, o
     batch = x.numel() // in_features
     _check(ctx._lib.kanso_gemv_q4_k(ctx.handle, _ptr(w), _ptr(x), _ptr(y), out_features,
                                     in_features, batch, _stream(stream)))
+
+
+# ---------------------------------------------------------------- packed Q8_0 / decoder ops
+
+
+def q8_0_packed_bytes(rows: int, in_features: int) -> int:
+    """Bytes of a packed Q8_0 matrix (16-row groups rounded up to pairs)."""
+    return int(_capi.load().kanso_q8_0_packed_bytes(rows, in_features))
+
+
+def q8_0_pack(ctx: Context, gguf: torch.Tensor, rows: int, in_features: int, packed: torch.Tensor,
+              group_stride: int = 1, group_offset: int = 0,
+              stream: torch.cuda.Stream | None = None) -> None:
+    """Re-lays GGUF block_q8_0 bytes into the packed layout (source group g ->
+    destination group g * group_stride + group_offset)."""
+    _check(ctx._lib.kanso_q8_0_pack(ctx.handle, _ptr(gguf), rows, in_features, _ptr(packed),
+                                    group_stride, group_offset, _stream(stream)))
+
+
+def pack_q8_0_matrix(ctx: Context, gguf: torch.Tensor, rows: int, in_features: int) -> torch.Tensor:
+    """A freshly allocated packed copy of one GGUF Q8_0 matrix."""
+    packed = torch.zeros(q8_0_packed_bytes(rows, in_features), dtype=torch.uint8,
+                         device=gguf.device)
+    q8_0_pack(ctx, gguf, rows, in_features, packed)
+    return packed
+
+
+def gemm_q8_0(ctx: Context, packed: torch.Tensor, x: torch.Tensor, y: torch.Tensor,
+              out_features: int, in_features: int,
+              stream: torch.cuda.Stream | None = None) -> None:
+    """y[t, out] = W x[t] over a packed matrix."""
+    T = x.numel() // in_features
+    _check(ctx._lib.kanso_gemm_q8_0(ctx.handle, _ptr(packed), _ptr(x), _ptr(y), out_features,
+                                    in_features, T, _stream(stream)))
+
+
+def gemm_q8_0_residual(ctx: Context, packed: torch.Tensor, x: torch.Tensor, y: torch.Tensor,
+                       out_features: int, in_features: int,
+                       stream: torch.cuda.Stream | None = None) -> None:
+    """y[t, out] += W x[t] (projection + residual add)."""
+    T = x.numel() // in_features
+    _check(ctx._lib.kanso_gemm_q8_0_residual(ctx.handle, _ptr(packed), _ptr(x), _ptr(y),
+                                             out_features, in_features, T, _stream(stream)))
+
+
+def embed_q8_0(ctx: Context, packed_table: torch.Tensor, vocab: int, hidden: int,
+               tokens: torch.Tensor, out: torch.Tensor,
+               stream: torch.cuda.Stream | None = None) -> None:
+    """out[t] = dequantized row tokens[t] of a packed Q8_0 embedding table."""
+    _check(ctx._lib.kanso_embed_q8_0(ctx.handle, _ptr(packed_table), vocab, hidden, _ptr(tokens),
+                                     tokens.numel(), _ptr(out), _stream(stream)))
+
+
+def qkv_rope_append(ctx: Context, packed_qkv: torch.Tensor, x: torch.Tensor, norm_w: torch.Tensor,
+                    positions: torch.Tensor, slot_mapping: torch.Tensor, cos_t: torch.Tensor,
+                    sin_t: torch.Tensor, q_out: torch.Tensor, k_pool: torch.Tensor,
+                    v_pool: torch.Tensor, *, hidden: int, num_heads: int, num_kv_heads: int,
+                    num_blocks: int, block_size: int, eps: float = 1e-5, head_dim: int = 64,
+                    stream: torch.cuda.Stream | None = None) -> None:
+    """RMSNorm + Q/K/V + RoPE; Q to q_out, K/V into pool row slot_mapping[t]."""
+    T = x.numel() // hidden
+    p = _capi.QkvParamsC(T, hidden, num_heads, num_kv_heads, head_dim,
+                         cos_t.numel() // (head_dim // 2), eps, num_blocks, block_size)
+    _check(ctx._lib.kanso_qkv_rope_append(
+        ctx.handle, C.byref(p), _ptr(packed_qkv), _ptr(x), _ptr(norm_w), _ptr(positions),
+        _ptr(slot_mapping), _ptr(cos_t), _ptr(sin_t), _ptr(q_out), _ptr(k_pool), _ptr(v_pool),
+        _stream(stream)))
+
+
+def gate_up_swiglu(ctx: Context, packed_gate_up: torch.Tensor, x: torch.Tensor,
+                   norm_w: torch.Tensor, h: torch.Tensor, *, hidden: int, intermediate: int,
+                   eps: float = 1e-5, stream: torch.cuda.Stream | None = None) -> None:
+    """h[t] = silu(gate(n)) * up(n) with n = RMSNorm(x[t]) * norm_w."""
+    T = x.numel() // hidden
+    _check(ctx._lib.kanso_gate_up_swiglu(ctx.handle, _ptr(packed_gate_up), _ptr(x), _ptr(norm_w),
+                                         eps, T, hidden, intermediate, _ptr(h), _stream(stream)))
+
+
+def lm_head_argmax(ctx: Context, packed: torch.Tensor, x: torch.Tensor, tokens: torch.Tensor, *,
+                   hidden: int, vocab: int, rows: torch.Tensor | None = None,
+                   norm_w: torch.Tensor | None = None, eps: float = 1e-5,
+                   logits: torch.Tensor | None = None,
+                   stream: torch.cuda.Stream | None = None) -> None:
+    """tokens[i] = greedy argmax of lm_head(RMSNorm(x[rows[i]]))."""
+    n = tokens.numel()
+    _check(ctx._lib.kanso_lm_head_argmax(ctx.handle, _ptr(packed), _ptr(x), _ptr(rows),
+                                         _ptr(norm_w), eps, n, hidden, vocab, _ptr(logits),
+                                         _ptr(tokens), _stream(stream)))

@@ -27,6 +27,8 @@ KANSO_DEV_QUERY_OVERFLOW = 1 << 2
 KANSO_DEV_TABLE_SHORT = 1 << 3
 KANSO_DEV_SLOT_OOB = 1 << 4
 KANSO_DEV_BLOCK_OOB = 1 << 5
+KANSO_DEV_POSITION_OOB = 1 << 6
+KANSO_DEV_TOKEN_OOB = 1 << 7
 
 KANSO_KV_F32 = 0
 KANSO_KV_INT8 = 1
@@ -83,6 +85,20 @@ class PackedStepC(C.Structure):
     ]
 
 
+class QkvParamsC(C.Structure):
+    _fields_ = [
+        ("num_tokens", C.c_uint32),
+        ("hidden", C.c_uint32),
+        ("num_heads", C.c_uint32),
+        ("num_kv_heads", C.c_uint32),
+        ("head_dim", C.c_uint32),
+        ("max_pos", C.c_uint32),
+        ("eps", C.c_float),
+        ("num_blocks", C.c_uint32),
+        ("block_size", C.c_uint32),
+    ]
+
+
 # Every symbol the header declares, with its signature.
 _P = C.c_void_p
 _U = C.c_uint32
@@ -102,6 +118,15 @@ SIGNATURES: dict[str, tuple] = {
     "kanso_kv_reset_blocks": (_I, [_P, _U, _P, _U, _U, _U, _U, _U, _P, _P, _P, _P, _P]),
     "kanso_gemv_q8_0": (_I, [_P, _P, _P, _P, _U, _U, _U, _P]),
     "kanso_gemv_q4_k": (_I, [_P, _P, _P, _P, _U, _U, _U, _P]),
+    "kanso_q8_0_packed_bytes": (C.c_size_t, [_U, _U]),
+    "kanso_q8_0_pack": (_I, [_P, _P, _U, _U, _P, _U, _U, _P]),
+    "kanso_gemm_q8_0": (_I, [_P, _P, _P, _P, _U, _U, _U, _P]),
+    "kanso_gemm_q8_0_residual": (_I, [_P, _P, _P, _P, _U, _U, _U, _P]),
+    "kanso_embed_q8_0": (_I, [_P, _P, _U, _U, _P, _U, _P, _P]),
+    "kanso_qkv_rope_append": (_I, [_P, C.POINTER(QkvParamsC), _P, _P, _P, _P, _P, _P, _P, _P, _P,
+                                   _P, _P]),
+    "kanso_gate_up_swiglu": (_I, [_P, _P, _P, _P, C.c_float, _U, _U, _U, _P, _P]),
+    "kanso_lm_head_argmax": (_I, [_P, _P, _P, _P, _P, C.c_float, _U, _U, _U, _P, _P, _P]),
     "kanso_set_profiling": (_I, [_P, _I]),
     "kanso_get_kernel_time": (_I, [_P, C.c_char_p, C.POINTER(C.c_double), C.POINTER(C.c_uint64)]),
 }

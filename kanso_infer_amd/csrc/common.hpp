@@ -42,6 +42,9 @@ struct kanso_ctx {
     // Grow-only auxiliary buffer for small per-call index arrays.
     void* aux = nullptr;
     size_t aux_bytes = 0;
+    // Grow-only buffer of 64-bit argmax keys (lm_head epilogue).
+    void* keys = nullptr;
+    size_t keys_bytes = 0;
     bool profiling = false;
     std::vector<kanso::ProfileRecord> pending;
     std::vector<std::pair<std::string, kanso::ProfileTotal>> totals;
@@ -63,6 +66,7 @@ namespace kanso {
 // enqueued earlier, so growth waits for the device before freeing the old buffer.
 int ensure_scratch(kanso_ctx* ctx, size_t bytes);
 int ensure_aux(kanso_ctx* ctx, size_t bytes);
+int ensure_keys(kanso_ctx* ctx, size_t bytes);
 
 // Profiling hooks around one kernel launch (no-ops unless ctx->profiling).
 int prof_begin(kanso_ctx* ctx, const char* name, hipStream_t stream, hipEvent_t* start);

@@ -46,6 +46,20 @@ int ensure_aux(kanso_ctx* ctx, size_t bytes) {
     return KANSO_OK;
 }
 
+int ensure_keys(kanso_ctx* ctx, size_t bytes) {
+    if (bytes <= ctx->keys_bytes) return KANSO_OK;
+    size_t want = align_up(bytes + bytes / 2, 1 << 16);
+    if (ctx->keys) {
+        KANSO_HIP_TRY(hipDeviceSynchronize());
+        KANSO_HIP_TRY(hipFree(ctx->keys));
+        ctx->keys = nullptr;
+        ctx->keys_bytes = 0;
+    }
+    KANSO_HIP_TRY(hipMalloc(&ctx->keys, want));
+    ctx->keys_bytes = want;
+    return KANSO_OK;
+}
+
 static int pooled_event(kanso_ctx* ctx, hipEvent_t* ev) {
     if (!ctx->event_pool.empty()) {
         *ev = ctx->event_pool.back();
@@ -144,6 +158,7 @@ int kanso_destroy(kanso_ctx* ctx) {
     }
     if (ctx->scratch) (void)hipFree(ctx->scratch);
     if (ctx->aux) (void)hipFree(ctx->aux);
+    if (ctx->keys) (void)hipFree(ctx->keys);
     if (ctx->status) (void)hipFree(ctx->status);
     for (hipEvent_t e : ctx->event_pool) (void)hipEventDestroy(e);
 

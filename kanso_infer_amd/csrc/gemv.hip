@@ -1,10 +1,10 @@
-// gemv.hip — dequant-on-the-fly GEMV / small GEMM over GGUF Q8_0 and Q4_K weights.
+// gemv.hip — dequant-on-the-fly GEMV / small GEMM over GGUF Q4_K weights (the
+// Q8_0 products live in gemm.hip).
 //
-// Reference: scalar_gemv_q8_0 (src/quant/q8_0.rs:69-93) and scalar_gemv_q4_k
-// (src/quant/q4_k.rs:162-186): out[r] = sum over blocks of the dequantized weights
-// times x, f32 accumulation; a batch of b activation rows is b GEMVs. Production
-// reads candle's GGUF blocks (f16 d / dmin: 34 B and 144 B), which is what these
-// kernels consume (src/quant/mod.rs:1-17 documents the layout difference).
+// Reference: scalar_gemv_q4_k (src/quant/q4_k.rs:162-186): out[r] = sum over
+// blocks of the dequantized weights times x, f32 accumulation; a batch of b
+// activation rows is b GEMVs. Production reads candle's GGUF blocks (f16 d / dmin:
+// 144 B), which is what this kernel consumes (src/quant/mod.rs:1-17).
 //
 // Mapping: 16 lanes share one weight row and stride over its blocks, 4 rows per
 // wave64, 16 rows per 256-thread workgroup. The 16 partial sums of a row meet in a
@@ -25,51 +25,6 @@ __device__ __forceinline__ float row_sum16(float v) {
 #pragma unroll
     for (int o = 1; o < kLanesPerRow; o <<= 1) v += wave_xor(v, o);
     return v;
-}
-
-template <int BC>
-__global__ __launch_bounds__(kGemvThreads) void gemv_q8_0_kernel(
-    const uint8_t* __restrict__ w, const float* __restrict__ x, float* __restrict__ y, uint32_t rows,
-    uint32_t in, uint32_t b0, uint32_t bn) {
-    const uint32_t row = blockIdx.x * kRowsPerBlock + threadIdx.x / kLanesPerRow;
-    const uint32_t sub = threadIdx.x % kLanesPerRow;
-    const uint32_t nb = in / 32;
-    const bool live = row < rows;
-    const uint8_t* wr = w + static_cast<size_t>(live ? row : 0) * nb * 34;
-    float acc[BC];
-#pragma unroll
-    for (int j = 0; j < BC; ++j) acc[j] = 0.f;
-    if (live) {
-        for (uint32_t blk = sub; blk < nb; blk += kLanesPerRow) {
-            const uint16_t* bp = reinterpret_cast<const uint16_t*>(wr + blk * 34);  // 2-byte aligned
-            const float d = __half2float(__ushort_as_half(bp[0]));
-            float qf[32];
-#pragma unroll
-            for (int i = 0; i < 16; ++i) {
-                const uint16_t pair = bp[1 + i];
-                qf[2 * i] = static_cast<float>(static_cast<int8_t>(pair & 0xff));
-                qf[2 * i + 1] = static_cast<float>(static_cast<int8_t>(pair >> 8));
-            }
-#pragma unroll
-            for (int j = 0; j < BC; ++j) {
-                if (j >= static_cast<int>(bn)) break;
-                const float4* xv = reinterpret_cast<const float4*>(x + static_cast<size_t>(b0 + j) * in + blk * 32);
-                float s = 0.f;
-#pragma unroll
-                for (int i = 0; i < 8; ++i) {
-                    const float4 xx = xv[i];
-                    s += qf[4 * i] * xx.x + qf[4 * i + 1] * xx.y + qf[4 * i + 2] * xx.z + qf[4 * i + 3] * xx.w;
-                }
-                acc[j] += d * s;
-            }
-        }
-    }
-#pragma unroll
-    for (int j = 0; j < BC; ++j) {
-        if (j >= static_cast<int>(bn)) break;
-        const float r = row_sum16(acc[j]);
-        if (live && sub == 0) y[static_cast<size_t>(b0 + j) * rows + row] = r;
-    }
 }
 
 // get_scale_min_k4 (src/quant/q4_k.rs:16-26) on the 12 packed scale bytes.
@@ -184,30 +139,6 @@ int check_gemv(kanso_ctx* ctx, const void* w, const float* x, float* y, uint32_t
 using namespace kanso;
 
 extern "C" {
-
-int kanso_gemv_q8_0(kanso_ctx* ctx, const void* w, const float* x, float* y, uint32_t out_features,
-                    uint32_t in_features, uint32_t batch, kanso_stream_t stream) {
-    int rc = check_gemv(ctx, w, x, y, out_features, in_features, batch, 32, "kanso_gemv_q8_0");
-    if (rc) return rc;
-    hipStream_t s = as_stream(stream);
-    const uint32_t grid = (out_features + kRowsPerBlock - 1) / kRowsPerBlock;
-    hipEvent_t ev;
-    if ((rc = prof_begin(ctx, "gemv", s, &ev))) return rc;
-    for (uint32_t b0 = 0; b0 < batch; b0 += kBatchChunk) {
-        const uint32_t bn = std::min<uint32_t>(kBatchChunk, batch - b0);
-        if (bn <= 1)
-            hipLaunchKernelGGL(gemv_q8_0_kernel<1>, dim3(grid), dim3(kGemvThreads), 0, s,
-                               static_cast<const uint8_t*>(w), x, y, out_features, in_features, b0, bn);
-        else if (bn <= 4)
-            hipLaunchKernelGGL(gemv_q8_0_kernel<4>, dim3(grid), dim3(kGemvThreads), 0, s,
-                               static_cast<const uint8_t*>(w), x, y, out_features, in_features, b0, bn);
-        else
-            hipLaunchKernelGGL(gemv_q8_0_kernel<8>, dim3(grid), dim3(kGemvThreads), 0, s,
-                               static_cast<const uint8_t*>(w), x, y, out_features, in_features, b0, bn);
-        KANSO_LAUNCH_CHECK();
-    }
-    return prof_end(ctx, "gemv", s, ev);
-}
 
 int kanso_gemv_q4_k(kanso_ctx* ctx, const void* w, const float* x, float* y, uint32_t out_features,
                     uint32_t in_features, uint32_t batch, kanso_stream_t stream) {

@@ -1,0 +1,411 @@
+// q8_gemm.hpp — dequant-on-the-fly Q8_0 matrix products on the bf16 matrix cores,
+// with the fused prologues / epilogues the decoder layer needs.
+//
+// Arithmetic. Y[t][r] = sum_b d[r][b] * sum_{i<32} q[r][32b+i] * x[t][32b+i]
+// (scalar_gemv_q8_0, src/quant/q8_0.rs:51-93). One v_mfma_f32_16x16x32_bf16 has
+// K = 32, exactly one Q8_0 block, so the per-block scale is applied to the MFMA
+// result before it joins the f32 accumulator — the reference's own order. The
+// int8 weights are exact in bf16; x is split into bf16 hi + lo (x - hi is exact in
+// f32), so sum q*x = MFMA(hi, q) + MFMA(lo, q) leaves only the ~2^-17 relative
+// residue of the split. Results do not depend on the batch size: a token's
+// output is computed in the same order whatever else is in the batch.
+//
+// Operand layouts (16x16x32 bf16): lane l holds A[m = l%16][k = 8(l/16) .. +7]
+// (x of token m), B[k = 8(l/16) .. +7][n = l%16] (weights of row n), and the
+// accumulator C[m = 4(l/16) + r][n = l%16], r = 0..3. So a lane's output row is
+// the row whose weights it loaded, and the block scale is a per-lane scalar.
+//
+// Work mapping. A workgroup of 4 waves owns a pair of 16-row weight groups
+// (32 output rows, chosen by the epilogue) and 16*MT tokens; wave w takes
+// k-blocks w, w+4, ... and the four partial sums meet in LDS in a fixed order.
+// MT is 1, 2 or 4 (token tiles per wave), so a weight operand is loaded once per
+// 16*MT tokens.
+//
+// Weight layouts:
+//   GGUF   : [rows][in/32] blocks {f16 d; i8 qs[32]} (34 B), the format the
+//            reference reads (src/quant/mod.rs:1-17);
+//   packed : [groups][in/32] tiles of 544 B, one per (16-row group, block):
+//            qs[kq][row][8] (512 B: lane l's 8 bytes are at 8l) then d[16] f16.
+//            Rows past the matrix are zero. Produced by kanso_q8_0_pack; the
+//            bytes are the GGUF bytes, re-laid so a wave's operand is one
+//            coalesced 512 B load.
+#pragma once
+
+#include "common.hpp"
+
+namespace kanso {
+
+typedef float floatx4 __attribute__((ext_vector_type(4)));
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+
+constexpr int kGemmThreads = 256;
+constexpr int kGemmWaves = kGemmThreads / kWave;
+constexpr uint32_t kPackedTileBytes = 544;  // 16 rows x (32 qs + 2 d)
+
+__device__ __forceinline__ float f16_bits_to_f32(uint16_t h) { return __half2float(__ushort_as_half(h)); }
+
+// 8 int8 (little-endian in q) -> 8 bf16 (exact: |q| <= 128 needs 8 bits).
+__device__ __forceinline__ bf16x8 i8x8_to_bf16(uint64_t q) {
+    uint32_t w[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const float f0 = static_cast<float>(static_cast<int8_t>((q >> (16 * i)) & 0xff));
+        const float f1 = static_cast<float>(static_cast<int8_t>((q >> (16 * i + 8)) & 0xff));
+        w[i] = (__builtin_bit_cast(uint32_t, f0) >> 16) | (__builtin_bit_cast(uint32_t, f1) & 0xffff0000u);
+    }
+    return __builtin_bit_cast(bf16x8, w);
+}
+
+struct Bf16Pair {
+    bf16x8 hi, lo;
+};
+
+__device__ __forceinline__ Bf16Pair split_bf16(const float (&x)[8]) {
+    Bf16Pair r;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+        const __bf16 h = static_cast<__bf16>(x[j]);
+        r.hi[j] = h;
+        r.lo[j] = static_cast<__bf16>(x[j] - static_cast<float>(h));
+    }
+    return r;
+}
+
+// ---------------------------------------------------------------- weight loaders
+
+struct WPacked {
+    const uint8_t* w;
+    uint32_t nb;  // in / 32
+    __device__ __forceinline__ void load(uint32_t g, uint32_t b, int lane, uint64_t& q, float& d) const {
+        const uint8_t* p = w + (static_cast<size_t>(g) * nb + b) * kPackedTileBytes;
+        q = *reinterpret_cast<const uint64_t*>(p + 8 * lane);
+        d = f16_bits_to_f32(*reinterpret_cast<const uint16_t*>(p + 512 + 2 * (lane & 15)));
+    }
+};
+
+struct WGguf {
+    const uint8_t* w;
+    uint32_t nb;
+    uint32_t rows;
+    __device__ __forceinline__ void load(uint32_t g, uint32_t b, int lane, uint64_t& q, float& d) const {
+        const uint32_t row = g * 16 + (lane & 15);
+        if (row >= rows) {
+            q = 0;
+            d = 0.f;
+            return;
+        }
+        // Blocks are 34 B, so qs is only 2-byte aligned: four u16 loads.
+        const uint16_t* p = reinterpret_cast<const uint16_t*>(w + (static_cast<size_t>(row) * nb + b) * 34);
+        d = f16_bits_to_f32(p[0]);
+        const uint16_t* qp = p + 1 + 4 * (lane >> 4);
+        q = static_cast<uint64_t>(qp[0]) | (static_cast<uint64_t>(qp[1]) << 16) |
+            (static_cast<uint64_t>(qp[2]) << 32) | (static_cast<uint64_t>(qp[3]) << 48);
+    }
+};
+
+// ---------------------------------------------------------------- activations
+
+// x rows: token m reads row (rows ? rows[m] : m) of a [*, ldx] f32 matrix. With
+// norm_w set, the row is RMS-normalised first: x / sqrt(mean(x^2) + eps) * w
+// (Model::rmsnorm, src/model.rs:653-659).
+struct XIn {
+    const float* x;
+    const int32_t* rows;
+    const float* norm_w;
+    float eps;
+    uint32_t ldx;
+    uint32_t T;
+    uint32_t in;
+    __device__ __forceinline__ const float* row(uint32_t m) const {
+        return x + static_cast<size_t>(rows ? static_cast<uint32_t>(rows[m]) : m) * ldx;
+    }
+};
+
+// ---------------------------------------------------------------- the kernel
+
+// Every epilogue provides
+//   groups(p, g0, g1): the two 16-row weight groups of pair p;
+//   apply(p, lane, m0, T, v0, v1): outputs of rows g0*16 + lane%16 (v0) and
+//     g1*16 + lane%16 (v1) for tokens m0 .. m0+3 (skip m >= T).
+template <int MT, class WL, class Epi>
+__global__ __launch_bounds__(kGemmThreads) void q8_gemm_kernel(WL wl, XIn xa, Epi epi) {
+    __shared__ float s_rms[16 * MT];
+    __shared__ floatx4 s_part[kGemmWaves][2][MT][kWave];
+    const int lane = threadIdx.x & (kWave - 1), wv = threadIdx.x / kWave;
+    const int kq = lane >> 4, mm = lane & 15;
+    const uint32_t p = blockIdx.x;
+    const uint32_t t0 = blockIdx.y * 16 * MT;
+    const uint32_t nb = xa.in / 32;
+    uint32_t g0, g1;
+    epi.groups(p, g0, g1);
+
+    if (xa.norm_w) {
+        // sum of squares of each token row of this tile; wave w takes 4*MT tokens
+        for (int i = 0; i < 4 * MT; ++i) {
+            const uint32_t tl = wv * 4 * MT + i, m = t0 + tl;
+            float s = 0.f;
+            if (m < xa.T) {
+                const float* xr = xa.row(m);
+                for (uint32_t k = 4 * lane; k < xa.in; k += 4 * kWave) {
+                    const float4 v = *reinterpret_cast<const float4*>(xr + k);
+                    s += v.x * v.x + v.y * v.y + v.z * v.z + v.w * v.w;
+                }
+            }
+            s = group_sum<kWave>(s);
+            if (lane == 0) s_rms[tl] = sqrtf(s / static_cast<float>(xa.in) + xa.eps);
+        }
+        __syncthreads();
+    }
+
+    const float* xr[MT];
+    bool mok[MT];
+#pragma unroll
+    for (int i = 0; i < MT; ++i) {
+        const uint32_t m = t0 + 16 * i + mm;
+        mok[i] = m < xa.T;
+        xr[i] = xa.row(mok[i] ? m : t0);
+    }
+    floatx4 acc[2][MT];
+#pragma unroll
+    for (int i = 0; i < MT; ++i) {
+        acc[0][i] = floatx4{0.f, 0.f, 0.f, 0.f};
+        acc[1][i] = floatx4{0.f, 0.f, 0.f, 0.f};
+    }
+
+    for (uint32_t b = wv; b < nb; b += kGemmWaves) {
+        uint64_t q0, q1;
+        float d0, d1;
+        wl.load(g0, b, lane, q0, d0);
+        wl.load(g1, b, lane, q1, d1);
+        const uint32_t k = 32 * b + 8 * kq;
+        float nw[8];
+        if (xa.norm_w) {
+            const float4 n0 = *reinterpret_cast<const float4*>(xa.norm_w + k);
+            const float4 n1 = *reinterpret_cast<const float4*>(xa.norm_w + k + 4);
+            nw[0] = n0.x; nw[1] = n0.y; nw[2] = n0.z; nw[3] = n0.w;
+            nw[4] = n1.x; nw[5] = n1.y; nw[6] = n1.z; nw[7] = n1.w;
+        }
+        float4 xv[MT][2];
+#pragma unroll
+        for (int i = 0; i < MT; ++i) {
+            xv[i][0] = *reinterpret_cast<const float4*>(xr[i] + k);
+            xv[i][1] = *reinterpret_cast<const float4*>(xr[i] + k + 4);
+        }
+        const bf16x8 w0 = i8x8_to_bf16(q0), w1 = i8x8_to_bf16(q1);
+#pragma unroll
+        for (int i = 0; i < MT; ++i) {
+            float xs[8] = {xv[i][0].x, xv[i][0].y, xv[i][0].z, xv[i][0].w,
+                           xv[i][1].x, xv[i][1].y, xv[i][1].z, xv[i][1].w};
+            if (!mok[i]) {
+#pragma unroll
+                for (int j = 0; j < 8; ++j) xs[j] = 0.f;
+            } else if (xa.norm_w) {
+                const float r = s_rms[16 * i + mm];
+#pragma unroll
+                for (int j = 0; j < 8; ++j) xs[j] = xs[j] / r * nw[j];
+            }
+            const Bf16Pair a = split_bf16(xs);
+            const floatx4 z = {0.f, 0.f, 0.f, 0.f};
+            floatx4 t = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a.hi, w0, z, 0, 0, 0);
+            t = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a.lo, w0, t, 0, 0, 0);
+            acc[0][i] += d0 * t;
+            t = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a.hi, w1, z, 0, 0, 0);
+            t = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a.lo, w1, t, 0, 0, 0);
+            acc[1][i] += d1 * t;
+        }
+    }
+
+#pragma unroll
+    for (int i = 0; i < MT; ++i) {
+        s_part[wv][0][i][lane] = acc[0][i];
+        s_part[wv][1][i][lane] = acc[1][i];
+    }
+    __syncthreads();
+    if (wv < MT) {
+        const int i = wv;
+        floatx4 v0 = s_part[0][0][i][lane], v1 = s_part[0][1][i][lane];
+#pragma unroll
+        for (int w = 1; w < kGemmWaves; ++w) {
+            v0 += s_part[w][0][i][lane];
+            v1 += s_part[w][1][i][lane];
+        }
+        epi.apply(p, lane, t0 + 16 * i + 4 * kq, xa.T, v0, v1);
+    }
+}
+
+// ---------------------------------------------------------------- epilogues
+
+// y[m][row] (= or +=) for rows < rows; pair p = groups 2p, 2p+1.
+template <bool ADD>
+struct EpiStore {
+    float* y;
+    uint32_t ldy;
+    uint32_t rows;
+    __device__ __forceinline__ void groups(uint32_t p, uint32_t& g0, uint32_t& g1) const {
+        g0 = 2 * p;
+        g1 = 2 * p + 1;
+    }
+    __device__ __forceinline__ void apply(uint32_t p, int lane, uint32_t m0, uint32_t T, const floatx4& v0,
+                                          const floatx4& v1) const {
+        const uint32_t r0 = 32 * p + (lane & 15), r1 = r0 + 16;
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            const uint32_t m = m0 + r;
+            if (m >= T) break;
+            float* yr = y + static_cast<size_t>(m) * ldy;
+            if (r0 < rows) yr[r0] = ADD ? yr[r0] + v0[r] : v0[r];
+            if (r1 < rows) yr[r1] = ADD ? yr[r1] + v1[r] : v1[r];
+        }
+    }
+};
+
+// Gate and up projections packed as interleaved groups (2j: gate rows 16j..,
+// 2j+1: up rows 16j..): h[m][16p + lane%16] = silu(gate) * up, silu(g) =
+// g / (1 + exp(-g)) (src/model.rs:375-378).
+struct EpiSwiGLU {
+    float* h;
+    uint32_t ldh;
+    uint32_t inter;
+    __device__ __forceinline__ void groups(uint32_t p, uint32_t& g0, uint32_t& g1) const {
+        g0 = 2 * p;
+        g1 = 2 * p + 1;
+    }
+    __device__ __forceinline__ void apply(uint32_t p, int lane, uint32_t m0, uint32_t T, const floatx4& g,
+                                          const floatx4& u) const {
+        const uint32_t j = 16 * p + (lane & 15);
+        if (j >= inter) return;
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            const uint32_t m = m0 + r;
+            if (m >= T) break;
+            h[static_cast<size_t>(m) * ldh + j] = g[r] / (1.0f + expf(-g[r])) * u[r];
+        }
+    }
+};
+
+// Fused Q/K/V projection epilogue for head_dim 64: weights are the row
+// concatenation [Wq; Wk; Wv] (heads of 64 rows = 4 groups). Pair p = (head p/2,
+// half p%2) takes groups 4h + half and 4h + half + 2, i.e. dims d and d + 32 of
+// the head, the two halves rotate-half RoPE mixes (src/model.rs:720-737):
+//   [x1 cos - x2 sin, x1 sin + x2 cos] with cos/sin rows of the token's position.
+// Q heads go to q[m][h][64]; K heads (rotated) and V heads go straight into the
+// F32 pool row slot_mapping[m] (write_kv_slots, src/kv_cache/storage.rs:219-254).
+struct EpiQkvRope {
+    float* q;
+    float* k_pool;
+    float* v_pool;
+    const int32_t* positions;
+    const int64_t* slots;
+    const float* cos_t;  // [max_pos][32]
+    const float* sin_t;
+    uint32_t* status;
+    uint32_t num_heads, num_kv_heads, max_pos;
+    int64_t num_slots;
+    __device__ __forceinline__ void groups(uint32_t p, uint32_t& g0, uint32_t& g1) const {
+        g0 = 4 * (p / 2) + (p % 2);
+        g1 = g0 + 2;
+    }
+    __device__ __forceinline__ void apply(uint32_t p, int lane, uint32_t m0, uint32_t T, const floatx4& x1,
+                                          const floatx4& x2) const {
+        const uint32_t head = p / 2;
+        const uint32_t d = 16 * (p % 2) + (lane & 15);
+        const bool is_q = head < num_heads, is_v = head >= num_heads + num_kv_heads;
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            const uint32_t m = m0 + r;
+            if (m >= T) break;
+            float a = x1[r], b = x2[r];
+            if (!is_v) {
+                uint32_t pos = static_cast<uint32_t>(positions[m]);
+                if (pos >= max_pos) {
+                    raise_status(status, KANSO_DEV_POSITION_OOB);
+                    pos = max_pos - 1;
+                }
+                const float c = cos_t[static_cast<size_t>(pos) * 32 + d];
+                const float s = sin_t[static_cast<size_t>(pos) * 32 + d];
+                const float ra = a * c - b * s;
+                const float rb = a * s + b * c;
+                a = ra;
+                b = rb;
+            }
+            if (is_q) {
+                float* qr = q + (static_cast<size_t>(m) * num_heads + head) * 64;
+                qr[d] = a;
+                qr[d + 32] = b;
+                continue;
+            }
+            const int64_t slot = slots[m];
+            if (slot < 0 || slot >= num_slots) {
+                raise_status(status, KANSO_DEV_SLOT_OOB);
+                continue;
+            }
+            const uint32_t kvh = is_v ? head - num_heads - num_kv_heads : head - num_heads;
+            float* dst = (is_v ? v_pool : k_pool) + (static_cast<size_t>(slot) * num_kv_heads + kvh) * 64;
+            dst[d] = a;
+            dst[d + 32] = b;
+        }
+    }
+};
+
+// Orderable key of (value, index): larger value wins, then the smaller index
+// (greedy_token keeps the first maximum, src/sampler.rs:7-17). NaN never wins.
+__device__ __forceinline__ unsigned long long argmax_key(float v, uint32_t idx) {
+    const uint32_t b = __builtin_bit_cast(uint32_t, v);
+    const uint32_t ord = (b & 0x80000000u) ? ~b : (b | 0x80000000u);
+    return (static_cast<unsigned long long>(ord) << 32) | (0xffffffffu - idx);
+}
+
+// lm_head: optional logits store, and a per-token argmax folded into keys[m]
+// with a 64-bit atomic max (order-independent, so the result is deterministic).
+struct EpiArgmax {
+    float* logits;  // may be null
+    uint32_t ld;
+    uint32_t rows;
+    unsigned long long* keys;
+    __device__ __forceinline__ void groups(uint32_t p, uint32_t& g0, uint32_t& g1) const {
+        g0 = 2 * p;
+        g1 = 2 * p + 1;
+    }
+    __device__ __forceinline__ void apply(uint32_t p, int lane, uint32_t m0, uint32_t T, const floatx4& v0,
+                                          const floatx4& v1) const {
+        const uint32_t r0 = 32 * p + (lane & 15), r1 = r0 + 16;
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            const uint32_t m = m0 + r;
+            const bool live = m < T;
+            unsigned long long key = 0;
+            if (live && r0 < rows && !(v0[r] != v0[r])) key = argmax_key(v0[r], r0);
+            if (live && r1 < rows && !(v1[r] != v1[r])) key = max(key, argmax_key(v1[r], r1));
+            if (live && logits) {
+                float* lr = logits + static_cast<size_t>(m) * ld;
+                if (r0 < rows) lr[r0] = v0[r];
+                if (r1 < rows) lr[r1] = v1[r];
+            }
+            // max over the 16 lanes that hold this token (same lane / 16)
+#pragma unroll
+            for (int o = 1; o < 16; o <<= 1) {
+                const unsigned long long other = __shfl_xor(key, o, kWave);
+                key = max(key, other);
+            }
+            if (live && (lane & 15) == 0 && key != 0) atomicMax(keys + m, key);
+        }
+    }
+};
+
+// Launch helper: grid (pairs, token tiles); MT from the token count.
+template <class WL, class Epi>
+inline int launch_q8_gemm(const WL& wl, const XIn& xa, const Epi& epi, uint32_t pairs, hipStream_t s) {
+    if (xa.T == 0 || pairs == 0) return KANSO_OK;
+    if (xa.T <= 16) {
+        hipLaunchKernelGGL((q8_gemm_kernel<1, WL, Epi>), dim3(pairs, 1), dim3(kGemmThreads), 0, s, wl, xa, epi);
+    } else if (xa.T <= 32) {
+        hipLaunchKernelGGL((q8_gemm_kernel<2, WL, Epi>), dim3(pairs, 1), dim3(kGemmThreads), 0, s, wl, xa, epi);
+    } else {
+        hipLaunchKernelGGL((q8_gemm_kernel<4, WL, Epi>), dim3(pairs, (xa.T + 63) / 64), dim3(kGemmThreads), 0, s,
+                           wl, xa, epi);
+    }
+    KANSO_LAUNCH_CHECK();
+    return KANSO_OK;
+}
+
+}  // namespace kanso

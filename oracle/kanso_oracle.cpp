@@ -487,6 +487,15 @@ void oracle_gemv_q4_k_f32d(const void* w, const float* x, float* y, uint32_t row
         }
 }
 
+void oracle_dequant_row_q8_0(const void* blocks, uint32_t n, float* out) {
+    // BlockQ8_0::dequantize (src/quant/q8_0.rs:35-39): d * q per element.
+    const Q8Block16* b = static_cast<const Q8Block16*>(blocks);
+    for (uint32_t i = 0; i < n; ++i) {
+        const Q8Block16& blk = b[i / 32];
+        out[i] = oracle_f16_to_f32(blk.d) * static_cast<float>(blk.qs[i % 32]);
+    }
+}
+
 void oracle_quantize_row_q8_0(const float* x, uint32_t n, void* blocks) {
     Q8Block16* out = static_cast<Q8Block16*>(blocks);
     for (uint32_t b = 0; b < n / 32; ++b) {

@@ -110,6 +110,8 @@ void oracle_gemv_q4_k_f32d(const void* w, const float* x, float* y, uint32_t row
  * not available here: its bytes are "parity unpinned"; only dequantization and the
  * GEMV over given bytes are pinned. */
 void oracle_quantize_row_q8_0(const float* x, uint32_t n, void* blocks);
+/* BlockQ8_0::dequantize (src/quant/q8_0.rs:35-39) over n elements of GGUF blocks. */
+void oracle_dequant_row_q8_0(const void* blocks, uint32_t n, float* out);
 void oracle_quantize_row_q4_k(const float* x, uint32_t n, void* blocks);
 
 /* ---- decoder glue (config 5) -------------------------------------------- */

@@ -58,6 +58,7 @@ def lib() -> C.CDLL:
             "oracle_gemv_q4_k_f32d": (None, [V, V, V, U, U, U]),
             "oracle_quantize_row_q8_0": (None, [V, U, V]),
             "oracle_quantize_row_q4_k": (None, [V, U, V]),
+            "oracle_dequant_row_q8_0": (None, [V, U, V]),
             "oracle_rmsnorm": (None, [V, V, V, U, U, F]),
             "oracle_rope_table": (None, [U, U, F, V, V]),
             "oracle_rope_apply": (None, [V, U, U, U, V, V, V]),
@@ -193,6 +194,14 @@ def quantize_row_q8_0(x) -> np.ndarray:
     out = np.zeros(x.size // 32 * 34, dtype=np.uint8)
     lib().oracle_quantize_row_q8_0(_p(x), x.size, _p(out))
     return out
+
+
+def dequant_q8_0_rows(blocks: np.ndarray, cols: int) -> np.ndarray:
+    b = np.ascontiguousarray(blocks, dtype=np.uint8)
+    n = b.size // 34 * 32
+    out = np.zeros(n, np.float32)
+    lib().oracle_dequant_row_q8_0(_p(b), n, _p(out))
+    return out.reshape(-1, cols)
 
 
 def quantize_row_q4_k(x) -> np.ndarray:
