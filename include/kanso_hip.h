@@ -111,7 +111,8 @@ typedef struct {
     uint32_t q_len;        /* tokens this step: 1 for decode, chunk_len for prefill */
     uint32_t table_offset; /* first entry of this sequence's table in table_arena   */
     uint32_t table_len;    /* entries of the table                                  */
-    uint32_t token_offset; /* this sequence's token history starts at token_arena[token_offset] */
+    uint32_t token_offset; /* token at position pos is token_arena[token_offset + pos]
+                              (32-bit unsigned arithmetic)                           */
 } kanso_seq_plan;
 
 /* Device outputs of kanso_pack_step (all caller-owned device buffers). */
@@ -284,6 +285,145 @@ int kanso_gate_up_swiglu(kanso_ctx* ctx, const void* packed_gate_up, const float
 int kanso_lm_head_argmax(kanso_ctx* ctx, const void* packed, const float* x, const int32_t* rows,
                          const float* norm_w, float eps, uint32_t num_rows, uint32_t hidden,
                          uint32_t vocab, float* logits, uint32_t* tokens, kanso_stream_t stream);
+
+/* Q8_0 quantization of n f32 values (n % 32 == 0) into GGUF blocks, on the device:
+ * per 32 values d = amax / 127, id = d != 0 ? 1 / d : 0, q = round(x * id) clamped
+ * to [-128, 127] (BlockQ8_0::from_f32_slice, src/quant/q8_0.rs:13-32), d stored as
+ * f16 (round to nearest even). Bit-exact with the CPU rule. */
+int kanso_quantize_q8_0(kanso_ctx* ctx, const float* x, uint64_t n, void* gguf_out,
+                        kanso_stream_t stream);
+
+/* ---- the decoder model and the continuous-batching engine ----------------
+ *
+ * kanso_model: a llama decoder (RMSNorm, rotate-half RoPE, GQA attention, SwiGLU
+ * MLP) with packed Q8_0 projections and an F32 paged KV pool, all device
+ * resident — the Model of src/model.rs behind forward_batch (:1360-1380).
+ * kanso_engine: Engine::step (src/engine.rs:213-505) in C++ driving it. */
+
+typedef struct kanso_model kanso_model;
+typedef struct kanso_engine kanso_engine;
+
+typedef struct {
+    uint32_t hidden;
+    uint32_t num_heads;
+    uint32_t num_kv_heads;
+    uint32_t head_dim;      /* 64 */
+    uint32_t num_layers;
+    uint32_t intermediate;  /* multiple of 32 */
+    uint32_t vocab;
+    float eps;              /* RMSNorm epsilon (1e-5)                            */
+    float rope_theta;       /* 10000                                             */
+    uint32_t max_position;  /* RoPE table rows (positions 0 .. max_position-1)   */
+    uint32_t tied_embeddings; /* 1: lm_head is the embedding table              */
+} kanso_model_config;
+
+/* Weight kinds of kanso_model_set_weight. Matrices are GGUF Q8_0 bytes [rows][in/32]
+ * x 34 B; norms are f32 [hidden]. Per-layer kinds take the layer index. */
+enum {
+    KANSO_W_EMBED = 0,      /* [vocab][hidden]                 */
+    KANSO_W_LM_HEAD = 1,    /* [vocab][hidden] (untied only)   */
+    KANSO_W_FINAL_NORM = 2,
+    KANSO_W_ATTN_NORM = 3,
+    KANSO_W_FFN_NORM = 4,
+    KANSO_W_Q = 5,          /* [heads*64][hidden]              */
+    KANSO_W_K = 6,          /* [kv_heads*64][hidden]           */
+    KANSO_W_V = 7,
+    KANSO_W_O = 8,          /* [hidden][heads*64]              */
+    KANSO_W_GATE = 9,       /* [intermediate][hidden]          */
+    KANSO_W_UP = 10,
+    KANSO_W_DOWN = 11       /* [hidden][intermediate]          */
+};
+
+int kanso_model_create(kanso_ctx* ctx, const kanso_model_config* cfg, kanso_model** out);
+int kanso_model_destroy(kanso_model* model);
+
+/* Uploads one weight from host memory (bytes must match the kind's size) and
+ * re-lays matrices into the packed layout. */
+int kanso_model_set_weight(kanso_model* model, uint32_t kind, uint32_t layer,
+                           const void* host_data, size_t bytes);
+
+/* Random-init weights generated on the device: every matrix N(0, std^2) from this
+ * build's counter-based generator (splitmix64 + Box-Muller), quantized to Q8_0 by
+ * the rule of kanso_quantize_q8_0; norms = 1 (create_mock_*, src/model.rs:520-651,
+ * with SmolLM2's std of 0.02 in place of N(0,1)). */
+int kanso_model_init_random(kanso_model* model, uint64_t seed, float std);
+
+/* Allocates the F32 KV pool: num_blocks blocks of block_size tokens per layer, and
+ * step buffers for up to max_tokens rows and max_seqs sequences per forward. */
+int kanso_model_alloc_kv(kanso_model* model, uint32_t num_blocks, uint32_t block_size,
+                         uint32_t max_tokens, uint32_t max_seqs);
+
+/* Device pointers of layer `layer`'s K and V pools ([num_blocks][bs][kv_heads][64]). */
+int kanso_model_kv_pool(kanso_model* model, uint32_t layer, float** k_pool, float** v_pool);
+
+/* Copies the K and V rows of pool slots slots[0..n) of layer `layer` to host
+ * arrays k_out / v_out ([n][kv_heads][64] f32) (KvStorageKind::read_kv_token,
+ * src/kv_cache/kind.rs:400-411). Synchronous. */
+int kanso_model_read_kv_rows(kanso_model* model, uint32_t layer, const uint64_t* slots,
+                             uint32_t n, float* k_out, float* v_out);
+
+/* Erases blocks (host array) in every layer's K and V pool (allocate_zeroed,
+ * src/kv_cache/mod.rs:25-35). */
+int kanso_model_reset_blocks(kanso_model* model, const uint32_t* blocks, uint32_t num_blocks,
+                             kanso_stream_t stream);
+
+/* One batched forward (Model::forward_batch, src/model.rs:1360-1380) of a step
+ * given as a compact plan (host arrays, as for kanso_pack_step: token_offset + pos
+ * is taken modulo 2^32, so an arena holding only this step's tokens uses
+ * token_offset = arena_index - start_pos). Packs on the device, runs every layer,
+ * and writes next_tokens[s] (host) = greedy token of sequence s's last row;
+ * logits [S][vocab] (device) too when non-NULL. Synchronises `stream`. */
+int kanso_model_forward(kanso_model* model, const kanso_seq_plan* plan, uint32_t num_seqs,
+                        const uint32_t* token_arena, uint32_t token_arena_len,
+                        const uint32_t* table_arena, uint32_t table_arena_len, float* logits,
+                        uint32_t* next_tokens, kanso_stream_t stream);
+
+/* Engine::new_with_budget (src/engine.rs:46-125): a block pool of total_blocks,
+ * a prefix cache, max_running sequences, token_budget tokens per step. model may be
+ * NULL: the engine then plans and commits with a deterministic stand-in token
+ * (kanso_engine_dry_token) instead of a forward — the scheduler alone, for tests. */
+int kanso_engine_create(kanso_model* model, uint32_t max_running, uint32_t total_blocks,
+                        uint32_t block_size, uint32_t token_budget, uint32_t dry_vocab,
+                        kanso_engine** out);
+int kanso_engine_destroy(kanso_engine* engine);
+
+/* add_request_with_stops (src/engine.rs:138-170): returns the request id. */
+int kanso_engine_add_request(kanso_engine* engine, const uint32_t* prompt, uint32_t prompt_len,
+                             uint32_t max_tokens, const uint32_t* stop_ids, uint32_t num_stop,
+                             uint64_t* request_id);
+
+/* One StepOutput (src/engine.rs:11-16). */
+typedef struct {
+    uint64_t request_id;
+    uint32_t token_id;
+    uint32_t is_finished;
+} kanso_step_output;
+
+/* Engine::step (src/engine.rs:213-505): plan, one forward, commit, retire. Writes
+ * up to capacity outputs (in emit order) and their count. */
+int kanso_engine_step(kanso_engine* engine, kanso_step_output* outputs, uint32_t capacity,
+                      uint32_t* num_outputs);
+
+/* The flattened batch of the last step (engine.rs:376-402, before padding):
+ * counts into sizes[0..3] = {tokens, sequences, table entries, sample rows}; when
+ * the arrays are non-NULL they receive tokens/positions/slots [T], context_lens /
+ * query_lens [S], table_lens [S] and the concatenated tables, sample rows. */
+int kanso_engine_last_plan(kanso_engine* engine, uint32_t* sizes, uint32_t* tokens,
+                           uint32_t* positions, uint64_t* slots, uint32_t* context_lens,
+                           uint32_t* query_lens, uint32_t* table_lens, uint32_t* tables,
+                           uint32_t* sample_rows);
+
+/* Counters: {waiting, running, free blocks, unfinished, sequences, prefix hits,
+ * prefix lookups, prefix matched tokens, prompt tokens admitted, steps}. */
+int kanso_engine_stats(kanso_engine* engine, uint64_t* stats10);
+
+/* cancel_request (src/engine.rs:516-531); *found = 0 when no such request is live. */
+int kanso_engine_cancel(kanso_engine* engine, uint64_t request_id, uint32_t* found);
+/* drain_finished (src/engine.rs:511-515). */
+int kanso_engine_drain_finished(kanso_engine* engine, uint32_t* dropped);
+
+/* The stand-in token of the model-less engine for (request id, position). */
+uint32_t kanso_engine_dry_token(uint64_t request_id, uint32_t position, uint32_t vocab);
 
 /* Timing of the library's own kernels with HIP events on the launch stream.
  * When enabled, every launch of the named kernel is bracketed by events and the

@@ -99,6 +99,34 @@ class QkvParamsC(C.Structure):
     ]
 
 
+class ModelConfigC(C.Structure):
+    _fields_ = [
+        ("hidden", C.c_uint32),
+        ("num_heads", C.c_uint32),
+        ("num_kv_heads", C.c_uint32),
+        ("head_dim", C.c_uint32),
+        ("num_layers", C.c_uint32),
+        ("intermediate", C.c_uint32),
+        ("vocab", C.c_uint32),
+        ("eps", C.c_float),
+        ("rope_theta", C.c_float),
+        ("max_position", C.c_uint32),
+        ("tied_embeddings", C.c_uint32),
+    ]
+
+
+class StepOutputC(C.Structure):
+    _fields_ = [
+        ("request_id", C.c_uint64),
+        ("token_id", C.c_uint32),
+        ("is_finished", C.c_uint32),
+    ]
+
+
+KANSO_W_EMBED, KANSO_W_LM_HEAD, KANSO_W_FINAL_NORM, KANSO_W_ATTN_NORM, KANSO_W_FFN_NORM = range(5)
+KANSO_W_Q, KANSO_W_K, KANSO_W_V, KANSO_W_O, KANSO_W_GATE, KANSO_W_UP, KANSO_W_DOWN = range(5, 12)
+
+
 # Every symbol the header declares, with its signature.
 _P = C.c_void_p
 _U = C.c_uint32
@@ -127,6 +155,25 @@ SIGNATURES: dict[str, tuple] = {
                                    _P, _P]),
     "kanso_gate_up_swiglu": (_I, [_P, _P, _P, _P, C.c_float, _U, _U, _U, _P, _P]),
     "kanso_lm_head_argmax": (_I, [_P, _P, _P, _P, _P, C.c_float, _U, _U, _U, _P, _P, _P]),
+    "kanso_quantize_q8_0": (_I, [_P, _P, C.c_uint64, _P, _P]),
+    "kanso_model_create": (_I, [_P, C.POINTER(ModelConfigC), C.POINTER(_P)]),
+    "kanso_model_destroy": (_I, [_P]),
+    "kanso_model_set_weight": (_I, [_P, _U, _U, _P, C.c_size_t]),
+    "kanso_model_init_random": (_I, [_P, C.c_uint64, C.c_float]),
+    "kanso_model_alloc_kv": (_I, [_P, _U, _U, _U, _U]),
+    "kanso_model_kv_pool": (_I, [_P, _U, C.POINTER(_P), C.POINTER(_P)]),
+    "kanso_model_reset_blocks": (_I, [_P, _P, _U, _P]),
+    "kanso_model_read_kv_rows": (_I, [_P, _U, _P, _U, _P, _P]),
+    "kanso_model_forward": (_I, [_P, _P, _U, _P, _U, _P, _U, _P, _P, _P]),
+    "kanso_engine_create": (_I, [_P, _U, _U, _U, _U, _U, C.POINTER(_P)]),
+    "kanso_engine_destroy": (_I, [_P]),
+    "kanso_engine_add_request": (_I, [_P, _P, _U, _U, _P, _U, C.POINTER(C.c_uint64)]),
+    "kanso_engine_step": (_I, [_P, _P, _U, C.POINTER(_U)]),
+    "kanso_engine_last_plan": (_I, [_P, _P, _P, _P, _P, _P, _P, _P, _P, _P]),
+    "kanso_engine_stats": (_I, [_P, _P]),
+    "kanso_engine_cancel": (_I, [_P, C.c_uint64, C.POINTER(_U)]),
+    "kanso_engine_drain_finished": (_I, [_P, C.POINTER(_U)]),
+    "kanso_engine_dry_token": (_U, [C.c_uint64, _U, _U]),
     "kanso_set_profiling": (_I, [_P, _I]),
     "kanso_get_kernel_time": (_I, [_P, C.c_char_p, C.POINTER(C.c_double), C.POINTER(C.c_uint64)]),
 }

@@ -1,0 +1,595 @@
+// model.hip — the device-resident llama decoder: weight upload / random init,
+// the paged F32 KV pool, and one batched forward per engine step.
+//
+// Reference: Model (src/model.rs:177-194) and forward_batch_rows (:1418-1739) on
+// the mixed-batch arm, with every per-layer op replaced by the fused kernels of
+// decoder.hip and the ragged attention of attention.hip. A step is:
+//   pack (kanso_pack_step) -> embed -> per layer [RMSNorm+QKV+RoPE+KV write ->
+//   ragged attention -> O + residual -> RMSNorm+gate/up+SwiGLU -> down + residual]
+//   -> final RMSNorm + lm_head + greedy argmax on each sequence's last row.
+// All step inputs travel in one host-to-device copy from a pinned staging buffer;
+// the S sampled tokens come back in one device-to-host copy.
+#include <cmath>
+#include <cstring>
+
+#include "model.hpp"
+
+namespace kanso {
+namespace {
+
+__device__ __forceinline__ uint64_t splitmix64(uint64_t x) {
+    x += 0x9e3779b97f4a7c15ull;
+    x = (x ^ (x >> 30)) * 0xbf58476d1ce4e5b9ull;
+    x = (x ^ (x >> 27)) * 0x94d049bb133111ebull;
+    return x ^ (x >> 31);
+}
+
+// N(0, std^2) from one 64-bit hash: two 24-bit uniforms, Box-Muller cosine branch.
+__global__ void randn_kernel(float* out, uint64_t n, uint64_t seed, float std) {
+    for (uint64_t i = blockIdx.x * 256ull + threadIdx.x; i < n; i += static_cast<uint64_t>(gridDim.x) * 256) {
+        const uint64_t h = splitmix64(seed ^ (i * 0xd1342543de82ef95ull));
+        const float u1 = (static_cast<float>(h >> 40) + 1.0f) * (1.0f / 16777216.0f);
+        const float u2 = static_cast<float>(h & 0xffffff) * (1.0f / 16777216.0f);
+        out[i] = std * sqrtf(-2.0f * logf(u1)) * cosf(6.283185307179586f * u2);
+    }
+}
+
+// BlockQ8_0::from_f32_slice (src/quant/q8_0.rs:13-32), one thread per block:
+// amax, d = amax / 127, id = 1 / d (0 when d == 0), q = round(x * id) clamped,
+// d stored as f16 (round to nearest even). Every step is one IEEE operation, so
+// the bytes equal the CPU rule's.
+__global__ void quantize_q8_0_kernel(const float* __restrict__ x, uint64_t nblocks, uint8_t* __restrict__ out) {
+    for (uint64_t b = blockIdx.x * 256ull + threadIdx.x; b < nblocks; b += static_cast<uint64_t>(gridDim.x) * 256) {
+        const float* xb = x + b * 32;
+        float amax = 0.f;
+        for (int i = 0; i < 32; ++i) amax = fmaxf(amax, fabsf(xb[i]));
+        const float d = amax / 127.0f;
+        const float id = d != 0.f ? 1.0f / d : 0.f;
+        uint8_t* ob = out + b * 34;
+        const uint16_t dh = __half_as_ushort(__float2half_rn(d));
+        ob[0] = static_cast<uint8_t>(dh & 0xff);
+        ob[1] = static_cast<uint8_t>(dh >> 8);
+        for (int i = 0; i < 32; ++i) {
+            const float r = roundf(xb[i] * id);
+            ob[2 + i] = static_cast<uint8_t>(static_cast<int8_t>(fminf(fmaxf(r, -128.0f), 127.0f)));
+        }
+    }
+}
+
+__global__ void fill_f32_kernel(float* p, uint64_t n, float v) {
+    for (uint64_t i = blockIdx.x * 256ull + threadIdx.x; i < n; i += static_cast<uint64_t>(gridDim.x) * 256) p[i] = v;
+}
+
+// Zeroes block blocks[i] of every layer's K and V pool: one float4 per thread.
+__global__ void reset_blocks_kernel(float* k, float* v, const uint32_t* blocks, uint32_t n, uint32_t layers,
+                                    size_t layer_elems, uint32_t block_elems, uint32_t num_blocks) {
+    const uint64_t per_block = block_elems / 4;
+    const uint64_t total = static_cast<uint64_t>(n) * layers * per_block;
+    for (uint64_t e = blockIdx.x * 256ull + threadIdx.x; e < total; e += static_cast<uint64_t>(gridDim.x) * 256) {
+        const uint32_t i = static_cast<uint32_t>(e / (layers * per_block));
+        const uint32_t l = static_cast<uint32_t>((e / per_block) % layers);
+        const uint64_t c = e % per_block;
+        const uint32_t blk = blocks[i];
+        if (blk >= num_blocks) continue;
+        const size_t off = l * layer_elems + static_cast<size_t>(blk) * block_elems + 4 * c;
+        *reinterpret_cast<float4*>(k + off) = make_float4(0.f, 0.f, 0.f, 0.f);
+        *reinterpret_cast<float4*>(v + off) = make_float4(0.f, 0.f, 0.f, 0.f);
+    }
+}
+
+uint32_t grid_for(uint64_t n) { return static_cast<uint32_t>(std::min<uint64_t>((n + 255) / 256, 8192)); }
+
+template <class T>
+int dev_alloc(kanso_model* m, T** p, size_t bytes) {
+    void* q = nullptr;
+    KANSO_HIP_TRY(hipMalloc(&q, std::max<size_t>(bytes, 256)));
+    m->allocations.push_back(q);
+    *p = static_cast<T*>(q);
+    return KANSO_OK;
+}
+
+int model_check(kanso_model* m, const char* who) {
+    if (!m) {
+        set_error("%s: null model", who);
+        return KANSO_E_INVALID_ARG;
+    }
+    return KANSO_OK;
+}
+
+// Packed buffer of the fused Q/K/V matrix.
+size_t qkv_rows(const kanso_model_config& c) { return static_cast<size_t>(c.num_heads + 2 * c.num_kv_heads) * 64; }
+
+int alloc_weights(kanso_model* m) {
+    const kanso_model_config& c = m->cfg;
+    int rc;
+    m->layers.resize(c.num_layers);
+    for (auto& L : m->layers) {
+        if ((rc = dev_alloc(m, &L.qkv, kanso_q8_0_packed_bytes(qkv_rows(c), c.hidden)))) return rc;
+        if ((rc = dev_alloc(m, &L.o, kanso_q8_0_packed_bytes(c.hidden, c.num_heads * 64)))) return rc;
+        if ((rc = dev_alloc(m, &L.gate_up, kanso_q8_0_packed_bytes(2 * c.intermediate, c.hidden)))) return rc;
+        if ((rc = dev_alloc(m, &L.down, kanso_q8_0_packed_bytes(c.hidden, c.intermediate)))) return rc;
+        if ((rc = dev_alloc(m, &L.attn_norm, c.hidden * sizeof(float)))) return rc;
+        if ((rc = dev_alloc(m, &L.ffn_norm, c.hidden * sizeof(float)))) return rc;
+        KANSO_HIP_TRY(hipMemset(L.qkv, 0, kanso_q8_0_packed_bytes(qkv_rows(c), c.hidden)));
+        KANSO_HIP_TRY(hipMemset(L.gate_up, 0, kanso_q8_0_packed_bytes(2 * c.intermediate, c.hidden)));
+    }
+    if ((rc = dev_alloc(m, &m->embed, kanso_q8_0_packed_bytes(c.vocab, c.hidden)))) return rc;
+    if (c.tied_embeddings) {
+        m->lm_head = m->embed;
+    } else if ((rc = dev_alloc(m, &m->lm_head, kanso_q8_0_packed_bytes(c.vocab, c.hidden)))) {
+        return rc;
+    }
+    if ((rc = dev_alloc(m, &m->final_norm, c.hidden * sizeof(float)))) return rc;
+    // RoPE table on the host with the reference's f32 arithmetic (build_rope_table,
+    // src/model.rs:698-718): theta_j = base^(-2j/D), angle = pos * theta_j.
+    const uint32_t half = c.head_dim / 2;
+    std::vector<float> theta(half), cs(static_cast<size_t>(c.max_position) * half), sn(cs.size());
+    for (uint32_t j = 0; j < half; ++j)
+        theta[j] = std::pow(c.rope_theta, -2.0f * static_cast<float>(j) / static_cast<float>(c.head_dim));
+    for (uint32_t p = 0; p < c.max_position; ++p)
+        for (uint32_t j = 0; j < half; ++j) {
+            const float a = static_cast<float>(p) * theta[j];
+            cs[static_cast<size_t>(p) * half + j] = std::cos(a);
+            sn[static_cast<size_t>(p) * half + j] = std::sin(a);
+        }
+    if ((rc = dev_alloc(m, &m->cos_t, cs.size() * sizeof(float)))) return rc;
+    if ((rc = dev_alloc(m, &m->sin_t, sn.size() * sizeof(float)))) return rc;
+    KANSO_HIP_TRY(hipMemcpy(m->cos_t, cs.data(), cs.size() * sizeof(float), hipMemcpyHostToDevice));
+    KANSO_HIP_TRY(hipMemcpy(m->sin_t, sn.data(), sn.size() * sizeof(float), hipMemcpyHostToDevice));
+    return KANSO_OK;
+}
+
+// Destination of a matrix kind: packed buffer, rows, in-features, group stride and
+// offset in that buffer.
+struct MatrixSlot {
+    uint8_t* dst;
+    uint32_t rows, in, stride, offset;
+};
+
+bool matrix_slot(kanso_model* m, uint32_t kind, uint32_t layer, MatrixSlot& ms) {
+    const kanso_model_config& c = m->cfg;
+    if (kind == KANSO_W_EMBED) {
+        ms = {m->embed, c.vocab, c.hidden, 1, 0};
+        return true;
+    }
+    if (kind == KANSO_W_LM_HEAD) {
+        ms = {m->lm_head, c.vocab, c.hidden, 1, 0};
+        return true;
+    }
+    if (layer >= c.num_layers) return false;
+    auto& L = m->layers[layer];
+    switch (kind) {
+        case KANSO_W_Q: ms = {L.qkv, c.num_heads * 64, c.hidden, 1, 0}; return true;
+        case KANSO_W_K: ms = {L.qkv, c.num_kv_heads * 64, c.hidden, 1, 4 * c.num_heads}; return true;
+        case KANSO_W_V:
+            ms = {L.qkv, c.num_kv_heads * 64, c.hidden, 1, 4 * (c.num_heads + c.num_kv_heads)};
+            return true;
+        case KANSO_W_O: ms = {L.o, c.hidden, c.num_heads * 64, 1, 0}; return true;
+        case KANSO_W_GATE: ms = {L.gate_up, c.intermediate, c.hidden, 2, 0}; return true;
+        case KANSO_W_UP: ms = {L.gate_up, c.intermediate, c.hidden, 2, 1}; return true;
+        case KANSO_W_DOWN: ms = {L.down, c.hidden, c.intermediate, 1, 0}; return true;
+        default: return false;
+    }
+}
+
+float* norm_slot(kanso_model* m, uint32_t kind, uint32_t layer) {
+    if (kind == KANSO_W_FINAL_NORM) return m->final_norm;
+    if (layer >= m->cfg.num_layers) return nullptr;
+    if (kind == KANSO_W_ATTN_NORM) return m->layers[layer].attn_norm;
+    if (kind == KANSO_W_FFN_NORM) return m->layers[layer].ffn_norm;
+    return nullptr;
+}
+
+int ensure_step_buffers(kanso_model* m, uint32_t T, uint32_t S, uint32_t tables, uint32_t arena) {
+    const kanso_model_config& c = m->cfg;
+    int rc;
+    if (T > m->cap_tokens || S > m->cap_seqs) {
+        const uint32_t t = std::max(T, m->cap_tokens), sq = std::max(S, m->cap_seqs);
+        if ((rc = dev_alloc(m, &m->hidden, static_cast<size_t>(t) * c.hidden * 4))) return rc;
+        if ((rc = dev_alloc(m, &m->q, static_cast<size_t>(t) * c.num_heads * 64 * 4))) return rc;
+        if ((rc = dev_alloc(m, &m->attn, static_cast<size_t>(t) * c.num_heads * 64 * 4))) return rc;
+        if ((rc = dev_alloc(m, &m->act, static_cast<size_t>(t) * c.intermediate * 4))) return rc;
+        if ((rc = dev_alloc(m, &m->cu, (sq + 1) * 4ull))) return rc;
+        if ((rc = dev_alloc(m, &m->seq_of_query, t * 4ull))) return rc;
+        if ((rc = dev_alloc(m, &m->positions, t * 4ull))) return rc;
+        if ((rc = dev_alloc(m, &m->slots, t * 8ull))) return rc;
+        if ((rc = dev_alloc(m, &m->tokens, t * 4ull))) return rc;
+        if ((rc = dev_alloc(m, &m->ctx_lens, sq * 4ull))) return rc;
+        if ((rc = dev_alloc(m, &m->next, sq * 4ull))) return rc;
+        void* h = nullptr;
+        KANSO_HIP_TRY(hipHostMalloc(&h, sq * 4ull));
+        if (m->h_next) (void)hipHostFree(m->h_next);
+        m->h_next = static_cast<uint32_t*>(h);
+        m->cap_tokens = t;
+        m->cap_seqs = sq;
+    }
+    if (tables > m->cap_tables) {
+        if ((rc = dev_alloc(m, &m->tables, static_cast<size_t>(tables) * 4))) return rc;
+        m->cap_tables = tables;
+    }
+    const size_t need = align_up(static_cast<size_t>(S) * sizeof(kanso_seq_plan), 256) +
+                        align_up(static_cast<size_t>(arena) * 4, 256) + align_up(static_cast<size_t>(S) * 4, 256);
+    if (need > m->stage_bytes) {
+        const size_t want = align_up(need + need / 2, 1 << 16);
+        if ((rc = dev_alloc(m, &m->d_stage, want))) return rc;
+        void* h = nullptr;
+        KANSO_HIP_TRY(hipHostMalloc(&h, want));
+        if (m->h_stage) (void)hipHostFree(m->h_stage);
+        m->h_stage = h;
+        m->stage_bytes = want;
+    }
+    return KANSO_OK;
+}
+
+}  // namespace
+
+int model_reset_blocks(kanso_model* m, const uint32_t* blocks, uint32_t n, hipStream_t s) {
+    if (n == 0) return KANSO_OK;
+    if (!m->k_pool) {
+        set_error("kanso_model_reset_blocks: KV pool not allocated");
+        return KANSO_E_INVALID_ARG;
+    }
+    int rc;
+    if (n > m->cap_reset) {
+        if ((rc = dev_alloc(m, &m->d_reset, n * 4ull))) return rc;
+        m->cap_reset = n;
+    }
+    // The list is tiny; a synchronous copy keeps the host array's lifetime simple.
+    KANSO_HIP_TRY(hipMemcpyAsync(m->d_reset, blocks, n * 4ull, hipMemcpyHostToDevice, s));
+    const uint32_t block_elems = m->block_size * m->cfg.num_kv_heads * m->cfg.head_dim;
+    const uint64_t total = static_cast<uint64_t>(n) * m->cfg.num_layers * (block_elems / 4);
+    hipLaunchKernelGGL(reset_blocks_kernel, dim3(grid_for(total)), dim3(256), 0, s, m->k_pool, m->v_pool,
+                       m->d_reset, n, m->cfg.num_layers, m->layer_pool_elems, block_elems, m->num_blocks);
+    KANSO_LAUNCH_CHECK();
+    KANSO_HIP_TRY(hipStreamSynchronize(s));
+    return KANSO_OK;
+}
+
+int model_forward(kanso_model* m, const HostStep& step, float* logits, uint32_t* next, hipStream_t s) {
+    const kanso_model_config& c = m->cfg;
+    const uint32_t S = static_cast<uint32_t>(step.plan.size());
+    if (S == 0) {
+        set_error("forward_batch: empty batch");
+        return KANSO_E_INVALID_SHAPE;
+    }
+    if (!m->k_pool) {
+        set_error("forward_batch: KV pool not allocated (kanso_model_alloc_kv)");
+        return KANSO_E_INVALID_ARG;
+    }
+    // Shapes from the plan (PaddedDecodeTables::new, src/model.rs:84-88).
+    uint32_t T = 0, max_blocks = 1, max_q = 0;
+    for (const auto& p : step.plan) {
+        if (p.q_len == 0) {
+            set_error("forward_batch: a sequence has query_len 0");
+            return KANSO_E_INVALID_SHAPE;
+        }
+        T += p.q_len;
+        max_q = std::max(max_q, p.q_len);
+        const uint32_t ctx = p.start_pos + p.q_len;
+        if (ctx > c.max_position) {
+            set_error("forward_batch: context %u beyond the RoPE table (%u positions)", ctx, c.max_position);
+            return KANSO_E_OUT_OF_BOUNDS;
+        }
+        max_blocks = std::max(max_blocks, std::max((ctx + m->block_size - 1) / m->block_size, 1u));
+    }
+    int rc = ensure_step_buffers(m, T, S, S * max_blocks, static_cast<uint32_t>(step.token_arena.size() +
+                                                                                   step.table_arena.size()));
+    if (rc) return rc;
+    // Stage: plan | token arena + table arena | last rows.
+    char* h = static_cast<char*>(m->h_stage);
+    const size_t off_arena = align_up(S * sizeof(kanso_seq_plan), 256);
+    const size_t arena_n = step.token_arena.size() + step.table_arena.size();
+    const size_t off_last = off_arena + align_up(arena_n * 4, 256);
+    std::memcpy(h, step.plan.data(), S * sizeof(kanso_seq_plan));
+    std::memcpy(h + off_arena, step.token_arena.data(), step.token_arena.size() * 4);
+    std::memcpy(h + off_arena + step.token_arena.size() * 4, step.table_arena.data(), step.table_arena.size() * 4);
+    int32_t* last = reinterpret_cast<int32_t*>(h + off_last);
+    int32_t run = 0;
+    for (uint32_t i = 0; i < S; ++i) {
+        run += static_cast<int32_t>(step.plan[i].q_len);
+        last[i] = run - 1;
+    }
+    KANSO_HIP_TRY(hipMemcpyAsync(m->d_stage, h, off_last + S * 4, hipMemcpyHostToDevice, s));
+    char* d = static_cast<char*>(m->d_stage);
+    const auto* d_plan = reinterpret_cast<const kanso_seq_plan*>(d);
+    const auto* d_tok_arena = reinterpret_cast<const uint32_t*>(d + off_arena);
+    const auto* d_tab_arena = d_tok_arena + step.token_arena.size();
+    const auto* d_last = reinterpret_cast<const int32_t*>(d + off_last);
+
+    kanso_packed_step packed{m->cu, m->seq_of_query, m->positions, m->slots, m->tokens, m->tables, m->ctx_lens};
+    if ((rc = kanso_pack_step(m->ctx, d_plan, S, d_tok_arena, d_tab_arena, m->block_size, max_blocks, T, &packed,
+                              reinterpret_cast<kanso_stream_t>(s))))
+        return rc;
+    if ((rc = op_embed(m->ctx, m->embed, c.vocab, c.hidden, m->tokens, T, m->hidden, s))) return rc;
+
+    kanso_qkv_params qp{T, c.hidden, c.num_heads, c.num_kv_heads, 64, c.max_position, c.eps, m->num_blocks,
+                        m->block_size};
+    kanso_ragged_attention_params ap{};
+    ap.num_seqs = S;
+    ap.num_heads = c.num_heads;
+    ap.num_kv_heads = c.num_kv_heads;
+    ap.head_dim = c.head_dim;
+    ap.block_size = m->block_size;
+    ap.max_num_blocks_per_seq = max_blocks;
+    ap.scale = static_cast<float>(1.0 / std::sqrt(static_cast<double>(c.head_dim)));  // src/model.rs:757-762
+    ap.total_q = T;
+    ap.kv_dtype = KANSO_KV_F32;
+    ap.num_blocks = m->num_blocks;
+    ap.max_q_len = max_q;
+    const uint32_t qd = c.num_heads * 64;
+    for (uint32_t l = 0; l < c.num_layers; ++l) {
+        const auto& L = m->layers[l];
+        float* kp = m->k_pool + l * m->layer_pool_elems;
+        float* vp = m->v_pool + l * m->layer_pool_elems;
+        if ((rc = op_qkv_rope_append(m->ctx, &qp, L.qkv, m->hidden, L.attn_norm, m->positions, m->slots, m->cos_t,
+                                     m->sin_t, m->q, kp, vp, s)))
+            return rc;
+        if ((rc = kanso_ragged_paged_attention(m->ctx, &ap, m->q, kp, vp, nullptr, nullptr, m->tables,
+                                               m->cu, m->ctx_lens, m->attn, reinterpret_cast<kanso_stream_t>(s))))
+            return rc;
+        if ((rc = op_gemm_residual(L.o, m->attn, m->hidden, c.hidden, qd, T, s))) return rc;
+        if ((rc = op_gate_up_swiglu(L.gate_up, m->hidden, L.ffn_norm, c.eps, T, c.hidden, c.intermediate, m->act,
+                                    s)))
+            return rc;
+        if ((rc = op_gemm_residual(L.down, m->act, m->hidden, c.hidden, c.intermediate, T, s))) return rc;
+    }
+    if ((rc = op_lm_head_argmax(m->ctx, m->lm_head, m->hidden, d_last, m->final_norm, c.eps, S, c.hidden, c.vocab,
+                                logits, m->next, s)))
+        return rc;
+    KANSO_HIP_TRY(hipMemcpyAsync(m->h_next, m->next, S * 4ull, hipMemcpyDeviceToHost, s));
+    KANSO_HIP_TRY(hipStreamSynchronize(s));
+    std::memcpy(next, m->h_next, S * 4ull);
+    ++m->forward_calls;
+    return KANSO_OK;
+}
+
+}  // namespace kanso
+
+using namespace kanso;
+
+extern "C" {
+
+int kanso_quantize_q8_0(kanso_ctx* ctx, const float* x, uint64_t n, void* gguf_out, kanso_stream_t stream) {
+    if (!ctx || !x || !gguf_out) {
+        set_error("kanso_quantize_q8_0: null argument");
+        return KANSO_E_INVALID_ARG;
+    }
+    if (n == 0 || n % 32 != 0) {
+        set_error("kanso_quantize_q8_0: n %llu must be a non-zero multiple of 32", static_cast<unsigned long long>(n));
+        return KANSO_E_INVALID_SHAPE;
+    }
+    hipLaunchKernelGGL(quantize_q8_0_kernel, dim3(grid_for(n / 32)), dim3(256), 0, as_stream(stream), x, n / 32,
+                       static_cast<uint8_t*>(gguf_out));
+    KANSO_LAUNCH_CHECK();
+    return KANSO_OK;
+}
+
+int kanso_model_create(kanso_ctx* ctx, const kanso_model_config* cfg, kanso_model** out) {
+    if (!ctx || !cfg || !out) {
+        set_error("kanso_model_create: null argument");
+        return KANSO_E_INVALID_ARG;
+    }
+    *out = nullptr;
+    const kanso_model_config& c = *cfg;
+    if (c.head_dim != 64 || c.num_heads == 0 || c.num_kv_heads == 0 || c.num_heads % c.num_kv_heads != 0 ||
+        c.num_heads / c.num_kv_heads > 8 || c.hidden == 0 || c.hidden % 32 != 0 || c.intermediate == 0 ||
+        c.intermediate % 32 != 0 || c.vocab == 0 || c.num_layers == 0 || c.max_position == 0) {
+        set_error("kanso_model_create: unsupported shape (head_dim %u must be 64; hidden %u and intermediate %u "
+                  "multiples of 32; heads %u / kv heads %u with group <= 8)",
+                  c.head_dim, c.hidden, c.intermediate, c.num_heads, c.num_kv_heads);
+        return KANSO_E_INVALID_SHAPE;
+    }
+    KANSO_HIP_TRY(hipSetDevice(ctx->device));
+    auto* m = new kanso_model();
+    m->ctx = ctx;
+    m->cfg = c;
+    int rc = alloc_weights(m);
+    if (rc) {
+        kanso_model_destroy(m);
+        return rc;
+    }
+    *out = m;
+    return KANSO_OK;
+}
+
+int kanso_model_destroy(kanso_model* m) {
+    if (!m) return KANSO_OK;
+    (void)hipDeviceSynchronize();
+    for (void* p : m->allocations) (void)hipFree(p);
+    if (m->h_stage) (void)hipHostFree(m->h_stage);
+    if (m->h_next) (void)hipHostFree(m->h_next);
+    delete m;
+    return KANSO_OK;
+}
+
+int kanso_model_set_weight(kanso_model* m, uint32_t kind, uint32_t layer, const void* host_data, size_t bytes) {
+    int rc = model_check(m, "kanso_model_set_weight");
+    if (rc) return rc;
+    if (!host_data) {
+        set_error("kanso_model_set_weight: null data");
+        return KANSO_E_INVALID_ARG;
+    }
+    if (float* nw = norm_slot(m, kind, layer)) {
+        if (bytes != m->cfg.hidden * sizeof(float)) {
+            set_error("kanso_model_set_weight: norm of %zu bytes, expected %zu", bytes, m->cfg.hidden * sizeof(float));
+            return KANSO_E_INVALID_SHAPE;
+        }
+        KANSO_HIP_TRY(hipMemcpy(nw, host_data, bytes, hipMemcpyHostToDevice));
+        return KANSO_OK;
+    }
+    MatrixSlot ms;
+    if ((kind == KANSO_W_LM_HEAD && m->cfg.tied_embeddings) || !matrix_slot(m, kind, layer, ms)) {
+        set_error("kanso_model_set_weight: kind %u / layer %u not a weight of this model", kind, layer);
+        return KANSO_E_INVALID_ARG;
+    }
+    const size_t want = static_cast<size_t>(ms.rows) * (ms.in / 32) * 34;
+    if (bytes != want) {
+        set_error("kanso_model_set_weight: kind %u has %zu bytes, expected %zu (GGUF Q8_0 [%u][%u])", kind, bytes,
+                  want, ms.rows, ms.in);
+        return KANSO_E_INVALID_SHAPE;
+    }
+    void* tmp = nullptr;
+    KANSO_HIP_TRY(hipMalloc(&tmp, bytes));
+    hipError_t e = hipMemcpy(tmp, host_data, bytes, hipMemcpyHostToDevice);
+    if (e == hipSuccess) {
+        rc = kanso_q8_0_pack(m->ctx, tmp, ms.rows, ms.in, ms.dst, ms.stride, ms.offset, nullptr);
+        e = hipDeviceSynchronize();
+    }
+    (void)hipFree(tmp);
+    if (e != hipSuccess) {
+        set_error("kanso_model_set_weight: %s", hipGetErrorString(e));
+        return KANSO_E_HIP;
+    }
+    return rc;
+}
+
+int kanso_model_init_random(kanso_model* m, uint64_t seed, float std) {
+    int rc = model_check(m, "kanso_model_init_random");
+    if (rc) return rc;
+    const kanso_model_config& c = m->cfg;
+    size_t max_elems = static_cast<size_t>(c.vocab) * c.hidden;
+    max_elems = std::max(max_elems, static_cast<size_t>(c.intermediate) * c.hidden);
+    float* f = nullptr;
+    uint8_t* g = nullptr;
+    KANSO_HIP_TRY(hipMalloc(&f, max_elems * 4));
+    if (hipMalloc(&g, max_elems / 32 * 34) != hipSuccess) {
+        (void)hipFree(f);
+        set_error("kanso_model_init_random: out of device memory");
+        return KANSO_E_HIP;
+    }
+    uint64_t stream_id = 0;
+    auto one = [&](uint32_t kind, uint32_t layer) -> int {
+        MatrixSlot ms;
+        if (!matrix_slot(m, kind, layer, ms)) return KANSO_E_INVALID_ARG;
+        const uint64_t n = static_cast<uint64_t>(ms.rows) * ms.in;
+        const uint64_t sd = seed * 0x100000001b3ull + (++stream_id) * 0x9e3779b97f4a7c15ull;
+        hipLaunchKernelGGL(randn_kernel, dim3(grid_for(n)), dim3(256), 0, nullptr, f, n, sd, std);
+        hipLaunchKernelGGL(quantize_q8_0_kernel, dim3(grid_for(n / 32)), dim3(256), 0, nullptr, f, n / 32, g);
+        KANSO_LAUNCH_CHECK();
+        return kanso_q8_0_pack(m->ctx, g, ms.rows, ms.in, ms.dst, ms.stride, ms.offset, nullptr);
+    };
+    rc = one(KANSO_W_EMBED, 0);
+    if (!rc && !c.tied_embeddings) rc = one(KANSO_W_LM_HEAD, 0);
+    for (uint32_t l = 0; l < c.num_layers && !rc; ++l)
+        for (uint32_t kind : {KANSO_W_Q, KANSO_W_K, KANSO_W_V, KANSO_W_O, KANSO_W_GATE, KANSO_W_UP, KANSO_W_DOWN})
+            if (!rc) rc = one(kind, l);
+    if (!rc) {
+        auto ones = [&](float* p) {
+            hipLaunchKernelGGL(fill_f32_kernel, dim3(grid_for(c.hidden)), dim3(256), 0, nullptr, p,
+                               static_cast<uint64_t>(c.hidden), 1.0f);
+        };
+        ones(m->final_norm);
+        for (auto& L : m->layers) {
+            ones(L.attn_norm);
+            ones(L.ffn_norm);
+        }
+    }
+    const hipError_t e = hipDeviceSynchronize();
+    (void)hipFree(f);
+    (void)hipFree(g);
+    if (!rc && e != hipSuccess) {
+        set_error("kanso_model_init_random: %s", hipGetErrorString(e));
+        return KANSO_E_HIP;
+    }
+    return rc;
+}
+
+int kanso_model_alloc_kv(kanso_model* m, uint32_t num_blocks, uint32_t block_size, uint32_t max_tokens,
+                         uint32_t max_seqs) {
+    int rc = model_check(m, "kanso_model_alloc_kv");
+    if (rc) return rc;
+    if (m->k_pool) {
+        set_error("kanso_model_alloc_kv: KV pool already allocated");
+        return KANSO_E_INVALID_ARG;
+    }
+    if (num_blocks == 0 || block_size == 0 || (block_size & (block_size - 1)) != 0 || max_tokens == 0 ||
+        max_seqs == 0) {
+        set_error("kanso_model_alloc_kv: num_blocks %u, block_size %u (power of two), max_tokens %u, max_seqs %u",
+                  num_blocks, block_size, max_tokens, max_seqs);
+        return KANSO_E_INVALID_SHAPE;
+    }
+    m->num_blocks = num_blocks;
+    m->block_size = block_size;
+    m->layer_pool_elems = static_cast<size_t>(num_blocks) * block_size * m->cfg.num_kv_heads * m->cfg.head_dim;
+    const size_t bytes = m->layer_pool_elems * m->cfg.num_layers * sizeof(float);
+    if ((rc = dev_alloc(m, &m->k_pool, bytes))) return rc;
+    if ((rc = dev_alloc(m, &m->v_pool, bytes))) return rc;
+    KANSO_HIP_TRY(hipMemset(m->k_pool, 0, bytes));
+    KANSO_HIP_TRY(hipMemset(m->v_pool, 0, bytes));
+    return ensure_step_buffers(m, max_tokens, max_seqs, max_seqs * 64, max_tokens + max_seqs * 64);
+}
+
+int kanso_model_kv_pool(kanso_model* m, uint32_t layer, float** k_pool, float** v_pool) {
+    int rc = model_check(m, "kanso_model_kv_pool");
+    if (rc) return rc;
+    if (!m->k_pool || layer >= m->cfg.num_layers) {
+        set_error("kanso_model_kv_pool: no pool for layer %u", layer);
+        return KANSO_E_INVALID_ARG;
+    }
+    if (k_pool) *k_pool = m->k_pool + layer * m->layer_pool_elems;
+    if (v_pool) *v_pool = m->v_pool + layer * m->layer_pool_elems;
+    return KANSO_OK;
+}
+
+int kanso_model_read_kv_rows(kanso_model* m, uint32_t layer, const uint64_t* slots, uint32_t n, float* k_out,
+                             float* v_out) {
+    int rc = model_check(m, "kanso_model_read_kv_rows");
+    if (rc) return rc;
+    if (!m->k_pool || layer >= m->cfg.num_layers || (n && (!slots || !k_out || !v_out))) {
+        set_error("kanso_model_read_kv_rows: no pool for layer %u or null argument", layer);
+        return KANSO_E_INVALID_ARG;
+    }
+    const size_t row = static_cast<size_t>(m->cfg.num_kv_heads) * m->cfg.head_dim;
+    const uint64_t num_slots = static_cast<uint64_t>(m->num_blocks) * m->block_size;
+    KANSO_HIP_TRY(hipDeviceSynchronize());
+    for (uint32_t i = 0; i < n; ++i) {
+        if (slots[i] >= num_slots) {
+            set_error("kanso_model_read_kv_rows: slot %llu outside %llu slots",
+                      static_cast<unsigned long long>(slots[i]), static_cast<unsigned long long>(num_slots));
+            return KANSO_E_OUT_OF_BOUNDS;
+        }
+        const size_t off = layer * m->layer_pool_elems + slots[i] * row;
+        KANSO_HIP_TRY(hipMemcpy(k_out + i * row, m->k_pool + off, row * 4, hipMemcpyDeviceToHost));
+        KANSO_HIP_TRY(hipMemcpy(v_out + i * row, m->v_pool + off, row * 4, hipMemcpyDeviceToHost));
+    }
+    return KANSO_OK;
+}
+
+int kanso_model_reset_blocks(kanso_model* m, const uint32_t* blocks, uint32_t n, kanso_stream_t stream) {
+    int rc = model_check(m, "kanso_model_reset_blocks");
+    if (rc) return rc;
+    if (n && !blocks) {
+        set_error("kanso_model_reset_blocks: null block list");
+        return KANSO_E_INVALID_ARG;
+    }
+    return model_reset_blocks(m, blocks, n, as_stream(stream));
+}
+
+int kanso_model_forward(kanso_model* m, const kanso_seq_plan* plan, uint32_t num_seqs, const uint32_t* token_arena,
+                        uint32_t token_arena_len, const uint32_t* table_arena, uint32_t table_arena_len,
+                        float* logits, uint32_t* next_tokens, kanso_stream_t stream) {
+    int rc = model_check(m, "kanso_model_forward");
+    if (rc) return rc;
+    if (!plan || !token_arena || !table_arena || !next_tokens || num_seqs == 0) {
+        set_error("kanso_model_forward: null argument or empty plan");
+        return KANSO_E_INVALID_ARG;
+    }
+    HostStep hs;
+    hs.plan.assign(plan, plan + num_seqs);
+    hs.token_arena.assign(token_arena, token_arena + token_arena_len);
+    hs.table_arena.assign(table_arena, table_arena + table_arena_len);
+    for (const auto& p : hs.plan) {
+        if (static_cast<uint64_t>(p.table_offset) + p.table_len > table_arena_len) {
+            set_error("kanso_model_forward: table range outside the table arena");
+            return KANSO_E_OUT_OF_BOUNDS;
+        }
+        for (uint32_t i = 0; i < p.q_len; ++i)
+            if (static_cast<uint32_t>(p.token_offset + p.start_pos + i) >= token_arena_len) {
+                set_error("kanso_model_forward: token outside the token arena");
+                return KANSO_E_OUT_OF_BOUNDS;
+            }
+    }
+    return model_forward(m, hs, logits, next_tokens, as_stream(stream));
+}
+
+}  // extern "C"

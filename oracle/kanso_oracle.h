@@ -133,6 +133,43 @@ uint32_t oracle_greedy(const float* logits, uint32_t n);
 /* fnv1a_64 (src/bench.rs:20-29): one XOR per u32 token widened to u64. */
 uint64_t oracle_fnv1a_64(const uint32_t* tokens, size_t n);
 
+/* ---- batched llama forward (config 5), kanso_oracle_model.cpp ------------ */
+
+typedef struct {
+    uint32_t hidden, num_heads, num_kv_heads, head_dim, num_layers, intermediate, vocab;
+    float eps, rope_theta;
+} oracle_model_config;
+
+/* GGUF Q8_0 matrices ([rows][in/32] x 34 B) and f32 norm weights; per-layer
+ * fields are arrays of num_layers pointers. lm_head may alias embed (tied). */
+typedef struct {
+    const void* embed;
+    const void* lm_head;
+    const float* final_norm;
+    const void* const* wq;
+    const void* const* wk;
+    const void* const* wv;
+    const void* const* wo;
+    const void* const* w_gate;
+    const void* const* w_up;
+    const void* const* w_down;
+    const float* const* attn_norm;
+    const float* const* ffn_norm;
+} oracle_model_weights;
+
+/* Model::forward_batch_rows with RowSelection::LastPerSequence (src/model.rs:
+ * 1418-1739), the mixed-batch arm: embed, per layer RMSNorm -> Q/K/V -> RoPE ->
+ * write_kv_slots into the per-layer F32 pools -> ragged attention with the offset
+ * causal mask -> O + residual -> RMSNorm -> SwiGLU MLP + residual; final RMSNorm
+ * of each sequence's last row and lm_head. logits [S][vocab]. Returns 0 or -1. */
+int oracle_forward_batch(const oracle_model_config* cfg, const oracle_model_weights* w,
+                         const uint32_t* tokens, const int32_t* positions,
+                         const int64_t* slot_mapping, uint32_t T, float* const* k_pools,
+                         float* const* v_pools, uint32_t num_blocks, uint32_t block_size,
+                         const uint32_t* block_tables, uint32_t max_blocks,
+                         const int32_t* cu_seqlens, const uint32_t* context_lens, uint32_t S,
+                         float* logits, int nthreads);
+
 #ifdef __cplusplus
 }
 #endif

@@ -1,0 +1,102 @@
+// kanso_oracle_model.cpp — CPU restatement of kanso-infer's batched llama forward
+// (Model::forward_batch_rows, src/model.rs:1418-1739) over Q8_0 weights and an F32
+// paged KV pool.
+//
+// TEST INFRASTRUCTURE ONLY: the checker of the GPU decoder forward and of the
+// greedy token streams; nothing in the product links or loads it.
+//
+// Each step restates the reference op in the reference's order, using the
+// restated primitives of kanso_oracle.cpp (rmsnorm, Q8_0 GEMV, RoPE, the ragged
+// attention with the offset causal mask, SiLU gating, greedy argmax).
+
+#include <cmath>
+#include <cstring>
+#include <vector>
+
+#include "kanso_oracle.h"
+
+extern "C" {
+
+int oracle_forward_batch(const oracle_model_config* cfg, const oracle_model_weights* w,
+                         const uint32_t* tokens, const int32_t* positions,
+                         const int64_t* slot_mapping, uint32_t T, float* const* k_pools,
+                         float* const* v_pools, uint32_t num_blocks, uint32_t block_size,
+                         const uint32_t* block_tables, uint32_t max_blocks,
+                         const int32_t* cu_seqlens, const uint32_t* context_lens, uint32_t S,
+                         float* logits, int nthreads) {
+    const uint32_t Hd = cfg->hidden, H = cfg->num_heads, HKV = cfg->num_kv_heads;
+    const uint32_t D = cfg->head_dim, I = cfg->intermediate, V = cfg->vocab;
+    if (T == 0 || S == 0 || H % HKV != 0 || Hd % 32 != 0 || I % 32 != 0 || D % 2 != 0) return -1;
+    if (static_cast<uint32_t>(cu_seqlens[S]) != T) return -1;
+    // Model::embed (src/model.rs:425-431): dequantized table rows.
+    std::vector<float> hidden(static_cast<size_t>(T) * Hd);
+    for (uint32_t t = 0; t < T; ++t) {
+        if (tokens[t] >= V) return -1;
+        const uint8_t* blocks = static_cast<const uint8_t*>(w->embed) + static_cast<size_t>(tokens[t]) * (Hd / 32) * 34;
+        oracle_dequant_row_q8_0(blocks, Hd, &hidden[static_cast<size_t>(t) * Hd]);
+    }
+    // rope_cos_sin (src/model.rs:667-696): rows of a table grown in 1024 steps; a
+    // row depends only on its position.
+    int32_t max_pos = 0;
+    for (uint32_t t = 0; t < T; ++t) max_pos = std::max(max_pos, positions[t]);
+    const uint32_t rope_len = (static_cast<uint32_t>(max_pos) + 1 + 1023) / 1024 * 1024;
+    std::vector<float> cos_t(static_cast<size_t>(rope_len) * D / 2), sin_t(cos_t.size());
+    oracle_rope_table(rope_len, D, cfg->rope_theta, cos_t.data(), sin_t.data());
+
+    std::vector<float> normed(static_cast<size_t>(T) * Hd);
+    std::vector<float> q(static_cast<size_t>(T) * H * D), k(static_cast<size_t>(T) * HKV * D),
+        v(static_cast<size_t>(T) * HKV * D), attn(static_cast<size_t>(T) * H * D);
+    std::vector<float> proj(static_cast<size_t>(T) * Hd);
+    std::vector<float> gate(static_cast<size_t>(T) * I), up(static_cast<size_t>(T) * I),
+        act(static_cast<size_t>(T) * I);
+    kanso_ragged_attention_params ap;
+    ap.num_seqs = S;
+    ap.num_heads = H;
+    ap.num_kv_heads = HKV;
+    ap.head_dim = D;
+    ap.block_size = block_size;
+    ap.max_num_blocks_per_seq = max_blocks;
+    // attention_scale: 1 / sqrt(head_dim) (src/model.rs:757-762), applied in f32.
+    ap.scale = static_cast<float>(1.0 / std::sqrt(static_cast<double>(D)));
+    ap.total_q = T;
+    ap.kv_dtype = KANSO_KV_F32;
+    ap.num_blocks = num_blocks;
+    ap.max_q_len = 0;
+
+    for (uint32_t l = 0; l < cfg->num_layers; ++l) {
+        oracle_rmsnorm(hidden.data(), w->attn_norm[l], normed.data(), T, Hd, cfg->eps);
+        oracle_gemv_q8_0(w->wq[l], normed.data(), q.data(), H * D, Hd, T, nthreads);
+        oracle_gemv_q8_0(w->wk[l], normed.data(), k.data(), HKV * D, Hd, T, nthreads);
+        oracle_gemv_q8_0(w->wv[l], normed.data(), v.data(), HKV * D, Hd, T, nthreads);
+        oracle_rope_apply(q.data(), T, H, D, positions, cos_t.data(), sin_t.data());
+        oracle_rope_apply(k.data(), T, HKV, D, positions, cos_t.data(), sin_t.data());
+        // write_kv_slots (src/model.rs:1673; storage.rs:219-254)
+        if (oracle_kv_append(KANSO_KV_F32, k.data(), v.data(), slot_mapping, T, num_blocks, block_size,
+                             HKV, D, k_pools[l], v_pools[l], nullptr, nullptr) != 0)
+            return -1;
+        if (oracle_ragged_attention(q.data(), k_pools[l], v_pools[l], nullptr, nullptr, block_tables,
+                                    cu_seqlens, context_lens, &ap, attn.data(), nthreads) != 0)
+            return -1;
+        // hidden = hidden + attn_output(attn) (src/model.rs:1716-1717)
+        oracle_gemv_q8_0(w->wo[l], attn.data(), proj.data(), Hd, H * D, T, nthreads);
+        for (size_t i = 0; i < hidden.size(); ++i) hidden[i] = hidden[i] + proj[i];
+        // ffn: rmsnorm, gate/up, silu * up, down, residual (src/model.rs:1719-1721, 367-380)
+        oracle_rmsnorm(hidden.data(), w->ffn_norm[l], normed.data(), T, Hd, cfg->eps);
+        oracle_gemv_q8_0(w->w_gate[l], normed.data(), gate.data(), I, Hd, T, nthreads);
+        oracle_gemv_q8_0(w->w_up[l], normed.data(), up.data(), I, Hd, T, nthreads);
+        oracle_silu_mul(gate.data(), up.data(), act.data(), T * I);
+        oracle_gemv_q8_0(w->w_down[l], act.data(), proj.data(), Hd, I, T, nthreads);
+        for (size_t i = 0; i < hidden.size(); ++i) hidden[i] = hidden[i] + proj[i];
+    }
+    // final norm, then lm_head on each sequence's last row (src/model.rs:1726-1738)
+    std::vector<float> last(static_cast<size_t>(S) * Hd);
+    for (uint32_t s = 0; s < S; ++s)
+        std::memcpy(&last[static_cast<size_t>(s) * Hd],
+                    &hidden[static_cast<size_t>(cu_seqlens[s + 1] - 1) * Hd], Hd * sizeof(float));
+    std::vector<float> last_normed(last.size());
+    oracle_rmsnorm(last.data(), w->final_norm, last_normed.data(), S, Hd, cfg->eps);
+    oracle_gemv_q8_0(w->lm_head, last_normed.data(), logits, V, Hd, S, nthreads);
+    return 0;
+}
+
+}  // extern "C"

@@ -1,0 +1,71 @@
+"""CPU model of the parity tests: random-init Q8_0 weights (numpy, seeded), per-layer
+F32 KV pools, and the batched forward of oracle_forward_batch behind the
+engine_ref.Engine forward interface.
+
+TEST INFRASTRUCTURE ONLY (the checker of the GPU decoder and engine)."""
+from __future__ import annotations
+
+import numpy as np
+
+import oracle
+
+
+def random_weights(cfg: dict, seed: int, std: float = 0.02) -> dict:
+    """Every matrix N(0, std^2) quantized by the Q8_0 rule (src/quant/q8_0.rs:13-32);
+    norms = 1 plus a small seeded perturbation so the norm weights are exercised."""
+    rng = np.random.default_rng(seed)
+    h, D, I, V = cfg["hidden"], cfg["head_dim"], cfg["intermediate"], cfg["vocab"]
+    H, KV = cfg["num_heads"], cfg["num_kv_heads"]
+
+    def mat(rows, cols):
+        return oracle.quantize_row_q8_0((rng.standard_normal((rows, cols)) * std).astype(np.float32))
+
+    def norm():
+        return (1.0 + 0.05 * rng.standard_normal(h)).astype(np.float32)
+
+    w = {"embed": mat(V, h), "final_norm": norm(), "layers": []}
+    if not cfg.get("tied", True):
+        w["lm_head"] = mat(V, h)
+    for _ in range(cfg["num_layers"]):
+        w["layers"].append({
+            "attn_norm": norm(), "ffn_norm": norm(),
+            "wq": mat(H * D, h), "wk": mat(KV * D, h), "wv": mat(KV * D, h), "wo": mat(h, H * D),
+            "w_gate": mat(I, h), "w_up": mat(I, h), "w_down": mat(h, I)})
+    return w
+
+
+class OracleModel:
+    def __init__(self, cfg: dict, weights: dict, num_blocks: int, block_size: int, nthreads=8):
+        self.cfg, self.weights = cfg, weights
+        self.num_blocks, self.block_size = num_blocks, block_size
+        n = num_blocks * block_size * cfg["num_kv_heads"] * cfg["head_dim"]
+        self.k = [np.zeros(n, np.float32) for _ in range(cfg["num_layers"])]
+        self.v = [np.zeros(n, np.float32) for _ in range(cfg["num_layers"])]
+        self.nthreads = nthreads
+        self.last_logits = None
+
+    def reset_block(self, block: int) -> None:
+        """allocate_zeroed's erase (src/kv_cache/mod.rs:25-35) across every layer."""
+        w = self.block_size * self.cfg["num_kv_heads"] * self.cfg["head_dim"]
+        for a in self.k + self.v:
+            a[block * w:(block + 1) * w] = 0.0
+
+    def logits(self, plan) -> np.ndarray:
+        bs = self.block_size
+        ctx = np.asarray(plan.context_lens, np.int64)
+        max_blocks = int(max(1, ((ctx + bs - 1) // bs).max()))
+        tables = np.zeros((len(ctx), max_blocks), np.uint32)
+        for s, t in enumerate(plan.block_tables):  # PaddedDecodeTables (model.rs:84-105)
+            need = max(1, -(-int(ctx[s]) // bs))
+            for b in range(max_blocks):
+                tables[s, b] = t[min(b, need - 1)]
+        cu = np.concatenate([[0], np.cumsum(plan.query_lens)]).astype(np.int32)
+        return oracle.forward_batch(self.cfg, self.weights, self.k, self.v, self.num_blocks, bs,
+                                    plan.tokens, plan.positions, plan.slot_mapping, tables,
+                                    max_blocks, cu, ctx, nthreads=self.nthreads)
+
+    def forward(self, plan) -> list:
+        """engine_ref forward: greedy_token (src/sampler.rs:7-17) of each sequence."""
+        lg = self.logits(plan)
+        self.last_logits = lg
+        return [oracle.greedy(row) for row in lg]

@@ -300,3 +300,60 @@ def fnv1a_64(tokens) -> int:
 
 def available() -> bool:
     return LIB_PATH.exists() or os.environ.get("KANSO_ORACLE_BUILD") == "1"
+
+
+# ---------------------------------------------------------------- batched forward
+
+
+class ModelConfigC(C.Structure):
+    _fields_ = [(n, C.c_uint32) for n in ("hidden", "num_heads", "num_kv_heads", "head_dim",
+                                          "num_layers", "intermediate", "vocab")] + [
+        ("eps", C.c_float), ("rope_theta", C.c_float)]
+
+
+class ModelWeightsC(C.Structure):
+    _fields_ = [("embed", C.c_void_p), ("lm_head", C.c_void_p), ("final_norm", C.c_void_p)] + [
+        (n, C.POINTER(C.c_void_p)) for n in ("wq", "wk", "wv", "wo", "w_gate", "w_up", "w_down",
+                                             "attn_norm", "ffn_norm")]
+
+
+def forward_batch(cfg: dict, weights: dict, k_pools, v_pools, num_blocks, block_size, tokens,
+                  positions, slot_mapping, block_tables, max_blocks, cu_seqlens, context_lens,
+                  nthreads=8) -> np.ndarray:
+    """oracle_forward_batch: logits [S, vocab] of each sequence's last row. k_pools /
+    v_pools are per-layer float32 arrays updated in place (write_kv_slots)."""
+    L = cfg["num_layers"]
+    c = ModelConfigC(cfg["hidden"], cfg["num_heads"], cfg["num_kv_heads"], cfg["head_dim"], L,
+                     cfg["intermediate"], cfg["vocab"], cfg.get("eps", 1e-5),
+                     cfg.get("rope_theta", 10000.0))
+    keep = []
+
+    def arr(name):
+        a = (C.c_void_p * L)(*[_p(np.ascontiguousarray(layer[name])).value
+                                for layer in weights["layers"]])
+        keep.append(a)
+        return C.cast(a, C.POINTER(C.c_void_p))
+
+    lm = weights.get("lm_head", weights["embed"])
+    w = ModelWeightsC(_p(weights["embed"]), _p(lm), _p(weights["final_norm"]),
+                      *[arr(n) for n in ("wq", "wk", "wv", "wo", "w_gate", "w_up", "w_down",
+                                         "attn_norm", "ffn_norm")])
+    kp = (C.c_void_p * L)(*[_p(k).value for k in k_pools])
+    vp = (C.c_void_p * L)(*[_p(v).value for v in v_pools])
+    tokens = _u32(tokens)
+    positions = np.ascontiguousarray(positions, dtype=np.int32)
+    slots = np.ascontiguousarray(slot_mapping, dtype=np.int64)
+    tables = _u32(block_tables)
+    cu = np.ascontiguousarray(cu_seqlens, dtype=np.int32)
+    ctx = _u32(context_lens)
+    S = ctx.size
+    logits = np.zeros((S, cfg["vocab"]), np.float32)
+    fn = lib().oracle_forward_batch
+    fn.restype = C.c_int
+    rc = fn(C.byref(c), C.byref(w), _p(tokens), _p(positions), _p(slots), C.c_uint32(tokens.size),
+            C.cast(kp, C.POINTER(C.c_void_p)), C.cast(vp, C.POINTER(C.c_void_p)),
+            C.c_uint32(num_blocks), C.c_uint32(block_size), _p(tables), C.c_uint32(max_blocks),
+            _p(cu), _p(ctx), C.c_uint32(S), _p(logits), C.c_int(nthreads))
+    if rc != 0:
+        raise RuntimeError("oracle_forward_batch rejected the batch")
+    return logits

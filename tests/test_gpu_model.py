@@ -1,0 +1,166 @@
+"""GPU decoder forward and the engine on it, against the oracle: logits of mixed
+steps (prefill chunks + decodes) through kanso_model_forward, and whole engine runs
+whose greedy token streams must match the oracle engine's by the FNV-1a checksum
+(src/bench.rs:20-29)."""
+import numpy as np
+import pytest
+import torch
+
+import engine_ref as R
+import kanso_infer_amd as K
+import oracle
+from gpu_helpers import assert_close, dev, host
+from kanso_infer_amd import _capi
+from kanso_infer_amd.engine import Engine, Model, ModelConfig, fnv1a_64
+from model_ref import OracleModel, random_weights
+
+pytestmark = pytest.mark.gpu
+
+SMALL = dict(hidden=256, num_heads=4, num_kv_heads=2, head_dim=64, num_layers=2, intermediate=512,
+             vocab=1000)
+# SmolLM2-360M widths (15:5 GQA, 960 / 2560, vocab 49152), 4 of the 32 layers
+SMOL4 = dict(hidden=960, num_heads=15, num_kv_heads=5, head_dim=64, num_layers=4,
+             intermediate=2560, vocab=49152)
+
+
+def gpu_model(ctx, cfg, weights, num_blocks, block_size, max_tokens=512, max_seqs=64):
+    mc = ModelConfig(cfg["hidden"], cfg["num_heads"], cfg["num_kv_heads"], cfg["num_layers"],
+                     cfg["intermediate"], cfg["vocab"], max_position=4096)
+    m = Model(ctx, mc)
+    m.load_weights(weights)
+    m.alloc_kv(num_blocks, block_size, max_tokens, max_seqs)
+    return m
+
+
+def compact(plan, bs):
+    """engine_ref.StepPlan -> the kanso_model_forward arrays."""
+    rows, toks, tabs = [], [], []
+    off = 0
+    for s in range(len(plan.query_lens)):
+        ql, ctx = plan.query_lens[s], plan.context_lens[s]
+        start = ctx - ql
+        rows.append([start, ql, len(tabs), len(plan.block_tables[s]), (len(toks) - start) % (1 << 32)])
+        toks.extend(plan.tokens[off:off + ql])
+        tabs.extend(plan.block_tables[s])
+        off += ql
+    return np.array(rows, np.uint32), np.array(toks, np.uint32), np.array(tabs, np.uint32)
+
+
+def mixed_plans(rng, bs, vocab, nblocks):
+    """Step 1: three prefills; step 2: one continues its chunk, two decode."""
+    perm = list(rng.permutation(nblocks))
+    tables = [perm[0:6], perm[6:9], perm[9:20]]
+    prompts = [list(rng.integers(0, vocab, n)) for n in (37, 9, 150)]
+    p1 = [(prompts[0][:20], 0, tables[0]), (prompts[1], 0, tables[1]), (prompts[2][:100], 0, tables[2])]
+    p2 = [(prompts[1][:0] + [int(rng.integers(0, vocab))], 9, tables[1]),
+          (prompts[0][20:37], 20, tables[0]),
+          (prompts[2][100:101], 100, tables[2])]
+    from test_oracle_model import plan_of
+    return plan_of(p1, bs), plan_of(p2, bs)
+
+
+@pytest.mark.parametrize("cfg", [SMALL, SMOL4], ids=["small", "smollm2_width_4_layers"])
+def test_forward_logits_match_oracle(ctx, cfg):
+    bs, nblocks = 16, 40
+    rng = np.random.default_rng(11)
+    w = random_weights(cfg, seed=5)
+    gm = gpu_model(ctx, cfg, w, nblocks, bs)
+    om = OracleModel(cfg, w, nblocks, bs)
+    for step, plan in enumerate(mixed_plans(rng, bs, cfg["vocab"], nblocks)):
+        rows, toks, tabs = compact(plan, bs)
+        S = rows.shape[0]
+        logits = torch.empty(S * cfg["vocab"], device="cuda:0")
+        got_tok = gm.forward(rows, toks, tabs, logits=logits)
+        ctx.check_device_status()
+        want = om.logits(plan)
+        got = host(logits).reshape(S, cfg["vocab"])
+        assert_close(got, want, what=f"logits step {step}")
+        for s in range(S):
+            assert got_tok[s] == oracle.greedy(got[s])
+        # the K / V rows the step wrote match the oracle's pools
+        slots = np.asarray(plan.slot_mapping)
+        width = cfg["num_kv_heads"] * cfg["head_dim"]
+        for layer in range(cfg["num_layers"]):
+            k, v = gm.read_kv_rows(layer, slots)
+            assert_close(k, om.k[layer].reshape(-1, width)[slots], what=f"K pool layer {layer}")
+            assert_close(v, om.v[layer].reshape(-1, width)[slots], what=f"V pool layer {layer}")
+
+
+def test_quantize_q8_0_bit_exact(ctx):
+    rng = np.random.default_rng(3)
+    x = (rng.standard_normal(32 * 4096) * np.repeat(rng.uniform(0, 3, 4096), 32)).astype(np.float32)
+    x[:32] = 0.0  # an all-zero block: d = 0, id = 0
+    x[32:64] = np.float32(1e-30)  # d underflows in f16
+    out = torch.empty(x.size // 32 * 34, dtype=torch.uint8, device="cuda:0")
+    ctx._lib.kanso_quantize_q8_0(ctx.handle, dev(x).data_ptr(), x.size, out.data_ptr(), None)
+    torch.cuda.synchronize()
+    assert np.array_equal(host(out), oracle.quantize_row_q8_0(x))
+
+
+def test_init_random_statistics(ctx):
+    """Device random init: N(0, 0.02^2) weights, unit norms. The final RMSNorm makes
+    the last hidden row unit-RMS, so logits have a standard deviation near
+    0.02 * sqrt(960) ~ 0.62."""
+    cfg = ModelConfig.smollm2_360m(num_hidden_layers=2, max_position=64)
+    m = Model(ctx, cfg)
+    m.init_random(seed=7, std=0.02)
+    m.alloc_kv(8, 16, 16, 4)
+    logits = torch.empty(cfg.vocab_size, device="cuda:0")
+    toks = m.forward(np.array([[0, 5, 0, 1, 0]], np.uint32), np.array([1, 2, 3, 4, 5], np.uint32),
+                     np.array([3], np.uint32), logits=logits)
+    ctx.check_device_status()
+    lg = host(logits)
+    assert np.isfinite(lg).all()
+    assert int(toks[0]) == oracle.greedy(lg)
+    assert 0.45 < lg.std() < 0.8
+
+
+def engine_pair(ctx, cfg, w, max_running, total_blocks, bs, budget):
+    gm = gpu_model(ctx, cfg, w, total_blocks, bs, max_tokens=budget, max_seqs=max_running + 1)
+    eng = Engine(gm, max_running, total_blocks, bs, budget)
+    om = OracleModel(cfg, w, total_blocks, bs)
+    ref = R.Engine(om.forward, max_running, total_blocks, bs, budget, reset_block=om.reset_block)
+    return eng, ref
+
+
+def run_both(eng, ref, requests, max_steps=2000):
+    """requests: (prompt, gen_len, arrival_step); both engines step in lock step."""
+    order = sorted(range(len(requests)), key=lambda i: requests[i][2])
+    nxt = step = 0
+    gen_a, gen_b = [], []
+    while step < max_steps:
+        while nxt < len(order) and requests[order[nxt]][2] <= step:
+            p, g, _ = requests[order[nxt]]
+            eng.add_request(p, g)
+            ref.add_request(p, g)
+            nxt += 1
+        if nxt >= len(order) and not eng.has_unfinished_requests():
+            break
+        a = eng.step()
+        b = ref.step()
+        gen_a.extend(o.token_id for o in a)
+        gen_b.extend(t for _, t, _ in b)
+        assert [(o.request_id, o.token_id, o.is_finished) for o in a] == b, f"step {step}"
+        step += 1
+    assert not eng.has_unfinished_requests()
+    return gen_a, gen_b
+
+
+@pytest.mark.parametrize("cfg,budget,total_blocks", [(SMALL, 32, 64), (SMALL, 512, 14),
+                                                     (SMOL4, 64, 64)],
+                         ids=["small_chunked", "small_tight_pool", "smollm2_width_4_layers"])
+def test_engine_checksum_matches_oracle(ctx, cfg, budget, total_blocks):
+    rng = np.random.default_rng(budget + total_blocks)
+    w = random_weights(cfg, seed=9)
+    bs = 16
+    reqs = []
+    for i in range(6):
+        plen = int(rng.integers(3, 60))
+        # bench.rs prompt pattern for half the requests (prefix-cache hits), random otherwise
+        prompt = ([(i % 3 * 10 + p) % 30 for p in range(plen)] if i % 2 == 0
+                  else rng.integers(0, cfg["vocab"], plen).tolist())
+        reqs.append((prompt, int(rng.integers(4, 20)), int(rng.integers(0, 6))))
+    eng, ref = engine_pair(ctx, cfg, w, 4, total_blocks, bs, budget)
+    gen_a, gen_b = run_both(eng, ref, reqs)
+    assert fnv1a_64(gen_a) == R.fnv1a_64(gen_b) == oracle.fnv1a_64(gen_b)
+    assert len(gen_a) == sum(g for _, g, _ in reqs)

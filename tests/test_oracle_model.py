@@ -1,0 +1,104 @@
+"""Pins the oracle's batched forward (oracle_forward_batch) with invariants the
+reference's own tests assert: chunked prefill == monolithic prefill
+(tests/test_chunked_golden.rs:54-67), batched == per-sequence
+(tests/test_batched_forward.rs:49-226), and a float64 numpy restatement of one
+layer computed independently of the C++ code."""
+import numpy as np
+import pytest
+
+import engine_ref as R
+import oracle
+from model_ref import OracleModel, random_weights
+
+CFG = dict(hidden=128, num_heads=4, num_kv_heads=2, head_dim=32, num_layers=2, intermediate=256,
+           vocab=300)
+
+
+def plan_of(seqs, bs):
+    """seqs: list of (tokens, start_pos, table)."""
+    p = R.StepPlan([], [], [], [], [], [], [], [])
+    for s, (toks, start, table) in enumerate(seqs):
+        for i, t in enumerate(toks):
+            pos = start + i
+            p.tokens.append(t)
+            p.positions.append(pos)
+            p.slot_mapping.append(table[pos // bs] * bs + pos % bs)
+        p.block_tables.append(table)
+        p.context_lens.append(start + len(toks))
+        p.query_lens.append(len(toks))
+        p.request_ids.append(s + 1)
+    return p
+
+
+@pytest.fixture(scope="module")
+def weights():
+    return random_weights(CFG, seed=3, std=0.08)
+
+
+def test_chunked_equals_monolithic(weights):
+    bs = 4
+    prompt = list(np.random.default_rng(0).integers(0, CFG["vocab"], 23))
+    table = [5, 2, 9, 0, 7, 1]
+    a = OracleModel(CFG, weights, 16, bs)
+    mono = a.logits(plan_of([(prompt, 0, table)], bs))
+    b = OracleModel(CFG, weights, 16, bs)
+    for lo, hi in [(0, 8), (8, 9), (9, 20), (20, 23)]:
+        chunked = b.logits(plan_of([(prompt[lo:hi], lo, table)], bs))
+    np.testing.assert_allclose(chunked, mono, atol=1e-4, rtol=1e-4)
+
+
+def test_batched_equals_per_sequence(weights):
+    bs = 4
+    rng = np.random.default_rng(1)
+    seqs = [(list(rng.integers(0, CFG["vocab"], n)), 0, tab)
+            for n, tab in [(5, [3, 4]), (1, [8]), (11, [0, 1, 2])]]
+    batched = OracleModel(CFG, weights, 16, bs).logits(plan_of(seqs, bs))
+    for s, sq in enumerate(seqs):
+        alone = OracleModel(CFG, weights, 16, bs).logits(plan_of([sq], bs))
+        np.testing.assert_allclose(batched[s], alone[0], atol=1e-5, rtol=1e-5)
+
+
+def _f64_forward(cfg, w, tokens):
+    """One sequence from position 0, every op in float64 numpy (no paging)."""
+    h, H, KV, D = cfg["hidden"], cfg["num_heads"], cfg["num_kv_heads"], cfg["head_dim"]
+    deq = lambda m, cols: oracle.dequant_q8_0_rows(m, cols).astype(np.float64)
+    x = deq(w["embed"], h)[tokens]
+    T = len(tokens)
+    half = D // 2
+    theta = 10000.0 ** (-2.0 * np.arange(half) / D)
+    ang = np.arange(T)[:, None] * theta[None, :]
+    cos, sin = np.cos(ang), np.sin(ang)
+
+    def norm(v, g):
+        return v / np.sqrt((v * v).mean(-1, keepdims=True) + 1e-5) * g
+
+    def rope(v):  # [T, heads, D]
+        a, b = v[..., :half], v[..., half:]
+        return np.concatenate([a * cos[:, None] - b * sin[:, None], a * sin[:, None] + b * cos[:, None]], -1)
+
+    for L in w["layers"]:
+        n = norm(x, L["attn_norm"])
+        q = rope((n @ deq(L["wq"], h).T).reshape(T, H, D))
+        k = rope((n @ deq(L["wk"], h).T).reshape(T, KV, D))
+        v = (n @ deq(L["wv"], h).T).reshape(T, KV, D)
+        out = np.zeros((T, H, D))
+        for hh in range(H):
+            kv = hh // (H // KV)
+            s = q[:, hh] @ k[:, kv].T / np.sqrt(D)
+            s = np.where(np.tril(np.ones((T, T))) > 0, s, -np.inf)
+            p = np.exp(s - s.max(-1, keepdims=True))
+            out[:, hh] = (p / p.sum(-1, keepdims=True)) @ v[:, kv]
+        x = x + out.reshape(T, H * D) @ deq(L["wo"], H * D).T
+        n = norm(x, L["ffn_norm"])
+        g = n @ deq(L["w_gate"], h).T
+        u = n @ deq(L["w_up"], h).T
+        x = x + (g / (1 + np.exp(-g)) * u) @ deq(L["w_down"], cfg["intermediate"]).T
+    return norm(x[-1:], w["final_norm"]) @ deq(w.get("lm_head", w["embed"]), h).T
+
+
+def test_matches_float64_restatement(weights):
+    bs = 4
+    toks = list(np.random.default_rng(2).integers(0, CFG["vocab"], 13))
+    got = OracleModel(CFG, weights, 8, bs).logits(plan_of([(toks, 0, [6, 1, 3, 4])], bs))
+    want = _f64_forward(CFG, weights, toks)
+    np.testing.assert_allclose(got, want, atol=2e-4, rtol=1e-3)
