@@ -188,6 +188,81 @@ def gemv_bench(ctx, torch, K, oracle_mod, quick):
     return out
 
 
+def config5_workload(seed=0x5EED0005, num_requests=64, rate=40.0, step_secs=0.005):
+    """Config 5 requests: prompt lengths log-uniform [16, 2048], generation lengths
+    uniform [32, 512], Poisson arrivals at `rate` requests/s mapped to steps of
+    `step_secs` (the reference's sweep constants, src/bench/traffic.rs:5-9, 153-160),
+    synthetic prompts (req*10 + p) % 30 (src/bench.rs:470-474). numpy PCG64 seeded."""
+    from kanso_infer_amd.engine import generate_poisson_schedule, schedule_to_trace
+    rng = np.random.default_rng(seed)
+    plen = np.rint(np.exp(rng.uniform(np.log(16), np.log(2048), num_requests))).astype(int)
+    glen = rng.integers(32, 513, num_requests)
+    sched = generate_poisson_schedule(num_requests, rate, seed + 1)
+    return schedule_to_trace(sched, plen, glen, step_secs)
+
+
+def engine_bench(ctx, K, torch, num_requests=64):
+    """Config 5: SmolLM2-360M-architecture random-init model (32 layers, Q8_0 weights
+    N(0, 0.02^2), tied embeddings, F32 KV) under the C++ continuous-batching engine:
+    512-token budget, max_running 64, block size 16, greedy. Value = generated
+    tokens / wall seconds of the whole run (execute_engine_run, src/bench.rs:447-537)."""
+    from kanso_infer_amd.engine import Engine, Model, ModelConfig, run_benchmark_workload
+    cfg = ModelConfig.smollm2_360m(max_position=4096)
+    t0 = time.perf_counter()
+    model = Model(ctx, cfg)
+    model.init_random(seed=0x5EED0057, std=0.02)
+    reqs = config5_workload(num_requests=num_requests)
+    max_tokens = max(r.prompt_len + r.gen_len for r in reqs)
+    blocks_per_seq = -(-max_tokens // 16) + 1  # create_engine_for_model_profile, src/bench.rs:598-614
+    total_blocks = max(blocks_per_seq * len(reqs), 128)
+    model.alloc_kv(total_blocks, 16, 512, 65)
+    log(f"config5: model ready in {time.perf_counter() - t0:.1f} s, {total_blocks} KV blocks")
+    # warm-up on a throwaway engine (same model and pool), so first-call costs stay out
+    warm = Engine(model, 64, total_blocks, 16, 512)
+    from kanso_infer_amd.engine import TraceEntry
+    run_benchmark_workload(warm, [TraceEntry(300, 8, 0), TraceEntry(40, 8, 0), TraceEntry(600, 4, 1)])
+    warm.close()
+    eng = Engine(model, 64, total_blocks, 16, 512)
+    kv_tok = cfg.kv_cache_bytes_per_token_f32()
+    wbytes = cfg.weight_bytes_q8_0()
+    acc = dict(kv_bytes=0, steps_with_work=0, tokens=0, max_batch=0, step_times=[])
+
+    def on_step(e, outs):
+        plan = e.last_plan()
+        if plan["context_lens"].size:
+            acc["kv_bytes"] += int(plan["context_lens"].astype(np.int64).sum()) * kv_tok
+            acc["steps_with_work"] += 1
+            acc["tokens"] += int(plan["query_lens"].sum())
+            acc["max_batch"] = max(acc["max_batch"], int(plan["context_lens"].size))
+
+    rep = run_benchmark_workload(eng, reqs, on_step=on_step)
+    # every step with work reads all weights once and each sequence's whole context
+    step_bytes = acc["kv_bytes"] + acc["steps_with_work"] * wbytes
+    out = {
+        "metric": "batched decode tok/s (config 5, continuous batching)",
+        "tokens_per_s": round(rep["total_tokens_per_sec"], 1),
+        "generated_tokens": rep["total_tokens"],
+        "processed_tokens": acc["tokens"],
+        "wall_s": round(rep["total_duration_secs"], 3),
+        "steps": rep["steps"],
+        "steps_with_work": acc["steps_with_work"],
+        "ms_per_step": round(1000 * rep["total_duration_secs"] / max(rep["steps"], 1), 3),
+        "decode_ms_per_step": round(rep["decode_ms_per_step"], 3),
+        "max_sequences_per_step": acc["max_batch"],
+        "checksum_fnv1a64": f"{rep['checksum']:016x}",
+        "prefix_hit_rate": round(rep["prefix_hit_rate"], 4),
+        "bytes_read_per_step": int(step_bytes / max(acc["steps_with_work"], 1)),
+        "hbm_frac": round(step_bytes / rep["total_duration_secs"] / HBM_PEAK, 4),
+        "workload": f"{len(reqs)} requests, prompt log-uniform [16,2048], gen U[32,512], Poisson "
+                    "40 req/s at 5 ms/step, budget 512, max_running 64, bs 16, greedy; "
+                    "SmolLM2-360M shape (32 L, 960, GQA 15:5, 2560, vocab 49152), Q8_0 weights "
+                    "random N(0,0.02^2), F32 KV",
+    }
+    eng.close()
+    model.close()
+    return out
+
+
 TRAFFIC_PROFILE = ROOT / "profiles" / "attention_config2_hbm_traffic.md"
 
 
@@ -245,6 +320,8 @@ def main():
     ap.add_argument("--pmc-pass", action="store_true",
                     help="short run for rocprofv3 --pmc: a 512 MiB copy (calibration) then 20 "
                          "headline attention calls; prints nothing else")
+    ap.add_argument("--config5-only", action="store_true",
+                    help="run only the config-5 engine benchmark and print its JSON")
     ap.add_argument("--decode-only", action="store_true",
                     help="also time the headline batches' decode rows alone")
     args = ap.parse_args()
@@ -258,6 +335,11 @@ def main():
     from kanso_infer_amd import workloads
 
     ctx = K.Context(0)
+    if args.config5_only:
+        r5 = engine_bench(ctx, K, torch)
+        ctx.close()
+        print(json.dumps(r5), flush=True)
+        return
     log("building headline batches (config 2, 64k-block pool)")
     nb = 65536
     head = [workloads.config2_mixed(num_blocks=nb, seed_offset=i) for i in range(8)]
@@ -359,6 +441,9 @@ def main():
         import oracle as oracle_mod
         extras["gemv"] = gemv_bench(ctx, torch, K, oracle_mod, quick=False)
         extras["copy_kernel_gbps"] = round(copy_bandwidth(torch), 1)
+        torch.cuda.empty_cache()
+        extras["config5_engine"] = engine_bench(ctx, K, torch)
+        log(f"config5: {extras['config5_engine']}")
 
     cpu = None if args.no_cpu else cpu_baseline(head[0])
     if cpu:

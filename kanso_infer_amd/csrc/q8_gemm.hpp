@@ -15,11 +15,9 @@
 // accumulator C[m = 4(l/16) + r][n = l%16], r = 0..3. So a lane's output row is
 // the row whose weights it loaded, and the block scale is a per-lane scalar.
 //
-// Work mapping. A workgroup of 4 waves owns a pair of 16-row weight groups
-// (32 output rows, chosen by the epilogue) and 16*MT tokens; wave w takes
-// k-blocks w, w+4, ... and the four partial sums meet in LDS in a fixed order.
-// MT is 1, 2 or 4 (token tiles per wave), so a weight operand is loaded once per
-// 16*MT tokens.
+// Work mapping. Output rows come in pairs of 16-row weight groups (32 rows,
+// chosen by the epilogue); a workgroup owns one pair and 16, 32 or 64 tokens and
+// splits K over its waves (see q8_gemm_kernel).
 //
 // Weight layouts:
 //   GGUF   : [rows][in/32] blocks {f16 d; i8 qs[32]} (34 B), the format the
@@ -38,8 +36,6 @@ namespace kanso {
 typedef float floatx4 __attribute__((ext_vector_type(4)));
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 
-constexpr int kGemmThreads = 256;
-constexpr int kGemmWaves = kGemmThreads / kWave;
 constexpr uint32_t kPackedTileBytes = 544;  // 16 rows x (32 qs + 2 d)
 
 __device__ __forceinline__ float f16_bits_to_f32(uint16_t h) { return __half2float(__ushort_as_half(h)); }
@@ -127,36 +123,30 @@ struct XIn {
 //   groups(p, g0, g1): the two 16-row weight groups of pair p;
 //   apply(p, lane, m0, T, v0, v1): outputs of rows g0*16 + lane%16 (v0) and
 //     g1*16 + lane%16 (v1) for tokens m0 .. m0+3 (skip m >= T).
-template <int MT, class WL, class Epi>
-__global__ __launch_bounds__(kGemmThreads) void q8_gemm_kernel(WL wl, XIn xa, Epi epi) {
-    __shared__ float s_rms[16 * MT];
-    __shared__ floatx4 s_part[kGemmWaves][2][MT][kWave];
+//
+// A workgroup of KS waves owns one pair of weight groups and 16*MT tokens; wave w
+// takes k-blocks w, w + KS, ... and issues the loads of U such blocks (weights,
+// x, norm weights) before any arithmetic, so a matrix is requested in one or a few
+// rounds: at decode sizes the time is load latency, not bandwidth. The KS partial
+// sums meet in LDS in a fixed order (results do not depend on T beyond the choice
+// of MT).
+//
+// RMSNorm prologue folded into the product: RMSNorm(x) W = (1 / rms) ((x * w) W),
+// and the sum of squares of each token row is accumulated from the very x values
+// the waves load, so no pass over x precedes the main loop. The division by rms
+// happens on the reduced outputs.
+template <int KS, int U, int MT, class WL, class Epi>
+__global__ __launch_bounds__(KS * kWave) void q8_gemm_kernel(WL wl, XIn xa, Epi epi) {
+    __shared__ floatx4 s_part[KS][2][MT][kWave];
+    __shared__ float s_ss[KS][MT][16];
     const int lane = threadIdx.x & (kWave - 1), wv = threadIdx.x / kWave;
     const int kq = lane >> 4, mm = lane & 15;
     const uint32_t p = blockIdx.x;
     const uint32_t t0 = blockIdx.y * 16 * MT;
     const uint32_t nb = xa.in / 32;
+    const bool norm = xa.norm_w != nullptr;
     uint32_t g0, g1;
     epi.groups(p, g0, g1);
-
-    if (xa.norm_w) {
-        // sum of squares of each token row of this tile; wave w takes 4*MT tokens
-        for (int i = 0; i < 4 * MT; ++i) {
-            const uint32_t tl = wv * 4 * MT + i, m = t0 + tl;
-            float s = 0.f;
-            if (m < xa.T) {
-                const float* xr = xa.row(m);
-                for (uint32_t k = 4 * lane; k < xa.in; k += 4 * kWave) {
-                    const float4 v = *reinterpret_cast<const float4*>(xr + k);
-                    s += v.x * v.x + v.y * v.y + v.z * v.z + v.w * v.w;
-                }
-            }
-            s = group_sum<kWave>(s);
-            if (lane == 0) s_rms[tl] = sqrtf(s / static_cast<float>(xa.in) + xa.eps);
-        }
-        __syncthreads();
-    }
-
     const float* xr[MT];
     bool mok[MT];
 #pragma unroll
@@ -166,68 +156,96 @@ __global__ __launch_bounds__(kGemmThreads) void q8_gemm_kernel(WL wl, XIn xa, Ep
         xr[i] = xa.row(mok[i] ? m : t0);
     }
     floatx4 acc[2][MT];
+    float ss[MT];
 #pragma unroll
     for (int i = 0; i < MT; ++i) {
         acc[0][i] = floatx4{0.f, 0.f, 0.f, 0.f};
         acc[1][i] = floatx4{0.f, 0.f, 0.f, 0.f};
+        ss[i] = 0.f;
     }
-
-    for (uint32_t b = wv; b < nb; b += kGemmWaves) {
-        uint64_t q0, q1;
-        float d0, d1;
-        wl.load(g0, b, lane, q0, d0);
-        wl.load(g1, b, lane, q1, d1);
-        const uint32_t k = 32 * b + 8 * kq;
-        float nw[8];
-        if (xa.norm_w) {
-            const float4 n0 = *reinterpret_cast<const float4*>(xa.norm_w + k);
-            const float4 n1 = *reinterpret_cast<const float4*>(xa.norm_w + k + 4);
-            nw[0] = n0.x; nw[1] = n0.y; nw[2] = n0.z; nw[3] = n0.w;
-            nw[4] = n1.x; nw[5] = n1.y; nw[6] = n1.z; nw[7] = n1.w;
-        }
-        float4 xv[MT][2];
+    for (uint32_t b0 = wv; b0 < nb; b0 += KS * U) {
+        uint64_t q0[U], q1[U];
+        float d0[U], d1[U];
+        float4 xv[U][MT][2], nv[U][2];
 #pragma unroll
-        for (int i = 0; i < MT; ++i) {
-            xv[i][0] = *reinterpret_cast<const float4*>(xr[i] + k);
-            xv[i][1] = *reinterpret_cast<const float4*>(xr[i] + k + 4);
-        }
-        const bf16x8 w0 = i8x8_to_bf16(q0), w1 = i8x8_to_bf16(q1);
+        for (int u = 0; u < U; ++u) {
+            const uint32_t b = b0 + u * KS;
+            if (b < nb) {
+                wl.load(g0, b, lane, q0[u], d0[u]);
+                wl.load(g1, b, lane, q1[u], d1[u]);
+                const uint32_t k = 32 * b + 8 * kq;
 #pragma unroll
-        for (int i = 0; i < MT; ++i) {
-            float xs[8] = {xv[i][0].x, xv[i][0].y, xv[i][0].z, xv[i][0].w,
-                           xv[i][1].x, xv[i][1].y, xv[i][1].z, xv[i][1].w};
-            if (!mok[i]) {
-#pragma unroll
-                for (int j = 0; j < 8; ++j) xs[j] = 0.f;
-            } else if (xa.norm_w) {
-                const float r = s_rms[16 * i + mm];
-#pragma unroll
-                for (int j = 0; j < 8; ++j) xs[j] = xs[j] / r * nw[j];
+                for (int i = 0; i < MT; ++i) {
+                    xv[u][i][0] = *reinterpret_cast<const float4*>(xr[i] + k);
+                    xv[u][i][1] = *reinterpret_cast<const float4*>(xr[i] + k + 4);
+                }
+                if (norm) {
+                    nv[u][0] = *reinterpret_cast<const float4*>(xa.norm_w + k);
+                    nv[u][1] = *reinterpret_cast<const float4*>(xa.norm_w + k + 4);
+                }
             }
-            const Bf16Pair a = split_bf16(xs);
-            const floatx4 z = {0.f, 0.f, 0.f, 0.f};
-            floatx4 t = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a.hi, w0, z, 0, 0, 0);
-            t = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a.lo, w0, t, 0, 0, 0);
-            acc[0][i] += d0 * t;
-            t = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a.hi, w1, z, 0, 0, 0);
-            t = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a.lo, w1, t, 0, 0, 0);
-            acc[1][i] += d1 * t;
+        }
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+            if (b0 + u * KS >= nb) break;
+            const bf16x8 w0 = i8x8_to_bf16(q0[u]), w1 = i8x8_to_bf16(q1[u]);
+            const float nw[8] = {nv[u][0].x, nv[u][0].y, nv[u][0].z, nv[u][0].w,
+                                 nv[u][1].x, nv[u][1].y, nv[u][1].z, nv[u][1].w};
+#pragma unroll
+            for (int i = 0; i < MT; ++i) {
+                float xs[8] = {xv[u][i][0].x, xv[u][i][0].y, xv[u][i][0].z, xv[u][i][0].w,
+                               xv[u][i][1].x, xv[u][i][1].y, xv[u][i][1].z, xv[u][i][1].w};
+                if (!mok[i]) {
+#pragma unroll
+                    for (int j = 0; j < 8; ++j) xs[j] = 0.f;
+                } else if (norm) {
+#pragma unroll
+                    for (int j = 0; j < 8; ++j) {
+                        ss[i] += xs[j] * xs[j];
+                        xs[j] *= nw[j];
+                    }
+                }
+                const Bf16Pair a = split_bf16(xs);
+                const floatx4 z = {0.f, 0.f, 0.f, 0.f};
+                floatx4 t = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a.hi, w0, z, 0, 0, 0);
+                t = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a.lo, w0, t, 0, 0, 0);
+                acc[0][i] += d0[u] * t;
+                t = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a.hi, w1, z, 0, 0, 0);
+                t = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a.lo, w1, t, 0, 0, 0);
+                acc[1][i] += d1[u] * t;
+            }
         }
     }
-
 #pragma unroll
     for (int i = 0; i < MT; ++i) {
         s_part[wv][0][i][lane] = acc[0][i];
         s_part[wv][1][i][lane] = acc[1][i];
+        if (norm) {
+            // the four lanes holding a token's k-chunks: lane ^ 16, lane ^ 32
+            float s = ss[i] + wave_xor(ss[i], 16);
+            s += wave_xor(s, 32);
+            if (kq == 0) s_ss[wv][i][mm] = s;
+        }
     }
     __syncthreads();
     if (wv < MT) {
         const int i = wv;
         floatx4 v0 = s_part[0][0][i][lane], v1 = s_part[0][1][i][lane];
 #pragma unroll
-        for (int w = 1; w < kGemmWaves; ++w) {
+        for (int w = 1; w < KS; ++w) {
             v0 += s_part[w][0][i][lane];
             v1 += s_part[w][1][i][lane];
+        }
+        if (norm) {
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                float s = s_ss[0][i][4 * kq + r];
+#pragma unroll
+                for (int w = 1; w < KS; ++w) s += s_ss[w][i][4 * kq + r];
+                const float rms = sqrtf(s / static_cast<float>(xa.in) + xa.eps);
+                v0[r] /= rms;
+                v1[r] /= rms;
+            }
         }
         epi.apply(p, lane, t0 + 16 * i + 4 * kq, xa.T, v0, v1);
     }
@@ -392,18 +410,30 @@ struct EpiArgmax {
     }
 };
 
-// Launch helper: grid (pairs, token tiles); MT from the token count.
+// Launch helper: 16, 32 or 64 tokens per workgroup (MT = 1, 2, 4), K split over
+// 8 waves (so a token's result never depends on the batch size), U blocks of
+// loads in flight per wave: a whole 960-wide row in one round.
+template <int MT, class WL, class Epi>
+inline void launch_mt(const WL& wl, const XIn& xa, const Epi& epi, uint32_t pairs, uint32_t nb, hipStream_t s) {
+    const dim3 grid(pairs, (xa.T + 16 * MT - 1) / (16 * MT));
+    if constexpr (MT == 4)  // 64 tokens of x per block already fill the registers
+        hipLaunchKernelGGL((q8_gemm_kernel<8, 2, MT, WL, Epi>), grid, dim3(8 * kWave), 0, s, wl, xa, epi);
+    else if (nb <= 32)
+        hipLaunchKernelGGL((q8_gemm_kernel<8, 4, MT, WL, Epi>), grid, dim3(8 * kWave), 0, s, wl, xa, epi);
+    else
+        hipLaunchKernelGGL((q8_gemm_kernel<8, 5, MT, WL, Epi>), grid, dim3(8 * kWave), 0, s, wl, xa, epi);
+}
+
 template <class WL, class Epi>
 inline int launch_q8_gemm(const WL& wl, const XIn& xa, const Epi& epi, uint32_t pairs, hipStream_t s) {
     if (xa.T == 0 || pairs == 0) return KANSO_OK;
-    if (xa.T <= 16) {
-        hipLaunchKernelGGL((q8_gemm_kernel<1, WL, Epi>), dim3(pairs, 1), dim3(kGemmThreads), 0, s, wl, xa, epi);
-    } else if (xa.T <= 32) {
-        hipLaunchKernelGGL((q8_gemm_kernel<2, WL, Epi>), dim3(pairs, 1), dim3(kGemmThreads), 0, s, wl, xa, epi);
-    } else {
-        hipLaunchKernelGGL((q8_gemm_kernel<4, WL, Epi>), dim3(pairs, (xa.T + 63) / 64), dim3(kGemmThreads), 0, s,
-                           wl, xa, epi);
-    }
+    const uint32_t nb = xa.in / 32;
+    if (xa.T <= 16)
+        launch_mt<1>(wl, xa, epi, pairs, nb, s);
+    else if (xa.T <= 32)
+        launch_mt<2>(wl, xa, epi, pairs, nb, s);
+    else
+        launch_mt<4>(wl, xa, epi, pairs, nb, s);
     KANSO_LAUNCH_CHECK();
     return KANSO_OK;
 }

@@ -73,14 +73,17 @@ def test_gemv_gguf_any_batch(ctx, T):
     assert_close(host(y), oracle.gemv_q8_0(w, x, rows, cols, nthreads=8), what=f"gguf T{T}")
 
 
-def test_batch_invariance(ctx):
-    """A token's output does not depend on what else is in the batch."""
-    rows, cols = 960, 960
+@pytest.mark.parametrize("cols", [960, 2560])
+def test_batch_invariance(ctx, cols):
+    """A token's output does not depend on the rest of the batch: every batch size
+    assigns k-blocks to the same waves and sums them in the same order."""
+    sizes = (1, 7, 16, 17, 32, 33, 40, 64, 200, 512)
+    rows = 960
     w = q8_weights(rows, cols, 9)
     packed = K.pack_q8_0_matrix(ctx, dev(w), rows, cols)
-    x = np.random.default_rng(1).standard_normal((200, cols)).astype(np.float32)
+    x = np.random.default_rng(1).standard_normal((max(sizes), cols)).astype(np.float32)
     outs = []
-    for T in (1, 7, 40, 200):
+    for T in sizes:
         y = torch.empty(T * rows, dtype=torch.float32, device="cuda:0")
         K.gemm_q8_0(ctx, packed, dev(x[:T]), y, rows, cols)
         outs.append(host(y).reshape(T, rows)[0])
