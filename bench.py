@@ -36,6 +36,7 @@ sys.path.insert(0, str(ROOT))
 HBM_PEAK = 8.0e12
 PMC_COPY_BYTES = 512 << 20
 METRIC = "ragged paged-attn tokens/s + % HBM peak; batched decode tok/s at 1 MI355X"
+POOL_LAYOUT = 0  # KANSO_POOL_TOKEN_MAJOR unless --pool-layout head
 
 
 def log(msg: str) -> None:
@@ -98,7 +99,8 @@ class AttnBench:
             block_tables=d["tables"], cu_seqlens=d["cu"], context_lens=d["lens"], out=d["out"],
             num_heads=b.num_heads, num_kv_heads=b.num_kv_heads, head_dim=b.head_dim,
             block_size=b.block_size, scale=b.scale, kv_dtype=self.kv_dtype,
-            num_blocks=self.num_blocks, max_q_len=int(b.q_lens.max()))
+            num_blocks=self.num_blocks, max_q_len=int(b.q_lens.max()),
+            pool_layout=POOL_LAYOUT)
 
     def run(self, steps, warmup):
         torch = self.torch
@@ -320,11 +322,15 @@ def main():
     ap.add_argument("--pmc-pass", action="store_true",
                     help="short run for rocprofv3 --pmc: a 512 MiB copy (calibration) then 20 "
                          "headline attention calls; prints nothing else")
+    ap.add_argument("--pool-layout", choices=("token", "head"), default="token",
+                    help="row order inside a KV block for the attention benchmarks")
     ap.add_argument("--config5-only", action="store_true",
                     help="run only the config-5 engine benchmark and print its JSON")
     ap.add_argument("--decode-only", action="store_true",
                     help="also time the headline batches' decode rows alone")
     args = ap.parse_args()
+    global POOL_LAYOUT
+    POOL_LAYOUT = 1 if args.pool_layout == "head" else 0
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print("bench.py measures one GPU: this path has no multi-GPU component in this build "
               "(see DESIGN.md for how it would shard); run with --gpus 1", file=sys.stderr)

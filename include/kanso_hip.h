@@ -79,6 +79,14 @@ enum {
  *         of src/quant/q8_0.rs:13-32; head_dim must be a multiple of 32.       */
 enum { KANSO_KV_F32 = 0, KANSO_KV_INT8 = 1, KANSO_KV_Q8_0 = 2 };
 
+/* Row order inside a pool block (every pool tensor and its scales alike).
+ *   TOKEN_MAJOR: [num_blocks][block_size][num_kv_heads][...], the reference's
+ *                (src/kv_cache/storage.rs:70-76);
+ *   HEAD_MAJOR:  [num_blocks][num_kv_heads][block_size][...]: one (block, KV head)
+ *                is block_size contiguous rows, the layout this build's engine
+ *                uses (contiguous 4 KB runs per head at head_dim 64, F32). */
+enum { KANSO_POOL_TOKEN_MAJOR = 0, KANSO_POOL_HEAD_MAJOR = 1 };
+
 /* Same fields, order and types as PagedAttentionParams (src/metal/paged_attention.rs:12-22). */
 typedef struct {
     uint32_t num_seqs;
@@ -103,6 +111,7 @@ typedef struct {
     uint32_t kv_dtype;   /* KANSO_KV_*                                              */
     uint32_t num_blocks; /* physical blocks in the pool (bounds check of table ids) */
     uint32_t max_q_len;  /* upper bound of any sequence's query rows (0 = total_q)  */
+    uint32_t pool_layout; /* KANSO_POOL_*                                           */
 } kanso_ragged_attention_params;
 
 /* One planned sequence of a step, as Engine::step plans it (src/engine.rs:221-226). */

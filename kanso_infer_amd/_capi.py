@@ -34,6 +34,9 @@ KANSO_KV_F32 = 0
 KANSO_KV_INT8 = 1
 KANSO_KV_Q8_0 = 2
 
+KANSO_POOL_TOKEN_MAJOR = 0
+KANSO_POOL_HEAD_MAJOR = 1
+
 
 class PagedAttentionParamsC(C.Structure):
     _fields_ = [
@@ -60,6 +63,7 @@ class RaggedAttentionParamsC(C.Structure):
         ("kv_dtype", C.c_uint32),
         ("num_blocks", C.c_uint32),
         ("max_q_len", C.c_uint32),
+        ("pool_layout", C.c_uint32),
     ]
 
 

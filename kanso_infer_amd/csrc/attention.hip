@@ -63,6 +63,7 @@ struct AttnArgs {
     uint32_t max_blocks, num_blocks, part_size, max_parts, total_q, capacity;
     uint32_t chunk_part;  // partition size of MFMA chunk rows (>= part_size)
     uint32_t use_mfma;
+    uint32_t head_major;  // pool rows [block][kv head][offset] instead of [block][offset][kv head]
     uint32_t pool_bytes, scale_bytes;  // per pool tensor, for buffer resources (< 4 GiB)
     float scale_log2;
 };
@@ -354,7 +355,9 @@ __device__ __forceinline__ PartView load_part(const AttnArgs& a, uint32_t seq, u
 __device__ __forceinline__ size_t pool_row(const AttnArgs& a, const PartView& pv, uint32_t t, uint32_t kvh) {
     const uint32_t blk = block_of(a, t);
     const uint32_t phys = static_cast<uint32_t>(__shfl(pv.tab, static_cast<int>(blk - pv.blk0), kWave));
-    return (static_cast<size_t>(phys) * a.block_size + (t - blk * a.block_size)) * a.num_kv_heads + kvh;
+    const uint32_t off = t - blk * a.block_size;
+    if (a.head_major) return (static_cast<size_t>(phys) * a.num_kv_heads + kvh) * a.block_size + off;
+    return (static_cast<size_t>(phys) * a.block_size + off) * a.num_kv_heads + kvh;
 }
 
 // ---------------------------------------------------------------- decode rows
@@ -431,7 +434,7 @@ __device__ __forceinline__ void decode_compute(const AttnArgs& a, const PartView
     }
 }
 
-template <int D, int GMAX, int KVT, int NL, bool DB, bool BUF>
+template <int D, int GMAX, int KVT, int NL, int NB, bool BUF>
 __device__ void decode_item(const AttnArgs& a, const PoolRsrc& rs, uint32_t row, uint32_t part, uint32_t seq,
                             uint32_t kvh, int lane) {
     constexpr int LPT = D / 4;
@@ -458,23 +461,21 @@ __device__ void decode_item(const AttnArgs& a, const PoolRsrc& rs, uint32_t row,
                 a.q + (static_cast<size_t>(row) * a.num_heads + kvh * G + g) * D + dl * 4);
     }
 
-    if constexpr (DB) {
-        // Double-buffered: the next tile's loads are in flight during this tile's math.
-        DecodeTile<D, KVT, NL> ta, tb;
-        decode_load<D, KVT, NL, BUF>(a, rs, pv, t_begin, kvh, ts, dl, ta);
-        for (uint32_t t0 = t_begin; t0 < t_end; t0 += 2 * TT) {
-            const bool has_b = t0 + TT < t_end;
-            if (has_b) decode_load<D, KVT, NL, BUF>(a, rs, pv, t0 + TT, kvh, ts, dl, tb);
-            decode_compute<D, GMAX, KVT, NL>(a, pv, t0, ts, qv, acc, m, l, ta);
-            if (t0 + 2 * TT < t_end) decode_load<D, KVT, NL, BUF>(a, rs, pv, t0 + 2 * TT, kvh, ts, dl, ta);
-            if (has_b) decode_compute<D, GMAX, KVT, NL>(a, pv, t0 + TT, ts, qv, acc, m, l, tb);
-        }
-    } else {
-        // Single-buffered: fewer registers, more resident waves carry the loads.
-        for (uint32_t t0 = t_begin; t0 < t_end; t0 += TT) {
-            DecodeTile<D, KVT, NL> tl;
-            decode_load<D, KVT, NL, BUF>(a, rs, pv, t0, kvh, ts, dl, tl);
-            decode_compute<D, GMAX, KVT, NL>(a, pv, t0, ts, qv, acc, m, l, tl);
+    // A ring of NB tiles: while one tile is scored, the loads of the next NB - 1
+    // are in flight. The ring is walked NB tiles per iteration so every buffer
+    // index is a compile-time constant (registers, never scratch).
+    DecodeTile<D, KVT, NL> ring[NB];
+#pragma unroll
+    for (int j = 0; j + 1 < NB; ++j)
+        if (t_begin + j * TT < t_end) decode_load<D, KVT, NL, BUF>(a, rs, pv, t_begin + j * TT, kvh, ts, dl, ring[j]);
+    for (uint32_t t0 = t_begin; t0 < t_end; t0 += NB * TT) {
+#pragma unroll
+        for (int j = 0; j < NB; ++j) {
+            const uint32_t tj = t0 + j * TT;
+            if (tj >= t_end) break;
+            const uint32_t nxt = tj + (NB - 1) * TT;
+            if (nxt < t_end) decode_load<D, KVT, NL, BUF>(a, rs, pv, nxt, kvh, ts, dl, ring[(j + NB - 1) % NB]);
+            decode_compute<D, GMAX, KVT, NL>(a, pv, tj, ts, qv, acc, m, l, ring[j]);
         }
     }
 
@@ -773,7 +774,7 @@ __device__ void zero_empty_rows(const AttnArgs& a, const SeqTable& st, uint32_t 
 // partition x KV head) round-robin. Compute-bound MFMA work and bandwidth-bound
 // decode work therefore run side by side on different CUs. With no chunk items (or
 // more chunk items than workgroups) every wave also takes decode items.
-template <int D, int GMAX, int KVT, bool BUF, int GC>
+template <int D, int GMAX, int KVT, bool BUF, int GC, int NL = 8, int NB = 2>
 __global__ __launch_bounds__(kThreads, 2) void attn_main(AttnArgs a) {
     __shared__ SeqTable st;
     PoolRsrc rs;
@@ -832,7 +833,7 @@ __global__ __launch_bounds__(kThreads, 2) void attn_main(AttnArgs a) {
                 local -= np;
             }
         }
-        decode_item<D, GMAX, KVT, 8, true, BUF>(a, rs, static_cast<uint32_t>(st.cu[s] + i), local, s, kvh, lane);
+        decode_item<D, GMAX, KVT, NL, NB, BUF>(a, rs, static_cast<uint32_t>(st.cu[s] + i), local, s, kvh, lane);
     }
 }
 
@@ -942,15 +943,20 @@ bool head_dim_supported(uint32_t d) {
     return d == 4 || d == 8 || d == 16 || d == 32 || d == 64 || d == 128 || d == 256;
 }
 
-// Partition size: 256 tokens (the reference's PARTITION_SIZE) unless that leaves
-// fewer items than waves the grid keeps resident, then halved down to 64. Capped so
-// a partition touches at most 63 table entries (one register lane each) and kept a
-// power of two (a multiple of the 32-key MFMA tile).
-uint32_t choose_partition(const kanso_ctx* ctx, uint32_t rows, uint32_t kv_heads, uint32_t capacity,
+// Partition size. Every partial a row is split into costs a write, a read and a
+// merge, so partitions are as long as occupancy allows: the largest of 512, 256,
+// 128, 64 tokens for which the decode items (one per sequence, KV head and
+// partition of a context assumed half the table capacity, the only context size
+// the host knows without reading device data) still number at least half the
+// waves the grid keeps resident (measured on the config-2 batch: 512 beats 256 by
+// 5% and 768+ starves the machine). Capped so a partition touches at most 62
+// table entries (one register lane each).
+uint32_t choose_partition(const kanso_ctx* ctx, uint32_t seqs, uint32_t kv_heads, uint32_t capacity,
                           uint32_t block_size) {
-    uint32_t P = kRefPartition;
-    const uint64_t target = static_cast<uint64_t>(ctx->num_cus) * 8;
-    while (P > 64 && static_cast<uint64_t>(rows) * kv_heads * ((capacity + P - 1) / P) < target) P /= 2;
+    uint32_t P = 2 * kRefPartition;
+    const uint64_t target = static_cast<uint64_t>(ctx->num_cus) * kWaves;  // 2 WGs/CU resident, half of them
+    const uint32_t half_ctx = std::max(capacity / 2, 1u);
+    while (P > 64 && static_cast<uint64_t>(seqs) * kv_heads * ((half_ctx + P - 1) / P) < target) P /= 2;
     while (P > 32 && P > 62u * block_size) P /= 2;
     return P;
 }
@@ -1009,7 +1015,8 @@ int run_ragged(kanso_ctx* ctx, const kanso_ragged_attention_params* p, const flo
     }
     const uint32_t capacity = static_cast<uint32_t>(cap64);
     const uint32_t T = p->total_q;
-    const uint32_t P = choose_partition(ctx, T, HKV, capacity, p->block_size);
+    uint32_t P = choose_partition(ctx, S, HKV, capacity, p->block_size);
+    if (const char* v = std::getenv("KANSO_ATTN_PART")) P = static_cast<uint32_t>(std::atoi(v));
     const uint32_t max_parts = (capacity + P - 1) / P;
     const uint64_t partial_elems = static_cast<uint64_t>(T) * H * max_parts * D;
     if (partial_elems > (1ull << 31)) {
@@ -1071,7 +1078,16 @@ int run_ragged(kanso_ctx* ctx, const kanso_ragged_attention_params* p, const flo
     // chunk kernel reads the pool through buffer resources (pool below 4 GiB).
     const uint32_t max_q = p->max_q_len ? p->max_q_len : T;
     a.use_mfma = (D == 64 && G <= 4 && max_q > 1 && buf) ? 1u : 0u;
+    a.head_major = p->pool_layout == KANSO_POOL_HEAD_MAJOR ? 1u : 0u;
     Stage1Fn main_fn = pick_main_kv(p->kv_dtype, D, G, buf);
+    if (const char* v = std::getenv("KANSO_ATTN_VARIANT"); v && D == 64 && G == 3 && buf &&
+                                                            p->kv_dtype == KANSO_KV_F32) {
+        const int var = std::atoi(v);
+        if (var == 1) main_fn = attn_main<64, 3, KANSO_KV_F32, true, 3, 8, 3>;
+        if (var == 2) main_fn = attn_main<64, 3, KANSO_KV_F32, true, 3, 12, 2>;
+        if (var == 3) main_fn = attn_main<64, 3, KANSO_KV_F32, true, 3, 4, 3>;
+        if (var == 4) main_fn = attn_main<64, 3, KANSO_KV_F32, true, 3, 4, 4>;
+    }
     Stage1Fn reduce = pick_reduce(D);
     if (!main_fn || !reduce) {
         set_error("%s: no kernel for head_dim %u / kv_dtype %u", who, D, p->kv_dtype);
@@ -1185,6 +1201,7 @@ int kanso_paged_attention_v2(kanso_ctx* ctx, const kanso_paged_attention_params*
     rp.kv_dtype = KANSO_KV_F32;
     rp.num_blocks = 0;  // the reference call carries no pool size
     rp.max_q_len = 1;
+    rp.pool_layout = KANSO_POOL_TOKEN_MAJOR;
     return run_ragged(ctx, &rp, q, k_cache, v_cache, nullptr, nullptr, block_tables, cu_buf,
                       context_lens, out, s, "kanso_paged_attention_v2");
 }

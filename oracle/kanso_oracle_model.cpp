@@ -62,6 +62,7 @@ int oracle_forward_batch(const oracle_model_config* cfg, const oracle_model_weig
     ap.kv_dtype = KANSO_KV_F32;
     ap.num_blocks = num_blocks;
     ap.max_q_len = 0;
+    ap.pool_layout = KANSO_POOL_TOKEN_MAJOR;
 
     for (uint32_t l = 0; l < cfg->num_layers; ++l) {
         oracle_rmsnorm(hidden.data(), w->attn_norm[l], normed.data(), T, Hd, cfg->eps);

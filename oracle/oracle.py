@@ -26,7 +26,7 @@ class PagedParams(C.Structure):
 
 class RaggedParams(C.Structure):
     _fields_ = PagedParams._fields_ + [(n, C.c_uint32) for n in (
-        "total_q", "kv_dtype", "num_blocks", "max_q_len")]
+        "total_q", "kv_dtype", "num_blocks", "max_q_len", "pool_layout")]
 
 
 def _p(a: np.ndarray | None):
