@@ -150,24 +150,28 @@ def copy_bandwidth(torch, nbytes=2 << 30, iters=10):
 
 def gemv_bench(ctx, torch, K, oracle_mod, quick):
     """Q8_0 / Q4_K GEMV at the SmolLM2 projection shapes; each timing rotates over
-    weight copies totalling > 1 GB."""
+    weight copies totalling > 1 GB. kind q8_0: GGUF blocks (kanso_gemv_q8_0);
+    q8_0_packed: the same bytes in the decoder's packed layout (kanso_gemm_q8_0)."""
     dev = torch.device("cuda:0")
     shapes = [("q", 960, 960), ("kv", 320, 960), ("gate_up", 2560, 960), ("down", 960, 2560)]
     out = []
-    for kind in ("q8_0", "q4_k"):
+    for kind in ("q8_0", "q8_0_packed", "q4_k"):
         for name, rows, cols in shapes:
-            cols_eff = cols if kind == "q8_0" or cols % 256 == 0 else 1024
+            cols_eff = cols if kind != "q4_k" or cols % 256 == 0 else 1024
             label = name if cols_eff == cols else name + "_padded"
             rng = np.random.default_rng(rows + cols)
             wf = (rng.standard_normal((rows, cols_eff)) * 0.02).astype(np.float32)
             if cols_eff != cols:
                 wf[:, cols:] = 0.0
-            w = (oracle_mod.quantize_row_q8_0(wf) if kind == "q8_0"
+            w = (oracle_mod.quantize_row_q8_0(wf) if kind != "q4_k"
                  else oracle_mod.quantize_row_q4_k(wf))
-            wbytes = w.size
+            one = torch.from_numpy(w).to(dev)
+            if kind == "q8_0_packed":
+                one = K.pack_q8_0_matrix(ctx, one, rows, cols_eff)
+            wbytes = one.numel()
             copies = max(32, int((1.1e9) // wbytes) + 1)
-            arena = torch.from_numpy(w).to(dev).repeat(copies)
-            fn = K.gemv_q8_0 if kind == "q8_0" else K.gemv_q4_k
+            arena = one.repeat(copies)
+            fn = {"q8_0": K.gemv_q8_0, "q8_0_packed": K.gemm_q8_0, "q4_k": K.gemv_q4_k}[kind]
             for batch in ([1, 8, 32] if quick else [1, 4, 8, 16, 32]):
                 x = torch.randn(batch * cols_eff, device=dev)
                 y = torch.empty(batch * rows, device=dev)
@@ -181,7 +185,7 @@ def gemv_bench(ctx, torch, K, oracle_mod, quick):
                 g_ms, g_n = ctx.kernel_time("gemv")
                 ctx.set_profiling(False)
                 us = g_ms / max(g_n, 1) * 1e3
-                abytes = wbytes + batch * (cols_eff + rows) * 4
+                abytes = w.size + batch * (cols_eff + rows) * 4  # stored GGUF bytes
                 out.append(dict(kind=kind, shape=label, out=rows, inp=cols_eff, batch=batch,
                                 us=round(us, 2), gbps=round(abytes / (us * 1e-6) / 1e9, 1),
                                 frac=round(abytes / (us * 1e-6) / HBM_PEAK, 4)))
@@ -265,6 +269,99 @@ def engine_bench(ctx, K, torch, num_requests=64):
     return out
 
 
+def config5_cpu_baseline(threads=None):
+    """The oracle (C++ restatement of the reference CPU path, OpenMP) running the full
+    SmolLM2-360M-shape model: one decode step of 16 sequences with contexts
+    U[128, 1024] over a paged F32 pool. A bounded sample of config 5's work: a full
+    run would take hours on the host."""
+    sys.path.insert(0, str(ROOT / "oracle"))
+    import engine_ref
+    from model_ref import OracleModel, random_weights
+    threads = threads or min(os.cpu_count() or 1, 16)
+    cfg = dict(hidden=960, num_heads=15, num_kv_heads=5, head_dim=64, num_layers=32,
+               intermediate=2560, vocab=49152)
+    t0 = time.perf_counter()
+    w = random_weights(cfg, seed=1)
+    rng = np.random.default_rng(2)
+    S = 16
+    ctx = rng.integers(128, 1025, S)
+    need = (ctx + 15) // 16
+    nblocks = int(need.sum())
+    om = OracleModel(cfg, w, nblocks, 16, nthreads=threads)
+    for a in om.k + om.v:
+        a[:] = rng.standard_normal(a.size, dtype=np.float32)
+    plan = engine_ref.StepPlan([], [], [], [], [], [], [], [])
+    off = 0
+    for s in range(S):
+        table = list(range(off, off + int(need[s])))
+        off += int(need[s])
+        pos = int(ctx[s]) - 1
+        plan.tokens.append(int(rng.integers(0, cfg["vocab"])))
+        plan.positions.append(pos)
+        plan.slot_mapping.append(table[pos // 16] * 16 + pos % 16)
+        plan.block_tables.append(table)
+        plan.context_lens.append(int(ctx[s]))
+        plan.query_lens.append(1)
+        plan.request_ids.append(s + 1)
+    setup = time.perf_counter() - t0
+    t1 = time.perf_counter()
+    om.logits(plan)
+    el = time.perf_counter() - t1
+    return dict(value=round(S / el, 2), unit="tokens/s", cores=threads, kind="port",
+                sample=f"one decode step, 16 sequences, contexts U[128,1024] (mean {ctx.mean():.0f}), "
+                       f"32 layers, {el:.1f} s on {threads} threads (setup {setup:.1f} s)")
+
+
+def config5_checksum_parity(ctx, K, torch):
+    """Greedy token streams of the GPU engine and of the oracle engine (scheduler
+    restatement + CPU forward) on the same random-init weights: SmolLM2 widths, 4 of
+    the 32 layers, 6 requests with bench.rs-pattern and random prompts, chunked
+    prefill (budget 64). Returns both FNV-1a checksums."""
+    sys.path.insert(0, str(ROOT / "oracle"))
+    import engine_ref
+    import oracle as oracle_mod
+    from kanso_infer_amd.engine import Engine, Model, ModelConfig, fnv1a_64
+    from model_ref import OracleModel, random_weights
+    cfg = dict(hidden=960, num_heads=15, num_kv_heads=5, head_dim=64, num_layers=4,
+               intermediate=2560, vocab=49152)
+    w = random_weights(cfg, seed=9)
+    bs, budget, total_blocks, max_running = 16, 64, 64, 4
+    gm = Model(ctx, ModelConfig(960, 15, 5, 4, 2560, 49152, max_position=4096))
+    gm.load_weights(w)
+    gm.alloc_kv(total_blocks, bs, budget, max_running + 1)
+    eng = Engine(gm, max_running, total_blocks, bs, budget)
+    om = OracleModel(cfg, w, total_blocks, bs, nthreads=min(os.cpu_count() or 1, 16))
+    ref = engine_ref.Engine(om.forward, max_running, total_blocks, bs, budget,
+                            reset_block=om.reset_block)
+    rng = np.random.default_rng(7)
+    reqs = []
+    for i in range(6):
+        plen = int(rng.integers(3, 60))
+        prompt = ([(i % 3 * 10 + p) % 30 for p in range(plen)] if i % 2 == 0
+                  else rng.integers(0, cfg["vocab"], plen).tolist())
+        reqs.append((prompt, int(rng.integers(4, 20)), int(rng.integers(0, 6))))
+    order = sorted(range(len(reqs)), key=lambda i: reqs[i][2])
+    nxt = step = 0
+    a_tok, b_tok = [], []
+    while True:
+        while nxt < len(order) and reqs[order[nxt]][2] <= step:
+            p, g, _ = reqs[order[nxt]]
+            eng.add_request(p, g)
+            ref.add_request(p, g)
+            nxt += 1
+        if nxt >= len(order) and not eng.has_unfinished_requests():
+            break
+        a_tok.extend(o.token_id for o in eng.step())
+        b_tok.extend(t for _, t, _ in ref.step())
+        step += 1
+    eng.close()
+    gm.close()
+    return dict(gpu=f"{fnv1a_64(a_tok):016x}", oracle=f"{oracle_mod.fnv1a_64(b_tok):016x}",
+                match=a_tok == b_tok, tokens=len(a_tok), steps=step,
+                workload="SmolLM2 widths, 4 layers, 6 requests, budget 64, max_running 4, "
+                         "pool 64 blocks")
+
+
 TRAFFIC_PROFILE = ROOT / "profiles" / "attention_config2_hbm_traffic.md"
 
 
@@ -318,6 +415,8 @@ def main():
     ap.add_argument("--steps", type=int, default=200)
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--quick", action="store_true", help="headline only: skip extras")
+    ap.add_argument("--skip-gemv", action="store_true", help="skip the GEMV table")
+    ap.add_argument("--skip-config5", action="store_true", help="skip the config-5 engine run")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--pmc-pass", action="store_true",
                     help="short run for rocprofv3 --pmc: a 512 MiB copy (calibration) then 20 "
@@ -343,6 +442,9 @@ def main():
     ctx = K.Context(0)
     if args.config5_only:
         r5 = engine_bench(ctx, K, torch)
+        r5["checksum_parity"] = config5_checksum_parity(ctx, K, torch)
+        if not args.no_cpu:
+            r5["cpu_baseline"] = config5_cpu_baseline()
         ctx.close()
         print(json.dumps(r5), flush=True)
         return
@@ -445,11 +547,18 @@ def main():
 
         sys.path.insert(0, str(ROOT / "oracle"))
         import oracle as oracle_mod
-        extras["gemv"] = gemv_bench(ctx, torch, K, oracle_mod, quick=False)
+        if not args.skip_gemv:
+            extras["gemv"] = gemv_bench(ctx, torch, K, oracle_mod, quick=False)
         extras["copy_kernel_gbps"] = round(copy_bandwidth(torch), 1)
         torch.cuda.empty_cache()
+    if not args.quick and not args.skip_config5:
         extras["config5_engine"] = engine_bench(ctx, K, torch)
         log(f"config5: {extras['config5_engine']}")
+        extras["config5_engine"]["checksum_parity"] = config5_checksum_parity(ctx, K, torch)
+        log(f"config5 parity: {extras['config5_engine']['checksum_parity']}")
+        if not args.no_cpu:
+            extras["config5_engine"]["cpu_baseline"] = config5_cpu_baseline()
+            log(f"config5 cpu: {extras['config5_engine']['cpu_baseline']}")
 
     cpu = None if args.no_cpu else cpu_baseline(head[0])
     if cpu:

@@ -97,16 +97,15 @@ struct SeqTable {
 
 __device__ __forceinline__ bool is_chunk_seq(const AttnArgs& a, int32_t ql) { return a.use_mfma && ql > 1; }
 
-// Partition size of a sequence's rows: MFMA chunk rows use larger partitions (their
-// work items are already 64 rows wide), decode rows the split-K partition.
-__device__ __forceinline__ uint32_t part_of(const AttnArgs& a, int32_t ql) {
-    return is_chunk_seq(a, ql) ? a.chunk_part : a.part_size;
+// Partition size of a sequence's rows: MFMA chunk rows use their own partition
+// (their work items are already 64 rows wide), decode rows the split-K partition.
+__device__ __forceinline__ uint32_t part_of(const AttnArgs& a, int32_t ql, uint32_t P) {
+    return is_chunk_seq(a, ql) ? a.chunk_part : P;
 }
 
-// Items of one sequence for this kernel: per 16-row tile (chunk) or per row (decode),
-// ceil(limit / P) partitions of the tile's last row / the row.
-__device__ uint32_t seq_items(const AttnArgs& a, int32_t ql, int32_t ctx, bool chunk) {
-    const uint32_t P = chunk ? a.chunk_part : a.part_size;
+// Items of one sequence for this kernel: per 64-row tile (chunk) or per row
+// (decode), ceil(limit / P) partitions of the tile's last row / the row.
+__device__ uint32_t seq_items(const AttnArgs& a, int32_t ql, int32_t ctx, bool chunk, uint32_t P) {
     uint32_t n = 0;
     if (chunk) {
         for (int32_t i0 = 0; i0 < ql; i0 += kChunkBlockRows)
@@ -136,7 +135,7 @@ __device__ void load_seq_table(const AttnArgs& a, SeqTable& st) {
         if (static_cast<uint32_t>(ctx) > a.capacity) flags |= KANSO_DEV_CONTEXT_OVERFLOW;
         if (ql > ctx) flags |= KANSO_DEV_QUERY_OVERFLOW;
         const bool chunk = is_chunk_seq(a, ql);
-        run += chunk == CHUNK ? seq_items(a, ql, ctx, chunk) : 0u;
+        run += chunk == CHUNK ? seq_items(a, ql, ctx, chunk, CHUNK ? a.chunk_part : a.part_size) : 0u;
         st.pre[s + 1] = run;  // inclusive within this thread's segment
     }
     if (!CHUNK && flags && blockIdx.x == 0) raise_status(a.status, flags);
@@ -435,8 +434,8 @@ __device__ __forceinline__ void decode_compute(const AttnArgs& a, const PartView
 }
 
 template <int D, int GMAX, int KVT, int NL, int NB, bool BUF>
-__device__ void decode_item(const AttnArgs& a, const PoolRsrc& rs, uint32_t row, uint32_t part, uint32_t seq,
-                            uint32_t kvh, int lane) {
+__device__ void decode_item(const AttnArgs& a, const PoolRsrc& rs, uint32_t row, uint32_t part, uint32_t P,
+                            uint32_t seq, uint32_t kvh, int lane) {
     constexpr int LPT = D / 4;
     constexpr int TT = (kWave / LPT) * NL;
     const int ts = lane / LPT, dl = lane % LPT;
@@ -444,8 +443,8 @@ __device__ void decode_item(const AttnArgs& a, const PoolRsrc& rs, uint32_t row,
     const int32_t ql = a.cu[seq + 1] - a.cu[seq];
     const uint32_t limit = row_limit(static_cast<int32_t>(a.ctx_lens[seq]), ql,
                                      static_cast<int32_t>(row) - a.cu[seq], a.capacity);
-    const uint32_t t_begin = part * a.part_size;
-    const uint32_t t_end = min(t_begin + a.part_size, limit);
+    const uint32_t t_begin = part * P;
+    const uint32_t t_end = min(t_begin + P, limit);
     const PartView pv = load_part(a, seq, t_begin, t_end, lane);
 
     float4 qv[GMAX], acc[GMAX];
@@ -833,7 +832,8 @@ __global__ __launch_bounds__(kThreads, 2) void attn_main(AttnArgs a) {
                 local -= np;
             }
         }
-        decode_item<D, GMAX, KVT, NL, NB, BUF>(a, rs, static_cast<uint32_t>(st.cu[s] + i), local, s, kvh, lane);
+        decode_item<D, GMAX, KVT, NL, NB, BUF>(a, rs, static_cast<uint32_t>(st.cu[s] + i), local, a.part_size, s,
+                                               kvh, lane);
     }
 }
 
@@ -867,7 +867,7 @@ __global__ __launch_bounds__(kThreads) void attn_reduce(AttnArgs a) {
         }
         const int32_t ql = st.cu[lo + 1] - st.cu[lo];
         const uint32_t lim = row_limit(st.ctx[lo], ql, static_cast<int32_t>(row) - st.cu[lo], a.capacity);
-        const uint32_t np = ceil_div(lim, part_of(a, ql));
+        const uint32_t np = ceil_div(lim, part_of(a, ql, a.part_size));
         if (np > 1) merge_partials<D, N4, LPT>(a, static_cast<size_t>(row) * a.num_heads + h, np, sub, lane);
     }
 }
@@ -943,18 +943,20 @@ bool head_dim_supported(uint32_t d) {
     return d == 4 || d == 8 || d == 16 || d == 32 || d == 64 || d == 128 || d == 256;
 }
 
-// Partition size. Every partial a row is split into costs a write, a read and a
-// merge, so partitions are as long as occupancy allows: the largest of 512, 256,
-// 128, 64 tokens for which the decode items (one per sequence, KV head and
-// partition of a context assumed half the table capacity, the only context size
-// the host knows without reading device data) still number at least half the
-// waves the grid keeps resident (measured on the config-2 batch: 512 beats 256 by
-// 5% and 768+ starves the machine). Capped so a partition touches at most 62
-// table entries (one register lane each).
+// Decode partition. Every partial a row is split into costs a write, a read and a
+// merge, so partitions are as long as the occupancy allows: the largest of 512,
+// 256, 128, 64 tokens for which the decode items (sequences x KV heads x
+// partitions of a context assumed to be half the table capacity, the only context
+// size known on the host without reading device data) still reach one per
+// resident wave of one workgroup per CU, times four for 1-byte pools (whose items
+// move a quarter of the bytes). Calibrated on the BASELINE batches (config 2: 512
+// beats 256 by 5%; config 1: 64; config 3: 128). A device-side choice from the
+// actual contexts was measured too: its extra pass cost more than it saved.
+// Capped so a partition touches at most 62 table entries (one register lane each).
 uint32_t choose_partition(const kanso_ctx* ctx, uint32_t seqs, uint32_t kv_heads, uint32_t capacity,
-                          uint32_t block_size) {
+                          uint32_t block_size, uint32_t elem_bytes) {
     uint32_t P = 2 * kRefPartition;
-    const uint64_t target = static_cast<uint64_t>(ctx->num_cus) * kWaves;  // 2 WGs/CU resident, half of them
+    const uint64_t target = static_cast<uint64_t>(ctx->num_cus) * kWaves * (elem_bytes >= 4 ? 1 : 4);
     const uint32_t half_ctx = std::max(capacity / 2, 1u);
     while (P > 64 && static_cast<uint64_t>(seqs) * kv_heads * ((half_ctx + P - 1) / P) < target) P /= 2;
     while (P > 32 && P > 62u * block_size) P /= 2;
@@ -1015,8 +1017,7 @@ int run_ragged(kanso_ctx* ctx, const kanso_ragged_attention_params* p, const flo
     }
     const uint32_t capacity = static_cast<uint32_t>(cap64);
     const uint32_t T = p->total_q;
-    uint32_t P = choose_partition(ctx, S, HKV, capacity, p->block_size);
-    if (const char* v = std::getenv("KANSO_ATTN_PART")) P = static_cast<uint32_t>(std::atoi(v));
+    const uint32_t P = choose_partition(ctx, S, HKV, capacity, p->block_size, p->kv_dtype == KANSO_KV_F32 ? 4 : 1);
     const uint32_t max_parts = (capacity + P - 1) / P;
     const uint64_t partial_elems = static_cast<uint64_t>(T) * H * max_parts * D;
     if (partial_elems > (1ull << 31)) {
@@ -1057,9 +1058,7 @@ int run_ragged(kanso_ctx* ctx, const kanso_ragged_attention_params* p, const flo
     a.max_blocks = p->max_num_blocks_per_seq;
     a.num_blocks = p->num_blocks ? p->num_blocks : 0xffffffffu;
     a.part_size = P;
-    uint32_t cp = 256;
-    while (cp > P && cp > 62u * p->block_size) cp /= 2;
-    a.chunk_part = std::max(cp, P);
+    a.chunk_part = P;  // chunk items are 64 rows wide: the longest partition
     a.max_parts = max_parts;
     a.total_q = T;
     a.capacity = capacity;
@@ -1080,14 +1079,6 @@ int run_ragged(kanso_ctx* ctx, const kanso_ragged_attention_params* p, const flo
     a.use_mfma = (D == 64 && G <= 4 && max_q > 1 && buf) ? 1u : 0u;
     a.head_major = p->pool_layout == KANSO_POOL_HEAD_MAJOR ? 1u : 0u;
     Stage1Fn main_fn = pick_main_kv(p->kv_dtype, D, G, buf);
-    if (const char* v = std::getenv("KANSO_ATTN_VARIANT"); v && D == 64 && G == 3 && buf &&
-                                                            p->kv_dtype == KANSO_KV_F32) {
-        const int var = std::atoi(v);
-        if (var == 1) main_fn = attn_main<64, 3, KANSO_KV_F32, true, 3, 8, 3>;
-        if (var == 2) main_fn = attn_main<64, 3, KANSO_KV_F32, true, 3, 12, 2>;
-        if (var == 3) main_fn = attn_main<64, 3, KANSO_KV_F32, true, 3, 4, 3>;
-        if (var == 4) main_fn = attn_main<64, 3, KANSO_KV_F32, true, 3, 4, 4>;
-    }
     Stage1Fn reduce = pick_reduce(D);
     if (!main_fn || !reduce) {
         set_error("%s: no kernel for head_dim %u / kv_dtype %u", who, D, p->kv_dtype);
