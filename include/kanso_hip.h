@@ -211,8 +211,9 @@ int kanso_gemv_q8_0(kanso_ctx* ctx, const void* w, const float* x, float* y,
                     kanso_stream_t stream);
 
 /* Same with W in GGUF block_q4_K layout ([out][in/256] blocks of {f16 d; f16 dmin;
- * u8 scales[12]; u8 qs[128]}, 144 B); in % 256 == 0. Dequantization semantics of
- * src/quant/q4_k.rs:16-55. */
+ * u8 scales[12]; u8 qs[128]}, 144 B); in % 256 == 0, batch >= 1, w and x 16-byte
+ * aligned. Dequantization semantics of src/quant/q4_k.rs:16-55 (d1 q - m1 per
+ * 32-element sub-block), on the same matrix-core kernel as kanso_gemv_q8_0. */
 int kanso_gemv_q4_k(kanso_ctx* ctx, const void* w, const float* x, float* y,
                     uint32_t out_features, uint32_t in_features, uint32_t batch,
                     kanso_stream_t stream);

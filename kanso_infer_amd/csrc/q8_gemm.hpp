@@ -1,5 +1,5 @@
-// q8_gemm.hpp — dequant-on-the-fly Q8_0 matrix products on the bf16 matrix cores,
-// with the fused prologues / epilogues the decoder layer needs.
+// q8_gemm.hpp — dequant-on-the-fly Q8_0 (and Q4_K) matrix products on the bf16
+// matrix cores, with the fused prologues / epilogues the decoder layer needs.
 //
 // Arithmetic. Y[t][r] = sum_b d[r][b] * sum_{i<32} q[r][32b+i] * x[t][32b+i]
 // (scalar_gemv_q8_0, src/quant/q8_0.rs:51-93). One v_mfma_f32_16x16x32_bf16 has
@@ -22,6 +22,8 @@
 // Weight layouts:
 //   GGUF   : [rows][in/32] blocks {f16 d; i8 qs[32]} (34 B), the format the
 //            reference reads (src/quant/mod.rs:1-17);
+//   Q4_K   : GGUF block_q4_K rows (WQ4K: one 32-element sub-block per k-block, an
+//            affine block d q - m, the m term from a product against ones);
 //   packed : [groups][in/32] tiles of 544 B, one per (16-row group, block):
 //            qs[kq][row][8] (512 B: lane l's 8 bytes are at 8l) then d[16] f16.
 //            Rows past the matrix are zero. Produced by kanso_q8_0_pack; the
@@ -52,6 +54,12 @@ __device__ __forceinline__ bf16x8 i8x8_to_bf16(uint64_t q) {
     return __builtin_bit_cast(bf16x8, w);
 }
 
+__device__ __forceinline__ bf16x8 bf16_ones() {
+    const uint32_t one2 = 0x3f803f80u;  // two bf16 1.0
+    const uint32_t w[4] = {one2, one2, one2, one2};
+    return __builtin_bit_cast(bf16x8, w);
+}
+
 struct Bf16Pair {
     bf16x8 hi, lo;
 };
@@ -72,7 +80,9 @@ __device__ __forceinline__ Bf16Pair split_bf16(const float (&x)[8]) {
 struct WPacked {
     const uint8_t* w;
     uint32_t nb;  // in / 32
-    __device__ __forceinline__ void load(uint32_t g, uint32_t b, int lane, uint64_t& q, float& d) const {
+    static constexpr bool kHasMin = false;
+    __device__ __forceinline__ void load(uint32_t g, uint32_t b, int lane, uint64_t& q, float& d, float& m) const {
+        m = 0.f;
         const uint8_t* p = w + (static_cast<size_t>(g) * nb + b) * kPackedTileBytes;
         q = *reinterpret_cast<const uint64_t*>(p + 8 * lane);
         d = f16_bits_to_f32(*reinterpret_cast<const uint16_t*>(p + 512 + 2 * (lane & 15)));
@@ -83,7 +93,9 @@ struct WGguf {
     const uint8_t* w;
     uint32_t nb;
     uint32_t rows;
-    __device__ __forceinline__ void load(uint32_t g, uint32_t b, int lane, uint64_t& q, float& d) const {
+    static constexpr bool kHasMin = false;
+    __device__ __forceinline__ void load(uint32_t g, uint32_t b, int lane, uint64_t& q, float& d, float& m) const {
+        m = 0.f;
         const uint32_t row = g * 16 + (lane & 15);
         if (row >= rows) {
             q = 0;
@@ -96,6 +108,49 @@ struct WGguf {
         const uint16_t* qp = p + 1 + 4 * (lane >> 4);
         q = static_cast<uint64_t>(qp[0]) | (static_cast<uint64_t>(qp[1]) << 16) |
             (static_cast<uint64_t>(qp[2]) << 32) | (static_cast<uint64_t>(qp[3]) << 48);
+    }
+};
+
+// GGUF block_q4_K rows ([rows][in/256] x 144 B: f16 d, f16 dmin, 12 packed 6-bit
+// scale/min bytes, 128 nibble bytes). k-block b is 32-element sub-block b % 8 of
+// super-block b / 8: weights d * sc * q - dmin * m (BlockQ4_K::dequantize,
+// src/quant/q4_k.rs:30-55, with get_scale_min_k4, :16-26). Sub-blocks 2j and 2j+1
+// share the 32 bytes qs[32j ..): low nibbles for 2j, high for 2j+1.
+struct WQ4K {
+    static constexpr bool kHasMin = true;
+    const uint8_t* w;
+    uint32_t nsb;  // in / 256
+    uint32_t rows;
+    __device__ __forceinline__ void load(uint32_t g, uint32_t b, int lane, uint64_t& q, float& d, float& m) const {
+        const uint32_t row = g * 16 + (lane & 15);
+        if (row >= rows) {
+            q = 0;
+            d = 0.f;
+            m = 0.f;
+            return;
+        }
+        const uint8_t* blk = w + (static_cast<size_t>(row) * nsb + b / 8) * 144;
+        const uint32_t sub = b % 8, j = sub / 2;
+        const uint32_t dd = *reinterpret_cast<const uint32_t*>(blk);
+        const uint32_t s0 = *reinterpret_cast<const uint32_t*>(blk + 4);
+        const uint32_t s1 = *reinterpret_cast<const uint32_t*>(blk + 8);
+        const uint32_t s2 = *reinterpret_cast<const uint32_t*>(blk + 12);
+        const uint64_t raw = *reinterpret_cast<const uint64_t*>(blk + 16 + 32 * j + 8 * (lane >> 4));
+        const auto byte = [&](uint32_t i) -> uint32_t {
+            const uint32_t word = i < 4 ? s0 : (i < 8 ? s1 : s2);
+            return (word >> (8 * (i % 4))) & 0xff;
+        };
+        uint32_t sc, mn;
+        if (sub < 4) {
+            sc = byte(sub) & 63;
+            mn = byte(sub + 4) & 63;
+        } else {
+            sc = (byte(sub + 4) & 0xF) | ((byte(sub - 4) >> 6) << 4);
+            mn = (byte(sub + 4) >> 4) | ((byte(sub) >> 6) << 4);
+        }
+        d = f16_bits_to_f32(static_cast<uint16_t>(dd & 0xffff)) * static_cast<float>(sc);
+        m = f16_bits_to_f32(static_cast<uint16_t>(dd >> 16)) * static_cast<float>(mn);
+        q = (sub & 1) ? ((raw >> 4) & 0x0f0f0f0f0f0f0f0full) : (raw & 0x0f0f0f0f0f0f0f0full);
     }
 };
 
@@ -165,14 +220,14 @@ __global__ __launch_bounds__(KS * kWave) void q8_gemm_kernel(WL wl, XIn xa, Epi 
     }
     for (uint32_t b0 = wv; b0 < nb; b0 += KS * U) {
         uint64_t q0[U], q1[U];
-        float d0[U], d1[U];
+        float d0[U], d1[U], m0[U], m1[U];
         float4 xv[U][MT][2], nv[U][2];
 #pragma unroll
         for (int u = 0; u < U; ++u) {
             const uint32_t b = b0 + u * KS;
             if (b < nb) {
-                wl.load(g0, b, lane, q0[u], d0[u]);
-                wl.load(g1, b, lane, q1[u], d1[u]);
+                wl.load(g0, b, lane, q0[u], d0[u], m0[u]);
+                wl.load(g1, b, lane, q1[u], d1[u], m1[u]);
                 const uint32_t k = 32 * b + 8 * kq;
 #pragma unroll
                 for (int i = 0; i < MT; ++i) {
@@ -209,10 +264,20 @@ __global__ __launch_bounds__(KS * kWave) void q8_gemm_kernel(WL wl, XIn xa, Epi 
                 const floatx4 z = {0.f, 0.f, 0.f, 0.f};
                 floatx4 t = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a.hi, w0, z, 0, 0, 0);
                 t = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a.lo, w0, t, 0, 0, 0);
-                acc[0][i] += d0[u] * t;
-                t = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a.hi, w1, z, 0, 0, 0);
-                t = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a.lo, w1, t, 0, 0, 0);
-                acc[1][i] += d1[u] * t;
+                floatx4 t1 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a.hi, w1, z, 0, 0, 0);
+                t1 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a.lo, w1, t1, 0, 0, 0);
+                if constexpr (WL::kHasMin) {
+                    // block-wise affine weights w = d q - m: sum w x = d (sum q x) - m (sum x);
+                    // sum x per token comes out of one more product, against ones, already
+                    // in the accumulator layout.
+                    floatx4 sx = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a.hi, bf16_ones(), z, 0, 0, 0);
+                    sx = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a.lo, bf16_ones(), sx, 0, 0, 0);
+                    acc[0][i] += d0[u] * t - m0[u] * sx;
+                    acc[1][i] += d1[u] * t1 - m1[u] * sx;
+                } else {
+                    acc[0][i] += d0[u] * t;
+                    acc[1][i] += d1[u] * t1;
+                }
             }
         }
     }
