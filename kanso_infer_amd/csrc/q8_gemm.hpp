@@ -190,7 +190,11 @@ struct XIn {
 // and the sum of squares of each token row is accumulated from the very x values
 // the waves load, so no pass over x precedes the main loop. The division by rms
 // happens on the reduced outputs.
-template <int KS, int U, int MT, class WL, class Epi>
+//
+// The loads of a round are branch-free (a block past the row is replaced by the
+// last block, its scale forced to 0): a branch around them would make the
+// compiler wait for each block's loads at the join, serialising the round.
+template <int KS, int U, int MT, bool NORM, class WL, class Epi>
 __global__ __launch_bounds__(KS * kWave) void q8_gemm_kernel(WL wl, XIn xa, Epi epi) {
     __shared__ floatx4 s_part[KS][2][MT][kWave];
     __shared__ float s_ss[KS][MT][16];
@@ -199,7 +203,7 @@ __global__ __launch_bounds__(KS * kWave) void q8_gemm_kernel(WL wl, XIn xa, Epi 
     const uint32_t p = blockIdx.x;
     const uint32_t t0 = blockIdx.y * 16 * MT;
     const uint32_t nb = xa.in / 32;
-    const bool norm = xa.norm_w != nullptr;
+    constexpr bool norm = NORM;
     uint32_t g0, g1;
     epi.groups(p, g0, g1);
     const float* xr[MT];
@@ -222,27 +226,37 @@ __global__ __launch_bounds__(KS * kWave) void q8_gemm_kernel(WL wl, XIn xa, Epi 
         uint64_t q0[U], q1[U];
         float d0[U], d1[U], m0[U], m1[U];
         float4 xv[U][MT][2], nv[U][2];
+        bool live[U];
 #pragma unroll
         for (int u = 0; u < U; ++u) {
-            const uint32_t b = b0 + u * KS;
-            if (b < nb) {
-                wl.load(g0, b, lane, q0[u], d0[u], m0[u]);
-                wl.load(g1, b, lane, q1[u], d1[u], m1[u]);
-                const uint32_t k = 32 * b + 8 * kq;
+            live[u] = b0 + u * KS < nb;
+            const uint32_t b = live[u] ? b0 + u * KS : nb - 1;
+            wl.load(g0, b, lane, q0[u], d0[u], m0[u]);
+            wl.load(g1, b, lane, q1[u], d1[u], m1[u]);
+            const uint32_t k = 32 * b + 8 * kq;
 #pragma unroll
-                for (int i = 0; i < MT; ++i) {
-                    xv[u][i][0] = *reinterpret_cast<const float4*>(xr[i] + k);
-                    xv[u][i][1] = *reinterpret_cast<const float4*>(xr[i] + k + 4);
-                }
-                if (norm) {
-                    nv[u][0] = *reinterpret_cast<const float4*>(xa.norm_w + k);
-                    nv[u][1] = *reinterpret_cast<const float4*>(xa.norm_w + k + 4);
-                }
+            for (int i = 0; i < MT; ++i) {
+                xv[u][i][0] = *reinterpret_cast<const float4*>(xr[i] + k);
+                xv[u][i][1] = *reinterpret_cast<const float4*>(xr[i] + k + 4);
+            }
+            if constexpr (NORM) {
+                nv[u][0] = *reinterpret_cast<const float4*>(xa.norm_w + k);
+                nv[u][1] = *reinterpret_cast<const float4*>(xa.norm_w + k + 4);
+            } else {
+                nv[u][0] = nv[u][1] = make_float4(0.f, 0.f, 0.f, 0.f);
             }
         }
+        // keep every load of the round ahead of the arithmetic: the scheduler would
+        // otherwise sink later blocks' loads below earlier blocks' products
+        __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
         for (int u = 0; u < U; ++u) {
-            if (b0 + u * KS >= nb) break;
+            // a repeated block contributes nothing: zero scale and min, no squares
+            d0[u] = live[u] ? d0[u] : 0.f;
+            d1[u] = live[u] ? d1[u] : 0.f;
+            m0[u] = live[u] ? m0[u] : 0.f;
+            m1[u] = live[u] ? m1[u] : 0.f;
+            const float sq = live[u] ? 1.f : 0.f;
             const bf16x8 w0 = i8x8_to_bf16(q0[u]), w1 = i8x8_to_bf16(q1[u]);
             const float nw[8] = {nv[u][0].x, nv[u][0].y, nv[u][0].z, nv[u][0].w,
                                  nv[u][1].x, nv[u][1].y, nv[u][1].z, nv[u][1].w};
@@ -253,12 +267,14 @@ __global__ __launch_bounds__(KS * kWave) void q8_gemm_kernel(WL wl, XIn xa, Epi 
                 if (!mok[i]) {
 #pragma unroll
                     for (int j = 0; j < 8; ++j) xs[j] = 0.f;
-                } else if (norm) {
+                } else if constexpr (NORM) {
+                    float s2 = 0.f;
 #pragma unroll
                     for (int j = 0; j < 8; ++j) {
-                        ss[i] += xs[j] * xs[j];
+                        s2 += xs[j] * xs[j];
                         xs[j] *= nw[j];
                     }
+                    ss[i] += sq * s2;
                 }
                 const Bf16Pair a = split_bf16(xs);
                 const floatx4 z = {0.f, 0.f, 0.f, 0.f};
@@ -478,27 +494,35 @@ struct EpiArgmax {
 // Launch helper: 16, 32 or 64 tokens per workgroup (MT = 1, 2, 4), K split over
 // 8 waves (so a token's result never depends on the batch size), U blocks of
 // loads in flight per wave: a whole 960-wide row in one round.
-template <int MT, class WL, class Epi>
+template <int MT, bool NORM, class WL, class Epi>
 inline void launch_mt(const WL& wl, const XIn& xa, const Epi& epi, uint32_t pairs, uint32_t nb, hipStream_t s) {
     const dim3 grid(pairs, (xa.T + 16 * MT - 1) / (16 * MT));
     if constexpr (MT == 4)  // 64 tokens of x per block already fill the registers
-        hipLaunchKernelGGL((q8_gemm_kernel<8, 2, MT, WL, Epi>), grid, dim3(8 * kWave), 0, s, wl, xa, epi);
+        hipLaunchKernelGGL((q8_gemm_kernel<8, 2, MT, NORM, WL, Epi>), grid, dim3(8 * kWave), 0, s, wl, xa, epi);
     else if (nb <= 32)
-        hipLaunchKernelGGL((q8_gemm_kernel<8, 4, MT, WL, Epi>), grid, dim3(8 * kWave), 0, s, wl, xa, epi);
+        hipLaunchKernelGGL((q8_gemm_kernel<8, 4, MT, NORM, WL, Epi>), grid, dim3(8 * kWave), 0, s, wl, xa, epi);
     else
-        hipLaunchKernelGGL((q8_gemm_kernel<8, 5, MT, WL, Epi>), grid, dim3(8 * kWave), 0, s, wl, xa, epi);
+        hipLaunchKernelGGL((q8_gemm_kernel<8, 5, MT, NORM, WL, Epi>), grid, dim3(8 * kWave), 0, s, wl, xa, epi);
+}
+
+template <bool NORM, class WL, class Epi>
+inline void launch_norm(const WL& wl, const XIn& xa, const Epi& epi, uint32_t pairs, uint32_t nb, hipStream_t s) {
+    if (xa.T <= 16)
+        launch_mt<1, NORM>(wl, xa, epi, pairs, nb, s);
+    else if (xa.T <= 32)
+        launch_mt<2, NORM>(wl, xa, epi, pairs, nb, s);
+    else
+        launch_mt<4, NORM>(wl, xa, epi, pairs, nb, s);
 }
 
 template <class WL, class Epi>
 inline int launch_q8_gemm(const WL& wl, const XIn& xa, const Epi& epi, uint32_t pairs, hipStream_t s) {
     if (xa.T == 0 || pairs == 0) return KANSO_OK;
     const uint32_t nb = xa.in / 32;
-    if (xa.T <= 16)
-        launch_mt<1>(wl, xa, epi, pairs, nb, s);
-    else if (xa.T <= 32)
-        launch_mt<2>(wl, xa, epi, pairs, nb, s);
+    if (xa.norm_w)
+        launch_norm<true>(wl, xa, epi, pairs, nb, s);
     else
-        launch_mt<4>(wl, xa, epi, pairs, nb, s);
+        launch_norm<false>(wl, xa, epi, pairs, nb, s);
     KANSO_LAUNCH_CHECK();
     return KANSO_OK;
 }
