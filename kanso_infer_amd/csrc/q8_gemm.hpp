@@ -214,6 +214,10 @@ __global__ __launch_bounds__(KS * kWave) void q8_gemm_kernel(WL wl, XIn xa, Epi 
         mok[i] = m < xa.T;
         xr[i] = xa.row(mok[i] ? m : t0);
     }
+    // the epilogue's own operands (residual rows, RoPE tables, slots) are requested
+    // now, so their latency hides under the main loop
+    typename Epi::Pre pre{};
+    if (wv < MT) pre = epi.pre(p, lane, t0 + 16 * wv + 4 * kq, xa.T);
     floatx4 acc[2][MT];
     float ss[MT];
 #pragma unroll
@@ -328,7 +332,7 @@ __global__ __launch_bounds__(KS * kWave) void q8_gemm_kernel(WL wl, XIn xa, Epi 
                 v1[r] /= rms;
             }
         }
-        epi.apply(p, lane, t0 + 16 * i + 4 * kq, xa.T, v0, v1);
+        epi.apply(p, lane, t0 + 16 * i + 4 * kq, xa.T, v0, v1, pre);
     }
 }
 
@@ -344,16 +348,34 @@ struct EpiStore {
         g0 = 2 * p;
         g1 = 2 * p + 1;
     }
+    struct Pre {
+        float a0[4], a1[4];  // residual values (ADD)
+    };
+    __device__ __forceinline__ Pre pre(uint32_t p, int lane, uint32_t m0, uint32_t T) const {
+        Pre r{};
+        if constexpr (ADD) {
+            const uint32_t r0 = 32 * p + (lane & 15), r1 = r0 + 16;
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const uint32_t m = m0 + i;
+                if (m >= T) break;
+                const float* yr = y + static_cast<size_t>(m) * ldy;
+                if (r0 < rows) r.a0[i] = yr[r0];
+                if (r1 < rows) r.a1[i] = yr[r1];
+            }
+        }
+        return r;
+    }
     __device__ __forceinline__ void apply(uint32_t p, int lane, uint32_t m0, uint32_t T, const floatx4& v0,
-                                          const floatx4& v1) const {
+                                          const floatx4& v1, const Pre& pr) const {
         const uint32_t r0 = 32 * p + (lane & 15), r1 = r0 + 16;
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
             const uint32_t m = m0 + r;
             if (m >= T) break;
             float* yr = y + static_cast<size_t>(m) * ldy;
-            if (r0 < rows) yr[r0] = ADD ? yr[r0] + v0[r] : v0[r];
-            if (r1 < rows) yr[r1] = ADD ? yr[r1] + v1[r] : v1[r];
+            if (r0 < rows) yr[r0] = ADD ? pr.a0[r] + v0[r] : v0[r];
+            if (r1 < rows) yr[r1] = ADD ? pr.a1[r] + v1[r] : v1[r];
         }
     }
 };
@@ -369,8 +391,10 @@ struct EpiSwiGLU {
         g0 = 2 * p;
         g1 = 2 * p + 1;
     }
+    struct Pre {};
+    __device__ __forceinline__ Pre pre(uint32_t, int, uint32_t, uint32_t) const { return {}; }
     __device__ __forceinline__ void apply(uint32_t p, int lane, uint32_t m0, uint32_t T, const floatx4& g,
-                                          const floatx4& u) const {
+                                          const floatx4& u, const Pre&) const {
         const uint32_t j = 16 * p + (lane & 15);
         if (j >= inter) return;
 #pragma unroll
@@ -404,8 +428,34 @@ struct EpiQkvRope {
         g0 = 4 * (p / 2) + (p % 2);
         g1 = g0 + 2;
     }
+    struct Pre {
+        float c[4], s[4];  // RoPE cos / sin at the token's position (Q and K heads)
+        int64_t slot[4];   // pool row (K and V heads)
+    };
+    __device__ __forceinline__ Pre pre(uint32_t p, int lane, uint32_t m0, uint32_t T) const {
+        Pre r{};
+        const uint32_t head = p / 2;
+        const uint32_t d = 16 * (p % 2) + (lane & 15);
+        const bool is_q = head < num_heads, is_v = head >= num_heads + num_kv_heads;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const uint32_t m = m0 + i;
+            if (m >= T) break;
+            if (!is_v) {
+                uint32_t pos = static_cast<uint32_t>(positions[m]);
+                if (pos >= max_pos) {
+                    raise_status(status, KANSO_DEV_POSITION_OOB);
+                    pos = max_pos - 1;
+                }
+                r.c[i] = cos_t[static_cast<size_t>(pos) * 32 + d];
+                r.s[i] = sin_t[static_cast<size_t>(pos) * 32 + d];
+            }
+            if (!is_q) r.slot[i] = slots[m];
+        }
+        return r;
+    }
     __device__ __forceinline__ void apply(uint32_t p, int lane, uint32_t m0, uint32_t T, const floatx4& x1,
-                                          const floatx4& x2) const {
+                                          const floatx4& x2, const Pre& pr) const {
         const uint32_t head = p / 2;
         const uint32_t d = 16 * (p % 2) + (lane & 15);
         const bool is_q = head < num_heads, is_v = head >= num_heads + num_kv_heads;
@@ -415,13 +465,7 @@ struct EpiQkvRope {
             if (m >= T) break;
             float a = x1[r], b = x2[r];
             if (!is_v) {
-                uint32_t pos = static_cast<uint32_t>(positions[m]);
-                if (pos >= max_pos) {
-                    raise_status(status, KANSO_DEV_POSITION_OOB);
-                    pos = max_pos - 1;
-                }
-                const float c = cos_t[static_cast<size_t>(pos) * 32 + d];
-                const float s = sin_t[static_cast<size_t>(pos) * 32 + d];
+                const float c = pr.c[r], s = pr.s[r];
                 const float ra = a * c - b * s;
                 const float rb = a * s + b * c;
                 a = ra;
@@ -433,7 +477,7 @@ struct EpiQkvRope {
                 qr[d + 32] = b;
                 continue;
             }
-            const int64_t slot = slots[m];
+            const int64_t slot = pr.slot[r];
             if (slot < 0 || slot >= num_slots) {
                 raise_status(status, KANSO_DEV_SLOT_OOB);
                 continue;
@@ -465,8 +509,10 @@ struct EpiArgmax {
         g0 = 2 * p;
         g1 = 2 * p + 1;
     }
+    struct Pre {};
+    __device__ __forceinline__ Pre pre(uint32_t, int, uint32_t, uint32_t) const { return {}; }
     __device__ __forceinline__ void apply(uint32_t p, int lane, uint32_t m0, uint32_t T, const floatx4& v0,
-                                          const floatx4& v1) const {
+                                          const floatx4& v1, const Pre&) const {
         const uint32_t r0 = 32 * p + (lane & 15), r1 = r0 + 16;
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
@@ -491,9 +537,11 @@ struct EpiArgmax {
     }
 };
 
-// Launch helper: 16, 32 or 64 tokens per workgroup (MT = 1, 2, 4), K split over
-// 8 waves (so a token's result never depends on the batch size), U blocks of
-// loads in flight per wave: a whole 960-wide row in one round.
+// Launch helper: K split over 8 waves (so a token's result never depends on the
+// batch size), U blocks of loads in flight per wave so that a whole row (960 or
+// 2560 wide) is requested in one round. Up to 256 tokens a workgroup takes 16 of
+// them (MT = 1): at decode sizes more workgroups in flight beat the weight reuse
+// of wider token tiles (re-reads hit L2 / MALL); above, 64 (MT = 4).
 template <int MT, bool NORM, class WL, class Epi>
 inline void launch_mt(const WL& wl, const XIn& xa, const Epi& epi, uint32_t pairs, uint32_t nb, hipStream_t s) {
     const dim3 grid(pairs, (xa.T + 16 * MT - 1) / (16 * MT));
@@ -501,16 +549,16 @@ inline void launch_mt(const WL& wl, const XIn& xa, const Epi& epi, uint32_t pair
         hipLaunchKernelGGL((q8_gemm_kernel<8, 2, MT, NORM, WL, Epi>), grid, dim3(8 * kWave), 0, s, wl, xa, epi);
     else if (nb <= 32)
         hipLaunchKernelGGL((q8_gemm_kernel<8, 4, MT, NORM, WL, Epi>), grid, dim3(8 * kWave), 0, s, wl, xa, epi);
-    else
+    else if (NORM || nb <= 40)  // (the norm weights of 10 blocks would not fit the registers)
         hipLaunchKernelGGL((q8_gemm_kernel<8, 5, MT, NORM, WL, Epi>), grid, dim3(8 * kWave), 0, s, wl, xa, epi);
+    else if constexpr (!NORM)  // 2560-wide rows (the down projection) in one round
+        hipLaunchKernelGGL((q8_gemm_kernel<8, 10, MT, NORM, WL, Epi>), grid, dim3(8 * kWave), 0, s, wl, xa, epi);
 }
 
 template <bool NORM, class WL, class Epi>
 inline void launch_norm(const WL& wl, const XIn& xa, const Epi& epi, uint32_t pairs, uint32_t nb, hipStream_t s) {
-    if (xa.T <= 16)
+    if (xa.T <= 256)
         launch_mt<1, NORM>(wl, xa, epi, pairs, nb, s);
-    else if (xa.T <= 32)
-        launch_mt<2, NORM>(wl, xa, epi, pairs, nb, s);
     else
         launch_mt<4, NORM>(wl, xa, epi, pairs, nb, s);
 }
