@@ -41,16 +41,21 @@ __global__ __launch_bounds__(256) void embed_q8_0_kernel(const uint8_t* __restri
     }
 }
 
-__global__ void zero_u64_kernel(unsigned long long* p, uint32_t n) {
-    const uint32_t i = blockIdx.x * blockDim.x + threadIdx.x;
-    if (i < n) p[i] = 0;
-}
-
-__global__ void argmax_finish_kernel(const unsigned long long* keys, uint32_t n, uint32_t* tokens) {
-    const uint32_t i = blockIdx.x * blockDim.x + threadIdx.x;
-    if (i < n) {
-        const unsigned long long k = keys[i];
-        tokens[i] = k ? 0xffffffffu - static_cast<uint32_t>(k & 0xffffffffu) : 0u;
+// One workgroup per token: the maximum of its per-pair keys (max is order-free,
+// so the token does not depend on the reduction order); key 0 = no finite logit.
+__global__ __launch_bounds__(256) void argmax_finish_kernel(const unsigned long long* keys, uint32_t pairs,
+                                                            uint32_t* tokens) {
+    __shared__ unsigned long long s_best[256 / kWave];
+    const unsigned long long* row = keys + static_cast<size_t>(blockIdx.x) * pairs;
+    unsigned long long best = 0;
+    for (uint32_t i = threadIdx.x; i < pairs; i += 256) best = max(best, row[i]);
+#pragma unroll
+    for (int o = 1; o < kWave; o <<= 1) best = max(best, static_cast<unsigned long long>(__shfl_xor(best, o, kWave)));
+    if ((threadIdx.x & (kWave - 1)) == 0) s_best[threadIdx.x / kWave] = best;
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        for (int w = 1; w < 256 / kWave; ++w) best = max(best, s_best[w]);
+        tokens[blockIdx.x] = best ? 0xffffffffu - static_cast<uint32_t>(best & 0xffffffffu) : 0u;
     }
 }
 
@@ -110,16 +115,16 @@ int op_gate_up_swiglu(const void* w, const float* x, const float* norm_w, float 
 int op_lm_head_argmax(kanso_ctx* ctx, const void* w, const float* x, const int32_t* rows, const float* norm_w,
                       float eps, uint32_t S, uint32_t hidden, uint32_t vocab, float* logits, uint32_t* tokens,
                       hipStream_t s) {
-    int rc = ensure_keys(ctx, static_cast<size_t>(S) * sizeof(unsigned long long));
+    if (S == 0) return KANSO_OK;
+    const uint32_t pairs = (vocab + 31) / 32;
+    int rc = ensure_keys(ctx, static_cast<size_t>(S) * pairs * sizeof(unsigned long long));
     if (rc) return rc;
     auto* keys = static_cast<unsigned long long*>(ctx->keys);
-    hipLaunchKernelGGL(zero_u64_kernel, dim3((S + 255) / 256), dim3(256), 0, s, keys, S);
-    KANSO_LAUNCH_CHECK();
     WPacked wl{static_cast<const uint8_t*>(w), hidden / 32};
     XIn xa{x, rows, norm_w, eps, hidden, S, hidden};
-    EpiArgmax epi{logits, vocab, vocab, keys};
-    if ((rc = launch_q8_gemm(wl, xa, epi, (vocab + 31) / 32, s))) return rc;
-    hipLaunchKernelGGL(argmax_finish_kernel, dim3((S + 255) / 256), dim3(256), 0, s, keys, S, tokens);
+    EpiArgmax epi{logits, vocab, vocab, keys, pairs};
+    if ((rc = launch_q8_gemm(wl, xa, epi, pairs, s))) return rc;
+    hipLaunchKernelGGL(argmax_finish_kernel, dim3(S), dim3(256), 0, s, keys, pairs, tokens);
     KANSO_LAUNCH_CHECK();
     return KANSO_OK;
 }

@@ -202,6 +202,8 @@ int ensure_step_buffers(kanso_model* m, uint32_t T, uint32_t S, uint32_t tables,
         m->h_next = static_cast<uint32_t*>(h);
         m->cap_tokens = t;
         m->cap_seqs = sq;
+        // per-pair argmax keys of the lm_head for every sampled row
+        if ((rc = ensure_keys(m->ctx, static_cast<size_t>(sq) * ((c.vocab + 31) / 32) * 8))) return rc;
     }
     if (tables > m->cap_tables) {
         if ((rc = dev_alloc(m, &m->tables, static_cast<size_t>(tables) * 4))) return rc;

@@ -498,13 +498,16 @@ __device__ __forceinline__ unsigned long long argmax_key(float v, uint32_t idx) 
     return (static_cast<unsigned long long>(ord) << 32) | (0xffffffffu - idx);
 }
 
-// lm_head: optional logits store, and a per-token argmax folded into keys[m]
-// with a 64-bit atomic max (order-independent, so the result is deterministic).
+// lm_head: optional logits store, and the best key of this pair's 32 rows for
+// each token stored to keys[m][p] (plain stores: a device-wide atomic per
+// workgroup and token serialises on the token's address); a second kernel takes
+// the maximum over the pairs.
 struct EpiArgmax {
     float* logits;  // may be null
     uint32_t ld;
     uint32_t rows;
-    unsigned long long* keys;
+    unsigned long long* keys;  // [T][pairs]
+    uint32_t pairs;
     __device__ __forceinline__ void groups(uint32_t p, uint32_t& g0, uint32_t& g1) const {
         g0 = 2 * p;
         g1 = 2 * p + 1;
@@ -532,7 +535,7 @@ struct EpiArgmax {
                 const unsigned long long other = __shfl_xor(key, o, kWave);
                 key = max(key, other);
             }
-            if (live && (lane & 15) == 0 && key != 0) atomicMax(keys + m, key);
+            if (live && (lane & 15) == 0) keys[static_cast<size_t>(m) * pairs + p] = key;
         }
     }
 };
