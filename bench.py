@@ -108,15 +108,19 @@ class AttnBench:
             self.call(i)
         self.ctx.check_device_status()
         torch.cuda.synchronize()
-        self.ctx.set_profiling(True)
+        # throughput: the calls alone, no per-kernel events in the timed region
         start, stop = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-        torch.cuda.synchronize()
         start.record()
         for i in range(steps):
             self.call(i)
         stop.record()
         torch.cuda.synchronize()
         total_ms = start.elapsed_time(stop)
+        # per-kernel durations: a second pass with HIP events around each launch
+        self.ctx.set_profiling(True)
+        for i in range(steps):
+            self.call(i)
+        torch.cuda.synchronize()
         k_ms, k_n = self.ctx.kernel_time("attention")
         r_ms, r_n = self.ctx.kernel_time("reduce")
         self.ctx.set_profiling(False)

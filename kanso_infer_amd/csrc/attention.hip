@@ -257,63 +257,81 @@ __device__ __forceinline__ float dot4(float4 a, float4 b) {
     return a.x * b.x + a.y * b.y + a.z * b.z + a.w * b.w;
 }
 
-// Merge of `np` partials of one (row, head) for head-dim elements [d0, d0 + 4*n4):
+// Merge of `np` partials of one (row, head) by the LPG lanes of its group:
 // out = sum_p acc_p 2^(m_p - M) / sum_p l_p 2^(m_p - M) (paged_attention_v2.metal:
-// 154-205), 1/denominator = 0 for an empty row.
-// Merge of one (row, head)'s partitions by the LPT lanes of its group (lane `sub`
-// holds output elements [4*N4*sub, 4*N4*(sub+1))). Partition statistics are read one
-// per lane and reduced across the group; partial vectors are fetched four at a time
-// so their loads overlap.
-template <int D, int N4, int LPT>
-__device__ __forceinline__ void merge_partials(const AttnArgs& a, size_t head, uint32_t np, uint32_t sub,
-                                               int lane) {
+// 154-205), 1/denominator = 0 for an empty row. LPT lanes cover a partial row
+// (lane `sub` holds elements [4*N4*sub, 4*N4*(sub+1))); the R = LPG / LPT lane
+// sets take partitions r, r + R, ..., and each issues U partial loads at once, so
+// a round requests R*U partials. LPG = 64 (R = 4 at head_dim 64) serves rows split
+// into many partitions; LPG = LPT packs several short merges into one wave.
+template <int D, int LPG>
+__device__ __forceinline__ void merge_partials(const AttnArgs& a, size_t head, uint32_t np, int lane) {
+    constexpr int LPT = D / 4 < LPG ? D / 4 : LPG;
+    constexpr int N4 = D / 4 / LPT;
+    constexpr int R = LPG / LPT;
+    constexpr int U = N4 >= 4 ? 2 : 8 / N4;
     const size_t base = head * a.max_parts;
+    const uint32_t gl = static_cast<uint32_t>(lane) % LPG;  // lane within the group
+    const uint32_t r = gl / LPT, sub = gl % LPT;
+    const uint32_t d0 = sub * 4 * N4;
+    float4 v[U][N4];
+    float2 st[U];
+    bool ok[U];
+    const auto load_round = [&](uint32_t p0) {
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+            const uint32_t p = p0 + r + R * u;
+            ok[u] = p < np;
+            const uint32_t pp = ok[u] ? p : 0;
+            st[u] = a.part_stats[base + pp];
+            const float4* src = reinterpret_cast<const float4*>(a.part_out + (base + pp) * D + d0);
+#pragma unroll
+            for (int k = 0; k < N4; ++k) v[u][k] = src[k];
+        }
+    };
+    // the first round's partials are requested together with the statistics the
+    // maximum needs, so a row of up to R*U partitions costs one memory latency
+    load_round(0);
     float M = -INFINITY;
-    for (uint32_t p = sub; p < np; p += LPT) M = fmaxf(M, a.part_stats[base + p].x);
-    M = group_max<LPT>(M);
+    for (uint32_t p = gl; p < np; p += LPG) M = fmaxf(M, a.part_stats[base + p].x);
+    M = group_max<LPG>(M);
     float4 o[N4];
 #pragma unroll
     for (int k = 0; k < N4; ++k) o[k] = make_float4(0.f, 0.f, 0.f, 0.f);
-    float L = 0.f;
-    const int gbase = lane - static_cast<int>(sub);
-    const int d0 = static_cast<int>(sub) * 4 * N4;
-    for (uint32_t p0 = 0; p0 < np; p0 += LPT) {
-        float f = 0.f;
-        if (p0 + sub < np) {
-            const float2 st = a.part_stats[base + p0 + sub];
-            f = fast_exp2(st.x - M);
-            L += st.y * f;
-        }
-        const uint32_t cnt = np - p0 < LPT ? np - p0 : LPT;
-        for (uint32_t j = 0; j < cnt; j += 4) {
-            float4 v[4][N4];
-            float fj[4];
+    float L = 0.f;  // counted once per partition: by the lane with sub == 0
+    for (uint32_t p0 = 0;;) {
 #pragma unroll
-            for (int u = 0; u < 4; ++u) {
-                const uint32_t jj = j + u < cnt ? j + u : cnt - 1;
-                fj[u] = __shfl(f, gbase + static_cast<int>(jj), kWave);
-                if (j + u >= cnt) fj[u] = 0.f;
-                const float4* src = reinterpret_cast<const float4*>(a.part_out + (base + p0 + jj) * D + d0);
+        for (int u = 0; u < U; ++u) {
+            const float f = ok[u] ? fast_exp2(st[u].x - M) : 0.f;
+            if (sub == 0) L += st[u].y * f;
 #pragma unroll
-                for (int k = 0; k < N4; ++k) v[u][k] = src[k];
+            for (int k = 0; k < N4; ++k) {
+                o[k].x += v[u][k].x * f;
+                o[k].y += v[u][k].y * f;
+                o[k].z += v[u][k].z * f;
+                o[k].w += v[u][k].w * f;
             }
-#pragma unroll
-            for (int u = 0; u < 4; ++u)
-#pragma unroll
-                for (int k = 0; k < N4; ++k) {
-                    o[k].x += v[u][k].x * fj[u];
-                    o[k].y += v[u][k].y * fj[u];
-                    o[k].z += v[u][k].z * fj[u];
-                    o[k].w += v[u][k].w * fj[u];
-                }
         }
+        p0 += R * U;
+        if (p0 >= np) break;
+        load_round(p0);
     }
-    L = group_sum<LPT>(L);
-    const float inv = L > 0.f ? 1.0f / L : 0.f;
+    L = group_sum<LPG>(L);
 #pragma unroll
     for (int k = 0; k < N4; ++k)
-        *reinterpret_cast<float4*>(a.out + head * D + d0 + 4 * k) =
-            make_float4(o[k].x * inv, o[k].y * inv, o[k].z * inv, o[k].w * inv);
+#pragma unroll
+        for (int m = LPT; m < LPG; m <<= 1) {
+            o[k].x += wave_xor(o[k].x, m);
+            o[k].y += wave_xor(o[k].y, m);
+            o[k].z += wave_xor(o[k].z, m);
+            o[k].w += wave_xor(o[k].w, m);
+        }
+    const float inv = L > 0.f ? 1.0f / L : 0.f;
+    if (r == 0)
+#pragma unroll
+        for (int k = 0; k < N4; ++k)
+            *reinterpret_cast<float4*>(a.out + head * D + d0 + 4 * k) =
+                make_float4(o[k].x * inv, o[k].y * inv, o[k].z * inv, o[k].w * inv);
 }
 
 __device__ __forceinline__ float comp(const float4& v, int i) {
@@ -837,10 +855,10 @@ __global__ __launch_bounds__(kThreads, 2) void attn_main(AttnArgs a) {
     }
 }
 
-// One wave per (row, query head) in a grid-stride loop: rows split over several
-// partitions are merged (a kernel boundary orders them after every partial);
-// single-partition rows were written by stage 1.
-template <int D>
+// One group of LPG lanes per (row, query head) in a grid-stride loop: rows split
+// over several partitions are merged (a kernel boundary orders them after every
+// partial); single-partition rows were written by stage 1.
+template <int D, int LPG>
 __global__ __launch_bounds__(kThreads) void attn_reduce(AttnArgs a) {
     __shared__ SeqTable st;
     const uint32_t tid = threadIdx.x;
@@ -849,15 +867,11 @@ __global__ __launch_bounds__(kThreads) void attn_reduce(AttnArgs a) {
         if (s < a.num_seqs) st.ctx[s] = static_cast<int32_t>(a.ctx_lens[s]);
     }
     __syncthreads();
-    // LPT lanes hold 4*N4 elements each; a wave merges PAIRS (row, head) pairs at once.
-    constexpr int LPT = D / 4 < kWave ? D / 4 : kWave;
-    constexpr int N4 = D / 4 / LPT;
-    constexpr int PAIRS = kWave / LPT;
     const int lane = threadIdx.x & (kWave - 1);
-    const uint32_t slot = static_cast<uint32_t>(lane / LPT), sub = static_cast<uint32_t>(lane % LPT);
-    const uint32_t n_groups = gridDim.x * kWaves * PAIRS;
+    constexpr uint32_t kGroups = kThreads / LPG;
+    const uint32_t n_groups = gridDim.x * kGroups;
     const uint32_t n_work = a.total_q * a.num_heads;
-    for (uint32_t w = (blockIdx.x * kWaves + threadIdx.x / kWave) * PAIRS + slot; w < n_work; w += n_groups) {
+    for (uint32_t w = blockIdx.x * kGroups + threadIdx.x / LPG; w < n_work; w += n_groups) {
         const uint32_t row = w / a.num_heads, h = w % a.num_heads;
         uint32_t lo = 0, hi = a.num_seqs;  // last s with cu[s] <= row
         while (hi - lo > 1) {
@@ -868,7 +882,7 @@ __global__ __launch_bounds__(kThreads) void attn_reduce(AttnArgs a) {
         const int32_t ql = st.cu[lo + 1] - st.cu[lo];
         const uint32_t lim = row_limit(st.ctx[lo], ql, static_cast<int32_t>(row) - st.cu[lo], a.capacity);
         const uint32_t np = ceil_div(lim, part_of(a, ql, a.part_size));
-        if (np > 1) merge_partials<D, N4, LPT>(a, static_cast<size_t>(row) * a.num_heads + h, np, sub, lane);
+        if (np > 1) merge_partials<D, LPG>(a, static_cast<size_t>(row) * a.num_heads + h, np, lane);
     }
 }
 
@@ -922,15 +936,23 @@ Stage1Fn pick_main_kv(uint32_t kv, uint32_t D, uint32_t G, bool buf) {
     return nullptr;
 }
 
-Stage1Fn pick_reduce(uint32_t D) {
+// Lanes per merge: a whole wave when a row may have more partitions than a
+// 16-lane group covers in two rounds, else the head's natural lane count.
+template <int D>
+Stage1Fn pick_reduce_d(bool wide) {
+    constexpr int narrow = D / 4 < kWave ? (D / 4 < 16 ? 16 : D / 4) : kWave;
+    return wide ? attn_reduce<D, kWave> : attn_reduce<D, narrow>;
+}
+
+Stage1Fn pick_reduce(uint32_t D, bool wide) {
     switch (D) {
-        case 4: return attn_reduce<4>;
-        case 8: return attn_reduce<8>;
-        case 16: return attn_reduce<16>;
-        case 32: return attn_reduce<32>;
-        case 64: return attn_reduce<64>;
-        case 128: return attn_reduce<128>;
-        case 256: return attn_reduce<256>;
+        case 4: return pick_reduce_d<4>(wide);
+        case 8: return pick_reduce_d<8>(wide);
+        case 16: return pick_reduce_d<16>(wide);
+        case 32: return pick_reduce_d<32>(wide);
+        case 64: return pick_reduce_d<64>(wide);
+        case 128: return pick_reduce_d<128>(wide);
+        case 256: return pick_reduce_d<256>(wide);
         default: return nullptr;
     }
 }
@@ -1079,7 +1101,8 @@ int run_ragged(kanso_ctx* ctx, const kanso_ragged_attention_params* p, const flo
     a.use_mfma = (D == 64 && G <= 4 && max_q > 1 && buf) ? 1u : 0u;
     a.head_major = p->pool_layout == KANSO_POOL_HEAD_MAJOR ? 1u : 0u;
     Stage1Fn main_fn = pick_main_kv(p->kv_dtype, D, G, buf);
-    Stage1Fn reduce = pick_reduce(D);
+    const bool wide_merge = max_parts > 16;
+    Stage1Fn reduce = pick_reduce(D, wide_merge);
     if (!main_fn || !reduce) {
         set_error("%s: no kernel for head_dim %u / kv_dtype %u", who, D, p->kv_dtype);
         return KANSO_E_INVALID_SHAPE;
@@ -1099,9 +1122,9 @@ int run_ragged(kanso_ctx* ctx, const kanso_ragged_attention_params* p, const flo
     hipLaunchKernelGGL(main_fn, dim3(grid), dim3(kThreads), 0, stream, a);
     KANSO_LAUNCH_CHECK();
     if ((rc = prof_end(ctx, "attention", stream, ev))) return rc;
-    const uint64_t pairs_per_wg = static_cast<uint64_t>(kWaves) * (kWave / std::min<uint32_t>(D / 4, kWave));
+    const uint64_t merges_per_wg = wide_merge ? kWaves : kThreads / std::max<uint32_t>(16, std::min<uint32_t>(D / 4, kWave));
     const uint32_t rgrid = static_cast<uint32_t>(std::max<uint64_t>(
-        1, std::min<uint64_t>((static_cast<uint64_t>(T) * H + pairs_per_wg - 1) / pairs_per_wg, ctx->num_cus * 8)));
+        1, std::min<uint64_t>((static_cast<uint64_t>(T) * H + merges_per_wg - 1) / merges_per_wg, ctx->num_cus * 8)));
     if ((rc = prof_begin(ctx, "reduce", stream, &ev))) return rc;
     hipLaunchKernelGGL(reduce, dim3(rgrid), dim3(kThreads), 0, stream, a);
     KANSO_LAUNCH_CHECK();
