@@ -521,6 +521,200 @@ __device__ void decode_item(const AttnArgs& a, const PoolRsrc& rs, uint32_t row,
     }
 }
 
+// ---------------------------------------------------------------- decode rows, 1-byte pools
+//
+// INT8 / Q8_0 pools keep their tiles raw: a lane loads QE = 8 elements (8 bytes,
+// one b64 buffer load) of a token row plus that row's scale, and dequantizes only
+// when the tile is scored. A tile of NL rows per lane then carries twice the bytes
+// of the float path in fewer registers. The per-row scale of K folds into the
+// score (s = scale_k * sum q k) and that of V into the probability (p * scale_v),
+// one multiply each instead of one per element; the reference dequantizes each
+// element first ((q as f32) * scale, src/kv_cache/quantized_storage.rs:284-357),
+// which only reorders
+// the same products. (A lane's 8 elements always sit in one Q8_0 block, so the
+// scale is applied to each lane's partial sum before the lanes are added.)
+constexpr int kQE = 8;
+
+template <int NL>
+struct DecodeTileQ {
+    uint2 k[NL], v[NL];
+    float ks[NL], vs[NL];
+};
+
+template <int KVT>
+__device__ __forceinline__ float load_row_scale(__amdgpu_buffer_rsrc_t sc, uint32_t row, bool ok, int D, int d0) {
+    if constexpr (KVT == KANSO_KV_INT8) {
+        return __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(sc, ok ? row * 4u : kOffNone, 0, 0));
+    } else {
+        const uint16_t hb = __builtin_amdgcn_raw_buffer_load_b16(
+            sc, ok ? (row * static_cast<uint32_t>(D / 32) + static_cast<uint32_t>(d0 / 32)) * 2u : kOffNone, 0, 0);
+        return __half2float(__ushort_as_half(hb));
+    }
+}
+
+__device__ __forceinline__ void i8x8_to_f32(uint2 w, float (&f)[kQE]) {
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        f[j] = static_cast<float>(static_cast<int8_t>((w.x >> (8 * j)) & 0xff));
+        f[4 + j] = static_cast<float>(static_cast<int8_t>((w.y >> (8 * j)) & 0xff));
+    }
+}
+
+template <int D, int KVT, int NL>
+__device__ __forceinline__ void decode_load_q(const AttnArgs& a, const PoolRsrc& rs, const PartView& pv,
+                                              uint32_t tile0, uint32_t kvh, int ts, int dl, DecodeTileQ<NL>& tl) {
+    constexpr int TPI = kWave / (D / kQE);
+#pragma unroll
+    for (int i = 0; i < NL; ++i) {
+        const uint32_t t = tile0 + i * TPI + ts;
+        const bool ok = t < pv.t_end;
+        const uint32_t r = static_cast<uint32_t>(pool_row(a, pv, ok ? t : tile0, kvh));
+        const uint32_t off = ok ? r * D + static_cast<uint32_t>(dl * kQE) : kOffNone;
+        tl.k[i] = __builtin_bit_cast(uint2, __builtin_amdgcn_raw_buffer_load_b64(rs.k, off, 0, 0));
+        tl.v[i] = __builtin_bit_cast(uint2, __builtin_amdgcn_raw_buffer_load_b64(rs.v, off, 0, 0));
+        tl.ks[i] = load_row_scale<KVT>(rs.ks, r, ok, D, dl * kQE);
+        tl.vs[i] = load_row_scale<KVT>(rs.vs, r, ok, D, dl * kQE);
+    }
+}
+
+// q is pre-multiplied by scale * log2(e), so the score is sum over lanes of
+// ks * sum(q k) in log2 units.
+template <int D, int GMAX, int NL>
+__device__ __forceinline__ void decode_compute_q(const AttnArgs& a, const PartView& pv, uint32_t tile0, int ts,
+                                                 const float (&q)[GMAX][kQE], float (&acc)[GMAX][kQE],
+                                                 float (&m)[GMAX], float (&l)[GMAX], const DecodeTileQ<NL>& tl) {
+    constexpr int LPT = D / kQE;
+    constexpr int TPI = kWave / LPT;
+    const uint32_t G = a.group;
+    float sc[GMAX][NL];
+#pragma unroll
+    for (int i = 0; i < NL; ++i) {
+        float kf[kQE];
+        i8x8_to_f32(tl.k[i], kf);
+        const bool ok = tile0 + i * TPI + ts < pv.t_end;
+#pragma unroll
+        for (int g = 0; g < GMAX; ++g) {
+            if (g >= static_cast<int>(G)) break;
+            float d = 0.f;
+#pragma unroll
+            for (int j = 0; j < kQE; ++j) d += q[g][j] * kf[j];
+            // the scale before the sum: a Q8_0 row has one scale per 32 elements
+            d = group_sum<LPT>(d * tl.ks[i]);
+            sc[g][i] = ok ? d : -INFINITY;
+        }
+    }
+    float alpha[GMAX];
+#pragma unroll
+    for (int g = 0; g < GMAX; ++g) {
+        if (g >= static_cast<int>(G)) break;
+        float mt = -INFINITY;
+#pragma unroll
+        for (int i = 0; i < NL; ++i) mt = fmaxf(mt, sc[g][i]);
+#pragma unroll
+        for (int o = LPT; o < kWave; o <<= 1) mt = fmaxf(mt, wave_xor(mt, o));
+        const float mn = fmaxf(m[g], mt);  // finite: every tile holds a live token
+        alpha[g] = fast_exp2(m[g] - mn);
+        m[g] = mn;
+        float ps = 0.f;
+#pragma unroll
+        for (int i = 0; i < NL; ++i) {
+            sc[g][i] = fast_exp2(sc[g][i] - mn);
+            ps += sc[g][i];
+        }
+#pragma unroll
+        for (int o = LPT; o < kWave; o <<= 1) ps += wave_xor(ps, o);
+        l[g] = l[g] * alpha[g] + ps;
+#pragma unroll
+        for (int j = 0; j < kQE; ++j) acc[g][j] *= alpha[g];
+    }
+#pragma unroll
+    for (int i = 0; i < NL; ++i) {
+        float vf[kQE];
+        i8x8_to_f32(tl.v[i], vf);
+#pragma unroll
+        for (int g = 0; g < GMAX; ++g) {
+            if (g >= static_cast<int>(G)) break;
+            const float pv_ = sc[g][i] * tl.vs[i];
+#pragma unroll
+            for (int j = 0; j < kQE; ++j) acc[g][j] += pv_ * vf[j];
+        }
+    }
+}
+
+template <int D, int GMAX, int KVT, int NL, int NB>
+__device__ void decode_item_q(const AttnArgs& a, const PoolRsrc& rs, uint32_t row, uint32_t part, uint32_t P,
+                              uint32_t seq, uint32_t kvh, int lane) {
+    constexpr int LPT = D / kQE;
+    constexpr int TT = (kWave / LPT) * NL;
+    const int ts = lane / LPT, dl = lane % LPT;
+    const uint32_t G = a.group;
+    const int32_t ql = a.cu[seq + 1] - a.cu[seq];
+    const uint32_t limit = row_limit(static_cast<int32_t>(a.ctx_lens[seq]), ql,
+                                     static_cast<int32_t>(row) - a.cu[seq], a.capacity);
+    const uint32_t t_begin = part * P;
+    const uint32_t t_end = min(t_begin + P, limit);
+    const PartView pv = load_part(a, seq, t_begin, t_end, lane);
+
+    float q[GMAX][kQE], acc[GMAX][kQE], m[GMAX], l[GMAX];
+#pragma unroll
+    for (int g = 0; g < GMAX; ++g) {
+        m[g] = -INFINITY;
+        l[g] = 0.f;
+#pragma unroll
+        for (int j = 0; j < kQE; ++j) q[g][j] = acc[g][j] = 0.f;
+        if (g < static_cast<int>(G)) {
+            const float4* src = reinterpret_cast<const float4*>(
+                a.q + (static_cast<size_t>(row) * a.num_heads + kvh * G + g) * D + dl * kQE);
+            const float4 x0 = src[0], x1 = src[1];
+            const float xs[kQE] = {x0.x, x0.y, x0.z, x0.w, x1.x, x1.y, x1.z, x1.w};
+#pragma unroll
+            for (int j = 0; j < kQE; ++j) q[g][j] = xs[j] * a.scale_log2;
+        }
+    }
+
+    DecodeTileQ<NL> ring[NB];
+#pragma unroll
+    for (int j = 0; j + 1 < NB; ++j)
+        if (t_begin + j * TT < t_end) decode_load_q<D, KVT, NL>(a, rs, pv, t_begin + j * TT, kvh, ts, dl, ring[j]);
+    for (uint32_t t0 = t_begin; t0 < t_end; t0 += NB * TT) {
+#pragma unroll
+        for (int j = 0; j < NB; ++j) {
+            const uint32_t tj = t0 + j * TT;
+            if (tj >= t_end) break;
+            const uint32_t nxt = tj + (NB - 1) * TT;
+            if (nxt < t_end) decode_load_q<D, KVT, NL>(a, rs, pv, nxt, kvh, ts, dl, ring[(j + NB - 1) % NB]);
+            decode_compute_q<D, GMAX, NL>(a, pv, tj, ts, q, acc, m, l, ring[j]);
+        }
+    }
+
+    const bool single = t_begin == 0 && t_end == limit;
+#pragma unroll
+    for (int g = 0; g < GMAX; ++g) {
+        if (g >= static_cast<int>(G)) break;
+#pragma unroll
+        for (int j = 0; j < kQE; ++j)
+#pragma unroll
+            for (int o = LPT; o < kWave; o <<= 1) acc[g][j] += wave_xor(acc[g][j], o);
+        const size_t head = static_cast<size_t>(row) * a.num_heads + kvh * G + g;
+        if (single) {
+            const float inv = l[g] > 0.f ? 1.0f / l[g] : 0.f;
+            if (ts == 0) {
+                float4* d4 = reinterpret_cast<float4*>(a.out + head * D + dl * kQE);
+                d4[0] = make_float4(acc[g][0] * inv, acc[g][1] * inv, acc[g][2] * inv, acc[g][3] * inv);
+                d4[1] = make_float4(acc[g][4] * inv, acc[g][5] * inv, acc[g][6] * inv, acc[g][7] * inv);
+            }
+            continue;
+        }
+        const size_t slot = head * a.max_parts + part;
+        if (ts == 0) {
+            float4* d4 = reinterpret_cast<float4*>(a.part_out + slot * D + dl * kQE);
+            d4[0] = make_float4(acc[g][0], acc[g][1], acc[g][2], acc[g][3]);
+            d4[1] = make_float4(acc[g][4], acc[g][5], acc[g][6], acc[g][7]);
+        }
+        if (lane == 0) a.part_stats[slot] = make_float2(m[g], l[g]);
+    }
+}
+
 // ---------------------------------------------------------------- chunk rows (MFMA)
 
 typedef float floatx4 __attribute__((ext_vector_type(4)));
@@ -850,8 +1044,12 @@ __global__ __launch_bounds__(kThreads, 2) void attn_main(AttnArgs a) {
                 local -= np;
             }
         }
-        decode_item<D, GMAX, KVT, NL, NB, BUF>(a, rs, static_cast<uint32_t>(st.cu[s] + i), local, a.part_size, s,
-                                               kvh, lane);
+        if constexpr (KVT != KANSO_KV_F32 && BUF && D >= kQE)
+            decode_item_q<D, GMAX, KVT, (GMAX <= 4 ? 8 : 4), 2>(a, rs, static_cast<uint32_t>(st.cu[s] + i), local, a.part_size, s,
+                                              kvh, lane);
+        else
+            decode_item<D, GMAX, KVT, NL, NB, BUF>(a, rs, static_cast<uint32_t>(st.cu[s] + i), local, a.part_size,
+                                                   s, kvh, lane);
     }
 }
 
@@ -893,10 +1091,12 @@ __global__ void iota_cu(int32_t* cu, uint32_t n) {
 
 using Stage1Fn = void (*)(AttnArgs);
 
+// Batches with prefill chunks get the kernel with the MFMA chunk path (it needs
+// the exact group size); all-decode batches the one without it (fewer registers).
 template <int D, int GMAX, int KVT, bool BUF>
-Stage1Fn pick_main_g(uint32_t G) {
+Stage1Fn pick_main_g(uint32_t G, bool mfma) {
     if constexpr (D == 64 && BUF) {
-        switch (G) {  // the MFMA chunk path needs the exact group size
+        if (mfma) switch (G) {
             case 1: return attn_main<D, GMAX, KVT, BUF, 1>;
             case 2: return attn_main<D, GMAX, KVT, BUF, 2>;
             case 3: return attn_main<D, GMAX, KVT, BUF, 3>;
@@ -908,31 +1108,31 @@ Stage1Fn pick_main_g(uint32_t G) {
 }
 
 template <int D, int KVT>
-Stage1Fn pick_group(uint32_t G, bool buf) {
+Stage1Fn pick_group(uint32_t G, bool buf, bool mfma) {
     if (D == 64 && G == 3)  // SmolLM2 (15 / 5 heads)
-        return buf ? pick_main_g<D, 3, KVT, true>(G) : pick_main_g<D, 3, KVT, false>(G);
-    if (G <= 4) return buf ? pick_main_g<D, 4, KVT, true>(G) : pick_main_g<D, 4, KVT, false>(G);
-    return buf ? pick_main_g<D, 8, KVT, true>(G) : pick_main_g<D, 8, KVT, false>(G);
+        return buf ? pick_main_g<D, 3, KVT, true>(G, mfma) : pick_main_g<D, 3, KVT, false>(G, mfma);
+    if (G <= 4) return buf ? pick_main_g<D, 4, KVT, true>(G, mfma) : pick_main_g<D, 4, KVT, false>(G, mfma);
+    return buf ? pick_main_g<D, 8, KVT, true>(G, mfma) : pick_main_g<D, 8, KVT, false>(G, mfma);
 }
 
 template <int KVT>
-Stage1Fn pick_decode(uint32_t D, uint32_t G, bool buf) {
+Stage1Fn pick_decode(uint32_t D, uint32_t G, bool buf, bool mfma) {
     switch (D) {
-        case 4: return KVT != KANSO_KV_Q8_0 ? pick_group<4, KVT>(G, buf) : nullptr;
-        case 8: return KVT != KANSO_KV_Q8_0 ? pick_group<8, KVT>(G, buf) : nullptr;
-        case 16: return KVT != KANSO_KV_Q8_0 ? pick_group<16, KVT>(G, buf) : nullptr;
-        case 32: return pick_group<32, KVT>(G, buf);
-        case 64: return pick_group<64, KVT>(G, buf);
-        case 128: return pick_group<128, KVT>(G, buf);
-        case 256: return pick_group<256, KVT>(G, buf);
+        case 4: return KVT != KANSO_KV_Q8_0 ? pick_group<4, KVT>(G, buf, mfma) : nullptr;
+        case 8: return KVT != KANSO_KV_Q8_0 ? pick_group<8, KVT>(G, buf, mfma) : nullptr;
+        case 16: return KVT != KANSO_KV_Q8_0 ? pick_group<16, KVT>(G, buf, mfma) : nullptr;
+        case 32: return pick_group<32, KVT>(G, buf, mfma);
+        case 64: return pick_group<64, KVT>(G, buf, mfma);
+        case 128: return pick_group<128, KVT>(G, buf, mfma);
+        case 256: return pick_group<256, KVT>(G, buf, mfma);
         default: return nullptr;
     }
 }
 
-Stage1Fn pick_main_kv(uint32_t kv, uint32_t D, uint32_t G, bool buf) {
-    if (kv == KANSO_KV_F32) return pick_decode<KANSO_KV_F32>(D, G, buf);
-    if (kv == KANSO_KV_INT8) return pick_decode<KANSO_KV_INT8>(D, G, buf);
-    if (kv == KANSO_KV_Q8_0) return pick_decode<KANSO_KV_Q8_0>(D, G, buf);
+Stage1Fn pick_main_kv(uint32_t kv, uint32_t D, uint32_t G, bool buf, bool mfma) {
+    if (kv == KANSO_KV_F32) return pick_decode<KANSO_KV_F32>(D, G, buf, mfma);
+    if (kv == KANSO_KV_INT8) return pick_decode<KANSO_KV_INT8>(D, G, buf, mfma);
+    if (kv == KANSO_KV_Q8_0) return pick_decode<KANSO_KV_Q8_0>(D, G, buf, mfma);
     return nullptr;
 }
 
@@ -1100,7 +1300,7 @@ int run_ragged(kanso_ctx* ctx, const kanso_ragged_attention_params* p, const flo
     const uint32_t max_q = p->max_q_len ? p->max_q_len : T;
     a.use_mfma = (D == 64 && G <= 4 && max_q > 1 && buf) ? 1u : 0u;
     a.head_major = p->pool_layout == KANSO_POOL_HEAD_MAJOR ? 1u : 0u;
-    Stage1Fn main_fn = pick_main_kv(p->kv_dtype, D, G, buf);
+    Stage1Fn main_fn = pick_main_kv(p->kv_dtype, D, G, buf, a.use_mfma != 0);
     const bool wide_merge = max_parts > 16;
     Stage1Fn reduce = pick_reduce(D, wide_merge);
     if (!main_fn || !reduce) {
