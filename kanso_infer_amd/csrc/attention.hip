@@ -8,31 +8,35 @@
 // (paged_attention_v2.metal:32-205: partitions, per-partition (m, d) statistics,
 // a merge) is kept; the mapping onto CDNA4 is this file's own:
 //
-//  * Work unit = one wave64. A device-built work list holds (rows, partition)
-//    items; every wave of a persistent grid walks it with a grid-wide stride, one
-//    item x KV head at a time. No LDS, no barriers: waves never wait on each other.
-//  * Decode rows (one query row): LPT = head_dim/4 lanes share a token, each lane
-//    loads one 16 B float4 of K and of V, so a load instruction moves 1 KB of fully
-//    used bytes (four 256 B rows at head_dim 64). Tiles of NL tokens per lane are
-//    double-buffered: the next tile's loads are in flight while the current tile
-//    is scored. Every query head of the GQA group is served from the same K/V
-//    registers, so K/V bytes are read once per (token, KV head).
-//  * Prefill-chunk rows: 16 rows x G heads per wave on the matrix cores
-//    (v_mfma_f32_16x16x4f32, full fp32 products). S^T = K Q^T is computed with K as
-//    the A operand (loaded straight from the pool in MFMA layout) and Q^T held in
-//    registers; the C layout of S^T is then exactly the B-operand layout of
-//    O^T = V^T P^T, so probabilities never leave registers and each query's
-//    softmax statistics live in that query's own lanes.
+//  * One persistent launch, two 4-wave workgroups per CU. No work list is
+//    materialised: each workgroup copies cu_seqlens / context_lens into LDS and
+//    scans the per-sequence item counts; a wave maps a work index to a sequence
+//    by binary search. Prefill-chunk items (64 rows x partition x KV head) go to
+//    the first workgroups, decode items (one row x partition x KV head) to every
+//    wave of the others, so matrix-core and bandwidth-bound work share the chip.
+//  * Decode rows, F32 pool: LPT = head_dim/4 lanes share a token, each lane loads
+//    one 16 B float4 of K and of V, so a load instruction moves 1 KB of fully used
+//    bytes. A ring of two tiles of NL tokens per lane keeps one tile's loads in
+//    flight while the other is scored. Every query head of the GQA group is
+//    served from the same K/V registers: K/V bytes are read once per (token, KV
+//    head).
+//  * Decode rows, INT8 / Q8_0 pool: 8 bytes per lane (one b64 load), tiles kept
+//    raw and dequantized when scored, row scales folded into score and
+//    probability.
+//  * Prefill-chunk rows: 16 rows x G heads per wave on the bf16 matrix cores with
+//    a hi / lo split of every f32 operand (v_mfma_f32_16x16x32_bf16, three
+//    products per pair, f32 accumulation). A 32-key K/V tile is staged once per
+//    workgroup in LDS in operand order. S^T = K Q^T puts the scores in exactly
+//    the B-operand layout of O^T = V^T P^T, so probabilities never leave
+//    registers and each query's softmax statistics live in that query's lanes.
 //  * Block tables: the <= 64 table entries a partition touches are loaded once
 //    into one register per lane; token -> physical block is a lane shuffle.
 //  * Scores live in the log2 domain (scale * log2(e) folded into one multiply);
 //    the online softmax rescales once per tile, not once per token.
 //  * A row whose context fits one partition is normalised and written directly;
 //    only rows split over several partitions go through the reduce kernel.
-//  * Chunk items come first in the work list, so compute-bound MFMA waves and
-//    bandwidth-bound decode waves share the machine instead of running in turn.
-//  * Quantized pools (INT8 per token-head scale, Q8_0 per-32 f16 scale) are
-//    dequantized in registers with the reference's own product (q as f32) * scale.
+//  * Quantized pools (INT8 per token-head scale, Q8_0 per-32 f16 scale) use the
+//    reference's products, (q as f32) * scale, reordered only by the scale folds.
 #include <cmath>
 #include <cstdlib>
 
