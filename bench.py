@@ -182,16 +182,26 @@ def gemv_bench(ctx, torch, K, oracle_mod, quick):
                 for i in range(4):
                     fn(ctx, arena[i * wbytes:(i + 1) * wbytes], x, y, rows, cols_eff)
                 torch.cuda.synchronize()
-                ctx.set_profiling(True)
                 n = min(copies, 200)
+                # us: HIP events around each launch on its stream (kernel duration
+                # plus event overhead); us_back_to_back: one event pair around n
+                # eager launches, bounded by the host's submission rate
+                ctx.set_profiling(True)
                 for i in range(n):
                     fn(ctx, arena[i * wbytes:(i + 1) * wbytes], x, y, rows, cols_eff)
                 g_ms, g_n = ctx.kernel_time("gemv")
                 ctx.set_profiling(False)
                 us = g_ms / max(g_n, 1) * 1e3
+                s_ev, e_ev = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+                s_ev.record()
+                for i in range(n):
+                    fn(ctx, arena[i * wbytes:(i + 1) * wbytes], x, y, rows, cols_eff)
+                e_ev.record()
+                torch.cuda.synchronize()
+                us_b2b = s_ev.elapsed_time(e_ev) / n * 1e3
                 abytes = w.size + batch * (cols_eff + rows) * 4  # stored GGUF bytes
                 out.append(dict(kind=kind, shape=label, out=rows, inp=cols_eff, batch=batch,
-                                us=round(us, 2), gbps=round(abytes / (us * 1e-6) / 1e9, 1),
+                                us=round(us, 2), us_back_to_back=round(us_b2b, 2), gbps=round(abytes / (us * 1e-6) / 1e9, 1),
                                 frac=round(abytes / (us * 1e-6) / HBM_PEAK, 4)))
             del arena
             torch.cuda.empty_cache()
