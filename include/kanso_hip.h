@@ -112,6 +112,8 @@ typedef struct {
     uint32_t num_blocks; /* physical blocks in the pool (bounds check of table ids) */
     uint32_t max_q_len;  /* upper bound of any sequence's query rows (0 = total_q)  */
     uint32_t pool_layout; /* KANSO_POOL_*                                           */
+    uint32_t partition_size; /* split-K partition of decode rows in tokens: 0 = chosen
+                                from the shape; else a power of two in [32, 512]   */
 } kanso_ragged_attention_params;
 
 /* One planned sequence of a step, as Engine::step plans it (src/engine.rs:221-226). */

@@ -204,14 +204,15 @@ def ragged_paged_attention(ctx: Context, *, q: torch.Tensor, k_pool: torch.Tenso
                            block_size: int, scale: float, kv_dtype: int = KANSO_KV_F32,
                            k_scales: torch.Tensor | None = None,
                            v_scales: torch.Tensor | None = None, num_blocks: int = 0,
-                           max_q_len: int = 0, pool_layout: int = 0,
+                           max_q_len: int = 0, pool_layout: int = 0, partition_size: int = 0,
                            stream: torch.cuda.Stream | None = None) -> None:
     """Mixed prefill + decode attention over the paged pool (kanso_ragged_paged_attention)."""
     num_seqs = cu_seqlens.numel() - 1
     max_blocks = block_tables.numel() // max(num_seqs, 1)
     total_q = q.numel() // (num_heads * head_dim)
     p = RaggedAttentionParamsC(num_seqs, num_heads, num_kv_heads, head_dim, block_size, max_blocks,
-                               scale, total_q, kv_dtype, num_blocks, max_q_len, pool_layout)
+                               scale, total_q, kv_dtype, num_blocks, max_q_len, pool_layout,
+                               partition_size)
     _check(ctx._lib.kanso_ragged_paged_attention(
         ctx.handle, C.byref(p), _ptr(q), _ptr(k_pool), _ptr(v_pool), _ptr(k_scales),
         _ptr(v_scales), _ptr(block_tables), _ptr(cu_seqlens), _ptr(context_lens), _ptr(out),

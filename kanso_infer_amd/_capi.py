@@ -64,6 +64,7 @@ class RaggedAttentionParamsC(C.Structure):
         ("num_blocks", C.c_uint32),
         ("max_q_len", C.c_uint32),
         ("pool_layout", C.c_uint32),
+        ("partition_size", C.c_uint32),
     ]
 
 

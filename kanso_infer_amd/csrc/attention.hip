@@ -1243,7 +1243,16 @@ int run_ragged(kanso_ctx* ctx, const kanso_ragged_attention_params* p, const flo
     }
     const uint32_t capacity = static_cast<uint32_t>(cap64);
     const uint32_t T = p->total_q;
-    const uint32_t P = choose_partition(ctx, S, HKV, capacity, p->block_size, p->kv_dtype == KANSO_KV_F32 ? 4 : 1);
+    if (p->partition_size && (p->partition_size < 32 || p->partition_size > 512 ||
+                              (p->partition_size & (p->partition_size - 1)) != 0 ||
+                              p->partition_size > 62u * p->block_size)) {
+        set_error("%s: partition_size %u must be 0 or a power of two in [32, min(512, 62 * block_size)]", who,
+                  p->partition_size);
+        return KANSO_E_INVALID_SHAPE;
+    }
+    const uint32_t P = p->partition_size ? p->partition_size
+                                         : choose_partition(ctx, S, HKV, capacity, p->block_size,
+                                                            p->kv_dtype == KANSO_KV_F32 ? 4 : 1);
     const uint32_t max_parts = (capacity + P - 1) / P;
     const uint64_t partial_elems = static_cast<uint64_t>(T) * H * max_parts * D;
     if (partial_elems > (1ull << 31)) {
@@ -1407,7 +1416,7 @@ int kanso_paged_attention_v2(kanso_ctx* ctx, const kanso_paged_attention_params*
     int32_t* cu_buf = static_cast<int32_t*>(ctx->aux);
     hipLaunchKernelGGL(iota_cu, dim3((p->num_seqs + 256) / 256), dim3(256), 0, s, cu_buf, p->num_seqs);
     KANSO_LAUNCH_CHECK();
-    kanso_ragged_attention_params rp;
+    kanso_ragged_attention_params rp{};
     rp.num_seqs = p->num_seqs;
     rp.num_heads = p->num_heads;
     rp.num_kv_heads = p->num_kv_heads;

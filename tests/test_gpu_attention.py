@@ -110,6 +110,28 @@ def test_ragged_small(ctx, seed, kv_dtype):
     assert_close(got, want, what=f"{b.label} kv {kv_dtype}")
 
 
+@pytest.mark.parametrize("partition", [32, 64, 128, 512])
+@pytest.mark.parametrize("kv_dtype", [oracle.KV_F32, oracle.KV_Q8_0])
+def test_explicit_partition_size(ctx, partition, kv_dtype):
+    """A caller-chosen split-K partition gives the oracle's result (decode and chunk rows)."""
+    b = workloads.small_mixed(11)
+    kp, vp, ks, vs = fill_pool(b, kv_dtype, 11)
+    q = np.random.default_rng(61).standard_normal(
+        b.total_q * b.num_heads * b.head_dim).astype(np.float32)
+    got = run_ragged_gpu(ctx, b, q, kp, vp, ks, vs, kv_dtype, partition_size=partition)
+    want = run_ragged_oracle(b, q, kp, vp, ks, vs, kv_dtype)
+    assert_close(got, want, what=f"{b.label} P {partition} kv {kv_dtype}")
+
+
+def test_rejects_bad_partition_size(ctx):
+    b = workloads.small_mixed(12)
+    kp, vp, ks, vs = fill_pool(b, oracle.KV_F32, 12)
+    q = np.zeros(b.total_q * b.num_heads * b.head_dim, np.float32)
+    for bad in (48, 16, 1024):
+        with pytest.raises(K.EngineError):
+            run_ragged_gpu(ctx, b, q, kp, vp, partition_size=bad)
+
+
 @pytest.mark.parametrize("variant", ["config1", "config2_small_pool", "config3_int8",
                                      "config3_q8_0"])
 def test_baseline_shapes(ctx, variant):
