@@ -456,15 +456,16 @@ __device__ __forceinline__ void decode_compute(const AttnArgs& a, const PartView
 }
 
 template <int D, int GMAX, int KVT, int NL, int NB, bool BUF>
-__device__ void decode_item(const AttnArgs& a, const PoolRsrc& rs, uint32_t row, uint32_t part, uint32_t P,
+__device__ void decode_item(const AttnArgs& a, const SeqTable& st, const PoolRsrc& rs, uint32_t row, uint32_t part,
+                            uint32_t P,
                             uint32_t seq, uint32_t kvh, int lane) {
     constexpr int LPT = D / 4;
     constexpr int TT = (kWave / LPT) * NL;
     const int ts = lane / LPT, dl = lane % LPT;
     const uint32_t G = a.group;
-    const int32_t ql = a.cu[seq + 1] - a.cu[seq];
-    const uint32_t limit = row_limit(static_cast<int32_t>(a.ctx_lens[seq]), ql,
-                                     static_cast<int32_t>(row) - a.cu[seq], a.capacity);
+    const int32_t ql = st.cu[seq + 1] - st.cu[seq];
+    const uint32_t limit = row_limit(st.ctx[seq], ql,
+                                     static_cast<int32_t>(row) - st.cu[seq], a.capacity);
     const uint32_t t_begin = part * P;
     const uint32_t t_end = min(t_begin + P, limit);
     const PartView pv = load_part(a, seq, t_begin, t_end, lane);
@@ -646,15 +647,16 @@ __device__ __forceinline__ void decode_compute_q(const AttnArgs& a, const PartVi
 }
 
 template <int D, int GMAX, int KVT, int NL, int NB>
-__device__ void decode_item_q(const AttnArgs& a, const PoolRsrc& rs, uint32_t row, uint32_t part, uint32_t P,
+__device__ void decode_item_q(const AttnArgs& a, const SeqTable& st, const PoolRsrc& rs, uint32_t row,
+                              uint32_t part, uint32_t P,
                               uint32_t seq, uint32_t kvh, int lane) {
     constexpr int LPT = D / kQE;
     constexpr int TT = (kWave / LPT) * NL;
     const int ts = lane / LPT, dl = lane % LPT;
     const uint32_t G = a.group;
-    const int32_t ql = a.cu[seq + 1] - a.cu[seq];
-    const uint32_t limit = row_limit(static_cast<int32_t>(a.ctx_lens[seq]), ql,
-                                     static_cast<int32_t>(row) - a.cu[seq], a.capacity);
+    const int32_t ql = st.cu[seq + 1] - st.cu[seq];
+    const uint32_t limit = row_limit(st.ctx[seq], ql,
+                                     static_cast<int32_t>(row) - st.cu[seq], a.capacity);
     const uint32_t t_begin = part * P;
     const uint32_t t_end = min(t_begin + P, limit);
     const PartView pv = load_part(a, seq, t_begin, t_end, lane);
@@ -887,13 +889,14 @@ __device__ __forceinline__ void chunk_compute(const AttnArgs& a, const ChunkStag
 // One workgroup item: 64 query rows (wave w: rows 16w .. 16w + 15 of the block) of
 // one sequence, one key partition, one KV head.
 template <int G, int KVT>
-__device__ void chunk_block(const AttnArgs& a, const PoolRsrc& rs, ChunkStage (&stage)[2], uint32_t row0,
+__device__ void chunk_block(const AttnArgs& a, const SeqTable& st, const PoolRsrc& rs, ChunkStage (&stage)[2],
+                            uint32_t row0,
                             uint32_t part, int nrows_blk, uint32_t seq, uint32_t kvh) {
     constexpr int D = 64;
     const int lane = threadIdx.x & (kWave - 1), wv = threadIdx.x / kWave;
-    const int32_t ql = a.cu[seq + 1] - a.cu[seq];
-    const int32_t ctx = static_cast<int32_t>(a.ctx_lens[seq]);
-    const int32_t li0 = static_cast<int32_t>(row0) - a.cu[seq];
+    const int32_t ql = st.cu[seq + 1] - st.cu[seq];
+    const int32_t ctx = st.ctx[seq];
+    const int32_t li0 = static_cast<int32_t>(row0) - st.cu[seq];
     const int nrows = min(kChunkWaveRows, nrows_blk - kChunkWaveRows * wv);  // this wave's rows (may be <= 0)
     const int qi = lane & 15;
     const bool qlive = qi < nrows;
@@ -1020,7 +1023,7 @@ __global__ __launch_bounds__(kThreads, 2) void attn_main(AttnArgs a) {
                         if (local < np) break;
                         local -= np;
                     }
-                    chunk_block<GC, KVT>(a, rs, stage, static_cast<uint32_t>(st.cu[s] + i0), local,
+                    chunk_block<GC, KVT>(a, st, rs, stage, static_cast<uint32_t>(st.cu[s] + i0), local,
                                          min(kChunkBlockRows, ql - i0), s, kvh);
                     __syncthreads();  // the next item's prologue reuses the stages
                 }
@@ -1048,12 +1051,11 @@ __global__ __launch_bounds__(kThreads, 2) void attn_main(AttnArgs a) {
                 local -= np;
             }
         }
+        const uint32_t row = static_cast<uint32_t>(st.cu[s] + i);
         if constexpr (KVT != KANSO_KV_F32 && BUF && D >= kQE)
-            decode_item_q<D, GMAX, KVT, (GMAX <= 4 ? 8 : 4), 2>(a, rs, static_cast<uint32_t>(st.cu[s] + i), local, a.part_size, s,
-                                              kvh, lane);
+            decode_item_q<D, GMAX, KVT, (GMAX <= 4 ? 8 : 4), 2>(a, st, rs, row, local, a.part_size, s, kvh, lane);
         else
-            decode_item<D, GMAX, KVT, NL, NB, BUF>(a, rs, static_cast<uint32_t>(st.cu[s] + i), local, a.part_size,
-                                                   s, kvh, lane);
+            decode_item<D, GMAX, KVT, NL, NB, BUF>(a, st, rs, row, local, a.part_size, s, kvh, lane);
     }
 }
 
