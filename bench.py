@@ -66,7 +66,7 @@ class AttnBench:
             # quantize N(0,1) rows into the pool with the fused append kernel itself
             self.k = torch.zeros(rows * b0.head_dim, dtype=torch.int8, device=dev)
             self.v = torch.zeros_like(self.k)
-            if kv_dtype == K.KANSO_KV_INT8:
+            if kv_dtype in (K.KANSO_KV_INT8, K.KANSO_KV_FP8):
                 self.ks = torch.ones(rows, dtype=torch.float32, device=dev)
             else:
                 self.ks = torch.zeros(rows * b0.head_dim // 32, dtype=torch.float16, device=dev)
@@ -549,7 +549,8 @@ def main():
         del b1
         torch.cuda.empty_cache()
 
-        for kv, name in ((K.KANSO_KV_INT8, "config3_int8"), (K.KANSO_KV_Q8_0, "config3_q8_0")):
+        for kv, name in ((K.KANSO_KV_INT8, "config3_int8"), (K.KANSO_KV_Q8_0, "config3_q8_0"),
+                         (K.KANSO_KV_FP8, "config3_fp8")):
             c3 = [workloads.config3_quant_decode(num_blocks=131072, seed_offset=i) for i in range(8)]
             b3 = AttnBench(ctx, c3, kv, seed=3)
             r3 = b3.run(args.steps, args.warmup)

@@ -77,7 +77,11 @@ enum {
  *         scales [num_blocks][block_size][num_kv_heads][head_dim/32] f16 (IEEE
  *         binary16 bits), one scale per 32 elements, quantized with the Q8_0 rule
  *         of src/quant/q8_0.rs:13-32; head_dim must be a multiple of 32.       */
-enum { KANSO_KV_F32 = 0, KANSO_KV_INT8 = 1, KANSO_KV_Q8_0 = 2 };
+/* KV pool kinds. INT8 and FP8 keep one f32 scale per (token, KV head) and
+ * head_dim bytes per row (src/kv_cache/quantized_storage.rs:433-489); FP8 bytes are
+ * OCP E4M3FN (bias 7, no infinities, NaN = S.1111.111). Q8_0 keeps one f16 scale
+ * per 32 elements (head_dim % 32 == 0). */
+enum { KANSO_KV_F32 = 0, KANSO_KV_INT8 = 1, KANSO_KV_Q8_0 = 2, KANSO_KV_FP8 = 3 };
 
 /* Row order inside a pool block (every pool tensor and its scales alike).
  *   TOKEN_MAJOR: [num_blocks][block_size][num_kv_heads][...], the reference's

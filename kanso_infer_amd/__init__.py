@@ -30,14 +30,14 @@ import numpy as np
 import torch
 
 from . import _capi
-from ._capi import (KANSO_KV_F32, KANSO_KV_INT8, KANSO_KV_Q8_0, PackedStepC,
+from ._capi import (KANSO_KV_F32, KANSO_KV_FP8, KANSO_KV_INT8, KANSO_KV_Q8_0, PackedStepC,
                     PagedAttentionParamsC, RaggedAttentionParamsC, SeqPlanC)
 
 __all__ = [
     "EngineError", "Context", "PagedAttentionParams", "paged_attention_num_partitions",
     "validate_paged_attention_params", "gpu_paged_attention_v2", "paged_attention_v2",
     "ragged_paged_attention", "pack_step", "kv_append", "kv_reset_blocks", "gemv_q8_0",
-    "gemv_q4_k", "KANSO_KV_F32", "KANSO_KV_INT8", "KANSO_KV_Q8_0", "q8_0_packed_bytes",
+    "gemv_q4_k", "KANSO_KV_F32", "KANSO_KV_INT8", "KANSO_KV_Q8_0", "KANSO_KV_FP8", "q8_0_packed_bytes",
     "q8_0_pack", "gemm_q8_0", "gemm_q8_0_residual", "embed_q8_0", "qkv_rope_append",
     "gate_up_swiglu", "lm_head_argmax",
 ]

@@ -33,6 +33,7 @@ KANSO_DEV_TOKEN_OOB = 1 << 7
 KANSO_KV_F32 = 0
 KANSO_KV_INT8 = 1
 KANSO_KV_Q8_0 = 2
+KANSO_KV_FP8 = 3
 
 KANSO_POOL_TOKEN_MAJOR = 0
 KANSO_POOL_HEAD_MAJOR = 1

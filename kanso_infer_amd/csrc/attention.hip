@@ -20,7 +20,7 @@
 //    flight while the other is scored. Every query head of the GQA group is
 //    served from the same K/V registers: K/V bytes are read once per (token, KV
 //    head).
-//  * Decode rows, INT8 / Q8_0 pool: 8 bytes per lane (one b64 load), tiles kept
+//  * Decode rows, INT8 / Q8_0 / FP8 pool: 8 bytes per lane (one b64 load), tiles kept
 //    raw and dequantized when scored, row scales folded into score and
 //    probability.
 //  * Prefill-chunk rows: 16 rows x G heads per wave on the bf16 matrix cores with
@@ -35,8 +35,9 @@
 //    the online softmax rescales once per tile, not once per token.
 //  * A row whose context fits one partition is normalised and written directly;
 //    only rows split over several partitions go through the reduce kernel.
-//  * Quantized pools (INT8 per token-head scale, Q8_0 per-32 f16 scale) use the
-//    reference's products, (q as f32) * scale, reordered only by the scale folds.
+//  * Quantized pools (INT8 and FP8 E4M3 per token-head scale, Q8_0 per-32 f16
+//    scale) use the reference's products, (q as f32) * scale, reordered only by
+//    the scale folds.
 #include <cmath>
 #include <cstdlib>
 
@@ -192,6 +193,18 @@ struct KvLoader<KANSO_KV_INT8> {
     }
 };
 
+// FP8 pool (E4M3 bytes) with one f32 scale per (token, KV head): fp8_to_f32(q) * scale.
+template <>
+struct KvLoader<KANSO_KV_FP8> {
+    __device__ __forceinline__ static float4 load(const void* pool, const void* scales, size_t row, int D, int d0) {
+        const uint32_t w = *reinterpret_cast<const uint32_t*>(static_cast<const uint8_t*>(pool) + row * D + d0);
+        const float sc = static_cast<const float*>(scales)[row];
+        float x0, x1, x2, x3;
+        e4m3x4_to_f32(w, x0, x1, x2, x3);
+        return make_float4(x0 * sc, x1 * sc, x2 * sc, x3 * sc);
+    }
+};
+
 // Q8_0 pool with one f16 scale per 32 elements: d * (q as f32).
 template <>
 struct KvLoader<KANSO_KV_Q8_0> {
@@ -240,6 +253,18 @@ struct KvBuf<KANSO_KV_INT8> {
         const char4 q = __builtin_bit_cast(char4, w);
         return make_float4(static_cast<float>(q.x) * sc, static_cast<float>(q.y) * sc,
                            static_cast<float>(q.z) * sc, static_cast<float>(q.w) * sc);
+    }
+};
+
+template <>
+struct KvBuf<KANSO_KV_FP8> {
+    __device__ __forceinline__ static float4 load(__amdgpu_buffer_rsrc_t pool, __amdgpu_buffer_rsrc_t scales,
+                                                  uint32_t row, bool ok, int D, int d0) {
+        const uint32_t w = __builtin_amdgcn_raw_buffer_load_b32(pool, ok ? row * D + d0 : kOffNone, 0, 0);
+        const float sc = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(scales, ok ? row * 4u : kOffNone, 0, 0));
+        float x0, x1, x2, x3;
+        e4m3x4_to_f32(w, x0, x1, x2, x3);
+        return make_float4(x0 * sc, x1 * sc, x2 * sc, x3 * sc);
     }
 };
 
@@ -528,7 +553,7 @@ __device__ void decode_item(const AttnArgs& a, const SeqTable& st, const PoolRsr
 
 // ---------------------------------------------------------------- decode rows, 1-byte pools
 //
-// INT8 / Q8_0 pools keep their tiles raw: a lane loads QE = 8 elements (8 bytes,
+// INT8 / Q8_0 / FP8 pools keep their tiles raw: a lane loads QE = 8 elements (8 bytes,
 // one b64 buffer load) of a token row plus that row's scale, and dequantizes only
 // when the tile is scored. A tile of NL rows per lane then carries twice the bytes
 // of the float path in fewer registers. The per-row scale of K folds into the
@@ -548,7 +573,7 @@ struct DecodeTileQ {
 
 template <int KVT>
 __device__ __forceinline__ float load_row_scale(__amdgpu_buffer_rsrc_t sc, uint32_t row, bool ok, int D, int d0) {
-    if constexpr (KVT == KANSO_KV_INT8) {
+    if constexpr (KVT == KANSO_KV_INT8 || KVT == KANSO_KV_FP8) {
         return __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(sc, ok ? row * 4u : kOffNone, 0, 0));
     } else {
         const uint16_t hb = __builtin_amdgcn_raw_buffer_load_b16(
@@ -557,11 +582,20 @@ __device__ __forceinline__ float load_row_scale(__amdgpu_buffer_rsrc_t sc, uint3
     }
 }
 
-__device__ __forceinline__ void i8x8_to_f32(uint2 w, float (&f)[kQE]) {
+// 8 pool bytes -> f32: int8 (INT8, Q8_0) or E4M3 (FP8) values, before the scale.
+template <int KVT>
+__device__ __forceinline__ void bytes8_to_f32(uint2 w, float (&f)[kQE]) {
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
-        f[j] = static_cast<float>(static_cast<int8_t>((w.x >> (8 * j)) & 0xff));
-        f[4 + j] = static_cast<float>(static_cast<int8_t>((w.y >> (8 * j)) & 0xff));
+        if constexpr (KVT == KANSO_KV_FP8) {
+            if (j == 0) {
+                e4m3x4_to_f32(w.x, f[0], f[1], f[2], f[3]);
+                e4m3x4_to_f32(w.y, f[4], f[5], f[6], f[7]);
+            }
+        } else {
+            f[j] = static_cast<float>(static_cast<int8_t>((w.x >> (8 * j)) & 0xff));
+            f[4 + j] = static_cast<float>(static_cast<int8_t>((w.y >> (8 * j)) & 0xff));
+        }
     }
 }
 
@@ -584,7 +618,7 @@ __device__ __forceinline__ void decode_load_q(const AttnArgs& a, const PoolRsrc&
 
 // q is pre-multiplied by scale * log2(e), so the score is sum over lanes of
 // ks * sum(q k) in log2 units.
-template <int D, int GMAX, int NL>
+template <int D, int GMAX, int KVT, int NL>
 __device__ __forceinline__ void decode_compute_q(const AttnArgs& a, const PartView& pv, uint32_t tile0, int ts,
                                                  const float (&q)[GMAX][kQE], float (&acc)[GMAX][kQE],
                                                  float (&m)[GMAX], float (&l)[GMAX], const DecodeTileQ<NL>& tl) {
@@ -595,7 +629,7 @@ __device__ __forceinline__ void decode_compute_q(const AttnArgs& a, const PartVi
 #pragma unroll
     for (int i = 0; i < NL; ++i) {
         float kf[kQE];
-        i8x8_to_f32(tl.k[i], kf);
+        bytes8_to_f32<KVT>(tl.k[i], kf);
         const bool ok = tile0 + i * TPI + ts < pv.t_end;
 #pragma unroll
         for (int g = 0; g < GMAX; ++g) {
@@ -635,7 +669,7 @@ __device__ __forceinline__ void decode_compute_q(const AttnArgs& a, const PartVi
 #pragma unroll
     for (int i = 0; i < NL; ++i) {
         float vf[kQE];
-        i8x8_to_f32(tl.v[i], vf);
+        bytes8_to_f32<KVT>(tl.v[i], vf);
 #pragma unroll
         for (int g = 0; g < GMAX; ++g) {
             if (g >= static_cast<int>(G)) break;
@@ -689,7 +723,7 @@ __device__ void decode_item_q(const AttnArgs& a, const SeqTable& st, const PoolR
             if (tj >= t_end) break;
             const uint32_t nxt = tj + (NB - 1) * TT;
             if (nxt < t_end) decode_load_q<D, KVT, NL>(a, rs, pv, nxt, kvh, ts, dl, ring[(j + NB - 1) % NB]);
-            decode_compute_q<D, GMAX, NL>(a, pv, tj, ts, q, acc, m, l, ring[j]);
+            decode_compute_q<D, GMAX, KVT, NL>(a, pv, tj, ts, q, acc, m, l, ring[j]);
         }
     }
 
@@ -1139,6 +1173,7 @@ Stage1Fn pick_main_kv(uint32_t kv, uint32_t D, uint32_t G, bool buf, bool mfma) 
     if (kv == KANSO_KV_F32) return pick_decode<KANSO_KV_F32>(D, G, buf, mfma);
     if (kv == KANSO_KV_INT8) return pick_decode<KANSO_KV_INT8>(D, G, buf, mfma);
     if (kv == KANSO_KV_Q8_0) return pick_decode<KANSO_KV_Q8_0>(D, G, buf, mfma);
+    if (kv == KANSO_KV_FP8) return pick_decode<KANSO_KV_FP8>(D, G, buf, mfma);
     return nullptr;
 }
 
@@ -1226,7 +1261,7 @@ int run_ragged(kanso_ctx* ctx, const kanso_ragged_attention_params* p, const flo
                   p->block_size, p->max_num_blocks_per_seq);
         return KANSO_E_INVALID_SHAPE;
     }
-    if (p->kv_dtype > KANSO_KV_Q8_0) {
+    if (p->kv_dtype > KANSO_KV_FP8) {
         set_error("%s: unknown kv_dtype %u", who, p->kv_dtype);
         return KANSO_E_INVALID_ARG;
     }
@@ -1305,7 +1340,7 @@ int run_ragged(kanso_ctx* ctx, const kanso_ragged_attention_params* p, const flo
     const uint64_t elem = p->kv_dtype == KANSO_KV_F32 ? 4 : 1;
     const uint64_t rows = static_cast<uint64_t>(p->num_blocks) * p->block_size * HKV;
     const uint64_t pool_bytes = rows * D * elem;
-    const uint64_t scale_bytes = p->kv_dtype == KANSO_KV_INT8 ? rows * 4
+    const uint64_t scale_bytes = p->kv_dtype == KANSO_KV_INT8 || p->kv_dtype == KANSO_KV_FP8 ? rows * 4
                                  : p->kv_dtype == KANSO_KV_Q8_0 ? rows * (D / 32) * 2 : 0;
     const bool buf = p->num_blocks != 0 && pool_bytes < (1ull << 32);
     a.pool_bytes = buf ? static_cast<uint32_t>(pool_bytes) : 0u;

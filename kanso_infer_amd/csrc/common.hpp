@@ -138,4 +138,35 @@ __device__ __forceinline__ void raise_status(uint32_t* status, uint32_t bits) {
     atomicOr(status, bits);
 }
 
+// OCP FP8 E4M3FN (bias 7, 3 mantissa bits, subnormal step 2^-9, no infinities,
+// NaN = S.1111.111, largest finite 448). Encode: round to nearest, ties to even;
+// 464 and above saturate to 448 (the KV quantizer never reaches them).
+__device__ __forceinline__ uint32_t f32_to_e4m3(float x) {
+    const uint32_t u = __float_as_uint(x);
+    const uint32_t sign = (u >> 24) & 0x80u;
+    const uint32_t a = u & 0x7fffffffu;
+    if (a > 0x7f800000u) return sign | 0x7fu;
+    if (a >= 0x43e80000u) return sign | 0x7eu;
+    if (a >= 0x3c800000u) return sign | (((a + 0x7ffffu + ((a >> 20) & 1u)) >> 20) - (120u << 3));
+    return sign | static_cast<uint32_t>(__builtin_rintf(__uint_as_float(a) * 512.0f));
+}
+
+// Four E4M3 bytes of a word -> f32 with gfx950's packed conversion
+// (v_cvt_pk_f32_fp8: OCP E4M3FN on CDNA4), two bytes per instruction.
+__device__ __forceinline__ void e4m3x4_to_f32(uint32_t w, float& a, float& b, float& c, float& d) {
+    const auto lo = __builtin_amdgcn_cvt_pk_f32_fp8(static_cast<int>(w), false);
+    const auto hi = __builtin_amdgcn_cvt_pk_f32_fp8(static_cast<int>(w), true);
+    a = lo[0];
+    b = lo[1];
+    c = hi[0];
+    d = hi[1];
+}
+
+__device__ __forceinline__ float e4m3_to_f32(uint32_t b) {
+    const uint32_t e = (b >> 3) & 0xfu, m = b & 7u;
+    float v = e ? __uint_as_float(((e + 120u) << 23) | (m << 20)) : static_cast<float>(m) * 0.001953125f;
+    v = (b & 0x7fu) == 0x7fu ? __uint_as_float(0x7fc00000u) : v;
+    return (b & 0x80u) ? -v : v;
+}
+
 }  // namespace kanso

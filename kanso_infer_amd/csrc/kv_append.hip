@@ -2,7 +2,7 @@
 //
 // Reference: KvStorageKind::write_kv_slots (src/kv_cache/kind.rs:348-374) — an F32
 // scatter of [T, Hkv, D] rows into pool row `slot` (storage.rs:219-254), or per
-// token and KV head quantize_head_slice (quantized_storage.rs:452-469) for INT8;
+// token and KV head quantize_head_slice (quantized_storage.rs:452-486) for INT8 and FP8;
 // Q8_0 rows use BlockQ8_0::from_f32_slice (src/quant/q8_0.rs:13-32) per 32 values
 // with d stored as f16.
 //
@@ -82,6 +82,37 @@ __device__ void quant_row_int8(const float* __restrict__ x, uint32_t D, int lane
     if (lane == 0) *scale_out = scale;
 }
 
+// quantize_head_slice, FP8 arm (quantized_storage.rs:470-486): scale =
+// 2^ceil(log2(amax / 64)) (1 for amax = 0), q = E4M3(x * (1 / scale)). ceil(log2)
+// is exact here (frexp of amax / 64), scale and 1 / scale are powers of two, and
+// the E4M3 encode rounds to nearest even.
+template <int PER>
+__device__ void quant_row_fp8(const float* __restrict__ x, uint32_t D, int lane, uint8_t* __restrict__ q,
+                              float* __restrict__ scale_out) {
+    float vals[PER];
+    float amax = 0.f;
+#pragma unroll
+    for (int k = 0; k < PER; ++k) {
+        const uint32_t d = lane + k * kWave;
+        vals[k] = d < D ? x[d] : 0.f;
+        amax = fmaxf(amax, fabsf(vals[k]));
+    }
+    amax = wave_max_all(amax);
+    float scale = 1.0f;
+    if (amax > 0.f) {
+        int e2;
+        const float fr = frexpf(amax / 64.0f, &e2);
+        scale = ldexpf(1.0f, fr == 0.5f ? e2 - 1 : e2);
+    }
+    const float inv = 1.0f / scale;
+#pragma unroll
+    for (int k = 0; k < PER; ++k) {
+        const uint32_t d = lane + k * kWave;
+        if (d < D) q[d] = static_cast<uint8_t>(f32_to_e4m3(vals[k] * inv));
+    }
+    if (lane == 0) *scale_out = scale;
+}
+
 // BlockQ8_0::from_f32_slice per 32 elements: d = amax / 127; id = d != 0 ? 1 / d : 0;
 // q = round(x * id).clamp(-128, 127); d stored as f16 (round to nearest even).
 template <int PER>
@@ -124,6 +155,11 @@ __global__ __launch_bounds__(kAppendThreads) void append_quant(
         if (KVT == KANSO_KV_INT8) {
             quant_row_int8<PER>(ksrc, D, lane, kq + dst_row * D, static_cast<float*>(ks) + dst_row);
             quant_row_int8<PER>(vsrc, D, lane, vq + dst_row * D, static_cast<float*>(vs) + dst_row);
+        } else if (KVT == KANSO_KV_FP8) {
+            quant_row_fp8<PER>(ksrc, D, lane, reinterpret_cast<uint8_t*>(kq) + dst_row * D,
+                               static_cast<float*>(ks) + dst_row);
+            quant_row_fp8<PER>(vsrc, D, lane, reinterpret_cast<uint8_t*>(vq) + dst_row * D,
+                               static_cast<float*>(vs) + dst_row);
         } else {
             quant_row_q8_0<PER>(ksrc, D, lane, kq + dst_row * D, static_cast<__half*>(ks) + dst_row * (D / 32));
             quant_row_q8_0<PER>(vsrc, D, lane, vq + dst_row * D, static_cast<__half*>(vs) + dst_row * (D / 32));
@@ -131,7 +167,7 @@ __global__ __launch_bounds__(kAppendThreads) void append_quant(
     }
 }
 
-// Erase blocks: quant / f32 bytes -> 0, INT8 scales -> 1.0 (QuantizedKvBlock::reset,
+// Erase blocks: quant / f32 bytes -> 0, INT8 / FP8 scales -> 1.0 (QuantizedKvBlock::reset,
 // quantized_storage.rs:35-40), Q8_0 scales -> 0.
 __global__ __launch_bounds__(kAppendThreads) void reset_blocks_kernel(
     const uint32_t* __restrict__ blocks, uint32_t n, uint32_t num_blocks, uint32_t block_bytes,
@@ -149,7 +185,7 @@ __global__ __launch_bounds__(kAppendThreads) void reset_blocks_kernel(
             kw[i] = 0u;
             vw[i] = 0u;
         }
-        if (kv_dtype == KANSO_KV_INT8) {
+        if (kv_dtype == KANSO_KV_INT8 || kv_dtype == KANSO_KV_FP8) {
             float* ksf = static_cast<float*>(ks) + static_cast<size_t>(blk) * scale_elems;
             float* vsf = static_cast<float*>(vs) + static_cast<size_t>(blk) * scale_elems;
             for (uint32_t i = threadIdx.x; i < scale_elems; i += kAppendThreads) {
@@ -184,7 +220,7 @@ int check_common(uint32_t kv_dtype, uint32_t num_blocks, uint32_t block_size, ui
         set_error("%s: null pool", who);
         return KANSO_E_INVALID_ARG;
     }
-    if (kv_dtype > KANSO_KV_Q8_0) {
+    if (kv_dtype > KANSO_KV_FP8) {
         set_error("%s: unknown kv_dtype %u", who, kv_dtype);
         return KANSO_E_INVALID_ARG;
     }
@@ -236,8 +272,9 @@ int kanso_kv_append(kanso_ctx* ctx, uint32_t kv_dtype, const float* k, const flo
                            slot_mapping, num_tokens, row4, num_slots, static_cast<float4*>(k_pool),
                            static_cast<float4*>(v_pool), ctx->status);
     } else {
-        QuantFn fn = kv_dtype == KANSO_KV_INT8 ? pick_quant<KANSO_KV_INT8>(head_dim)
-                                               : pick_quant<KANSO_KV_Q8_0>(head_dim);
+        QuantFn fn = kv_dtype == KANSO_KV_INT8  ? pick_quant<KANSO_KV_INT8>(head_dim)
+                     : kv_dtype == KANSO_KV_FP8 ? pick_quant<KANSO_KV_FP8>(head_dim)
+                                                : pick_quant<KANSO_KV_Q8_0>(head_dim);
         const uint64_t rows = static_cast<uint64_t>(num_tokens) * num_kv_heads;
         const uint32_t grid = static_cast<uint32_t>(std::min<uint64_t>((rows + kAppendWaves - 1) / kAppendWaves, 4096));
         hipLaunchKernelGGL(fn, dim3(grid), dim3(kAppendThreads), 0, s, k, v, slot_mapping, num_tokens,
@@ -262,7 +299,7 @@ int kanso_kv_reset_blocks(kanso_ctx* ctx, uint32_t kv_dtype, const uint32_t* blo
     if (num_reset == 0) return KANSO_OK;
     const uint32_t elems = block_size * num_kv_heads * head_dim;
     const uint32_t block_bytes = kv_dtype == KANSO_KV_F32 ? elems * 4 : elems;
-    const uint32_t scale_elems = kv_dtype == KANSO_KV_INT8   ? block_size * num_kv_heads
+    const uint32_t scale_elems = kv_dtype == KANSO_KV_INT8 || kv_dtype == KANSO_KV_FP8 ? block_size * num_kv_heads
                                  : kv_dtype == KANSO_KV_Q8_0 ? block_size * num_kv_heads * (head_dim / 32)
                                                              : 0;
     hipStream_t s = as_stream(stream);

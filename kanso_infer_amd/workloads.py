@@ -58,7 +58,7 @@ class AttnBatch:
         d = self.head_dim
         if kv_dtype == 0:
             return 2 * d * 4
-        if kv_dtype == 1:
+        if kv_dtype in (1, 3):  # INT8, FP8: one f32 scale per row
             return 2 * (d + 4)
         return 2 * (d + 2 * d // 32)
 

@@ -45,6 +45,12 @@ struct DequantView {
             const int8_t* src = static_cast<const int8_t*>(pool) + row_idx * d;
             const float sc = static_cast<const float*>(scales)[row_idx];
             for (uint32_t i = 0; i < d; ++i) out[i] = static_cast<float>(src[i]) * sc;
+        } else if (kv_dtype == KANSO_KV_FP8) {
+            // FP8 arm (quantized_storage.rs:351-358, fp8_to_f32 :438-449): the E4M3
+            // value of the byte times the row's scale.
+            const uint8_t* src = static_cast<const uint8_t*>(pool) + row_idx * d;
+            const float sc = static_cast<const float*>(scales)[row_idx];
+            for (uint32_t i = 0; i < d; ++i) out[i] = oracle_e4m3_to_f32(src[i]) * sc;
         } else {
             // BlockQ8_0::dequantize (src/quant/q8_0.rs:35-39): d * (q as f32), with d
             // read back from its f16 storage.
@@ -249,6 +255,64 @@ float oracle_quantize_head_int8(const float* x, uint32_t n, int8_t* q) {
     return scale;
 }
 
+// OCP FP8 E4M3FN (float8 0.7.0's F8E4M3, called at quantized_storage.rs:444 and
+// :480; the crate is not vendored): sign, 4 exponent bits with bias 7, 3 mantissa
+// bits, subnormals of 2^-9 steps, no infinities, NaN = S.1111.111, largest finite
+// 448. Encoding rounds to nearest, ties to even (IEEE's default); inputs of 464
+// and above saturate to 448 (the KV quantizer never produces them: |x / scale| <= 64).
+uint8_t oracle_f32_to_e4m3(float x) {
+    uint32_t u;
+    std::memcpy(&u, &x, 4);
+    const uint8_t sign = static_cast<uint8_t>((u >> 24) & 0x80u);
+    const uint32_t a = u & 0x7fffffffu;
+    if (a > 0x7f800000u) return sign | 0x7f;  // NaN
+    if (a >= 0x43e80000u) return sign | 0x7e;  // >= 464
+    if (a >= 0x3c800000u) {                    // >= 2^-6: normal
+        const uint32_t r = (a + 0x7ffffu + ((a >> 20) & 1u)) >> 20;  // 3 mantissa bits, RNE
+        return static_cast<uint8_t>(sign | (r - (120u << 3)));
+    }
+    float f;
+    std::memcpy(&f, &a, 4);
+    return static_cast<uint8_t>(sign | static_cast<uint8_t>(std::nearbyint(f * 512.0f)));  // m * 2^-9
+}
+
+float oracle_e4m3_to_f32(uint8_t b) {
+    const uint32_t e = (b >> 3) & 0xfu, m = b & 7u;
+    float v;
+    if ((b & 0x7f) == 0x7f) {
+        v = std::nanf("");
+    } else if (e == 0) {
+        v = static_cast<float>(m) * 0.001953125f;
+    } else {
+        const uint32_t bits = ((e + 120u) << 23) | (m << 20);
+        std::memcpy(&v, &bits, 4);
+    }
+    return (b & 0x80) ? -v : v;
+}
+
+float oracle_quantize_head_fp8(const float* x, uint32_t n, uint8_t* q) {
+    // quantize_head_slice, QuantMode::Fp8 (src/kv_cache/quantized_storage.rs:470-486):
+    // scale = 2^ceil(log2(amax / 64)) (1 for amax = 0), q = E4M3(x * (1 / scale)).
+    // ceil(log2 y) is taken exactly from y's exponent bits; the reference's f32
+    // log2 could round to an integer for y within an ulp above a power of two,
+    // where the two differ (parity unpinned there).
+    float amax = 0.0f;
+    for (uint32_t i = 0; i < n; ++i) {
+        const float ax = std::fabs(x[i]);
+        if (ax > amax) amax = ax;
+    }
+    float scale = 1.0f;
+    if (amax > 0.0f) {
+        int e2;
+        const float fr = std::frexp(amax / 64.0f, &e2);  // amax/64 = fr * 2^e2, fr in [0.5, 1)
+        const int k = fr == 0.5f ? e2 - 1 : e2;
+        scale = std::ldexp(1.0f, k);
+    }
+    const float inv_scale = 1.0f / scale;
+    for (uint32_t i = 0; i < n; ++i) q[i] = oracle_f32_to_e4m3(x[i] * inv_scale);
+    return scale;
+}
+
 float oracle_quantize_q8_0_block(const float* x, int8_t* qs) {
     // BlockQ8_0::from_f32_slice (src/quant/q8_0.rs:13-32).
     float amax = 0.0f;
@@ -336,6 +400,15 @@ int oracle_kv_append(uint32_t kv_dtype, const float* k, const float* v,
                     kr + h * head_dim, head_dim, static_cast<int8_t*>(k_pool) + r * head_dim);
                 static_cast<float*>(v_scales)[r] = oracle_quantize_head_int8(
                     vr + h * head_dim, head_dim, static_cast<int8_t*>(v_pool) + r * head_dim);
+            }
+        } else if (kv_dtype == KANSO_KV_FP8) {
+            // write_quantized_kv_token, Fp8 mode: the INT8 layout with E4M3 bytes.
+            for (uint32_t h = 0; h < num_kv_heads; ++h) {
+                const size_t r = slot * num_kv_heads + h;
+                static_cast<float*>(k_scales)[r] = oracle_quantize_head_fp8(
+                    kr + h * head_dim, head_dim, static_cast<uint8_t*>(k_pool) + r * head_dim);
+                static_cast<float*>(v_scales)[r] = oracle_quantize_head_fp8(
+                    vr + h * head_dim, head_dim, static_cast<uint8_t*>(v_pool) + r * head_dim);
             }
         } else {
             // Q8_0 rows: BlockQ8_0::from_f32_slice per 32 elements, d stored as f16.

@@ -65,6 +65,9 @@ int oracle_pack_step(const kanso_seq_plan* plan, uint32_t num_seqs,
 
 /* quantize_head_slice, INT8 arm (src/kv_cache/quantized_storage.rs:452-469). */
 float oracle_quantize_head_int8(const float* x, uint32_t n, int8_t* q);
+float oracle_quantize_head_fp8(const float* x, uint32_t n, uint8_t* q);
+uint8_t oracle_f32_to_e4m3(float x);
+float oracle_e4m3_to_f32(uint8_t b);
 
 /* BlockQ8_0::from_f32_slice (src/quant/q8_0.rs:13-32) on 32 values; returns d (f32). */
 float oracle_quantize_q8_0_block(const float* x, int8_t* qs);

@@ -13,7 +13,7 @@ import numpy as np
 
 LIB_PATH = Path(__file__).resolve().parent / "libkanso_oracle.so"
 
-KV_F32, KV_INT8, KV_Q8_0 = 0, 1, 2
+KV_F32, KV_INT8, KV_Q8_0, KV_FP8 = 0, 1, 2, 3
 
 _lib: C.CDLL | None = None
 
@@ -45,6 +45,9 @@ def lib() -> C.CDLL:
             "oracle_ragged_attention": (I, [V, V, V, V, V, V, V, V, C.POINTER(RaggedParams), V, I]),
             "oracle_pack_step": (I, [V, U, V, V, U, V, V, V, V, V, V, V, V]),
             "oracle_quantize_head_int8": (F, [V, U, V]),
+            "oracle_quantize_head_fp8": (F, [V, U, V]),
+            "oracle_f32_to_e4m3": (C.c_uint8, [F]),
+            "oracle_e4m3_to_f32": (F, [C.c_uint8]),
             "oracle_quantize_q8_0_block": (F, [V, V]),
             "oracle_f32_to_f16": (C.c_uint16, [F]),
             "oracle_f16_to_f32": (F, [C.c_uint16]),
@@ -148,6 +151,21 @@ def quantize_head_int8(x):
     return q, np.float32(s)
 
 
+def quantize_head_fp8(x):
+    x = _f32(x)
+    q = np.zeros(x.size, dtype=np.uint8)
+    s = lib().oracle_quantize_head_fp8(_p(x), x.size, _p(q))
+    return q, np.float32(s)
+
+
+def f32_to_e4m3(x: float) -> int:
+    return int(lib().oracle_f32_to_e4m3(C.c_float(float(x))))
+
+
+def e4m3_to_f32(b: int) -> float:
+    return float(lib().oracle_e4m3_to_f32(C.c_uint8(int(b))))
+
+
 def quantize_q8_0_block(x):
     x = _f32(x)
     assert x.size == 32
@@ -170,7 +188,7 @@ def kv_pool_arrays(kv_dtype, num_blocks, block_size, num_kv_heads, head_dim):
     if kv_dtype == KV_F32:
         return (np.zeros(rows * head_dim, np.float32), np.zeros(rows * head_dim, np.float32),
                 None, None)
-    if kv_dtype == KV_INT8:
+    if kv_dtype in (KV_INT8, KV_FP8):
         return (np.zeros(rows * head_dim, np.int8), np.zeros(rows * head_dim, np.int8),
                 np.ones(rows, np.float32), np.ones(rows, np.float32))
     return (np.zeros(rows * head_dim, np.int8), np.zeros(rows * head_dim, np.int8),

@@ -96,7 +96,7 @@ def test_device_flags_raise(ctx):
 
 
 @pytest.mark.parametrize("seed", range(4))
-@pytest.mark.parametrize("kv_dtype", [oracle.KV_F32, oracle.KV_INT8, oracle.KV_Q8_0])
+@pytest.mark.parametrize("kv_dtype", [oracle.KV_F32, oracle.KV_INT8, oracle.KV_Q8_0, oracle.KV_FP8])
 def test_ragged_small(ctx, seed, kv_dtype):
     shapes = [dict(), dict(num_heads=16, num_kv_heads=4), dict(num_heads=8, num_kv_heads=1,
                                                               head_dim=128),
@@ -111,7 +111,7 @@ def test_ragged_small(ctx, seed, kv_dtype):
 
 
 @pytest.mark.parametrize("partition", [32, 64, 128, 512])
-@pytest.mark.parametrize("kv_dtype", [oracle.KV_F32, oracle.KV_Q8_0])
+@pytest.mark.parametrize("kv_dtype", [oracle.KV_F32, oracle.KV_Q8_0, oracle.KV_FP8])
 def test_explicit_partition_size(ctx, partition, kv_dtype):
     """A caller-chosen split-K partition gives the oracle's result (decode and chunk rows)."""
     b = workloads.small_mixed(11)
@@ -133,7 +133,7 @@ def test_rejects_bad_partition_size(ctx):
 
 
 @pytest.mark.parametrize("variant", ["config1", "config2_small_pool", "config3_int8",
-                                     "config3_q8_0"])
+                                     "config3_q8_0", "config3_fp8"])
 def test_baseline_shapes(ctx, variant):
     """The BASELINE configs at their real shapes (pools sized to what the tables use)."""
     if variant == "config1":
@@ -142,7 +142,8 @@ def test_baseline_shapes(ctx, variant):
         b, kv = workloads.config2_mixed(num_blocks=10000), oracle.KV_F32
     else:
         b = workloads.config3_quant_decode()
-        kv = oracle.KV_INT8 if variant.endswith("int8") else oracle.KV_Q8_0
+        kv = {"int8": oracle.KV_INT8, "q8_0": oracle.KV_Q8_0,
+              "fp8": oracle.KV_FP8}[variant.split("_", 1)[1]]
     kp, vp, ks, vs = fill_pool(b, kv, 7)
     q = np.random.default_rng(8).standard_normal(
         b.total_q * b.num_heads * b.head_dim).astype(np.float32)
@@ -165,3 +166,25 @@ def test_ragged_equals_decode_entry(ctx):
                          dev(b.context_lens.astype(np.uint32)), out)
     ctx.check_device_status()
     np.testing.assert_array_equal(host(out), ragged)
+
+
+def test_fp8_pool_decodes_every_finite_code(ctx):
+    """Contexts of one token: the output is exactly that token's V row, so every
+    finite E4M3 code (254 of 256) is decoded by the kernel and compared bit for bit."""
+    codes = np.array([c for c in range(256) if c not in (0x7f, 0xff)], np.uint8)
+    d, S, bs = 64, 4, 16
+    vrows = np.zeros((S, d), np.uint8)
+    vrows.ravel()[:codes.size] = codes
+    b = workloads.AttnBatch(np.ones(S, np.int64), np.ones(S, np.int64),
+                            np.arange(S, dtype=np.uint32)[:, None], S, num_heads=1,
+                            num_kv_heads=1, head_dim=d, block_size=bs, scale=0.125)
+    kp = np.zeros(S * bs * d, np.int8)
+    vp = np.zeros(S * bs * d, np.int8)
+    for s in range(S):  # token 0 of block s
+        vp[s * bs * d:s * bs * d + d] = vrows[s].view(np.int8)
+    ks = np.ones(S * bs, np.float32)
+    vs = np.full(S * bs, 0.5, np.float32)
+    q = np.random.default_rng(3).standard_normal(S * d).astype(np.float32)
+    got = run_ragged_gpu(ctx, b, q, kp, vp, ks, vs, oracle.KV_FP8).reshape(S, d)
+    dec = np.array([oracle.e4m3_to_f32(c) for c in range(256)], np.float32)
+    np.testing.assert_array_equal(got, dec[vrows] * np.float32(0.5))

@@ -48,7 +48,7 @@ def test_pack_short_table_flagged(ctx):
         ctx.check_device_status()
 
 
-KV_KINDS = [oracle.KV_F32, oracle.KV_INT8, oracle.KV_Q8_0]
+KV_KINDS = [oracle.KV_F32, oracle.KV_INT8, oracle.KV_Q8_0, oracle.KV_FP8]
 
 
 def _pools(kv, nb, bs, h, d):
@@ -94,6 +94,15 @@ def test_append_config3_round_trip(ctx, kv):
         return
     rows = (slots[:, None] * h + np.arange(h)).ravel()
     q = kp.reshape(-1, d)[rows].astype(np.float32)
+    if kv == oracle.KV_FP8:
+        # E4M3: 3 mantissa bits, so half a step is 1/16 of the value (normal range)
+        # or half of the 2^-9 subnormal step
+        dec = np.array([oracle.e4m3_to_f32(b) for b in range(256)], np.float32)
+        sc = host(dev_arrays[2]).view(np.float32)[rows][:, None]
+        recon = dec[kp.reshape(-1, d)[rows].view(np.uint8)] * sc
+        err = np.abs(recon - k.reshape(-1, d))
+        assert (err <= np.abs(k.reshape(-1, d)) / 16 + sc * 2.0 ** -10 + 1e-6).all()
+        return
     if kv == oracle.KV_INT8:
         sc = host(dev_arrays[2]).view(np.float32)[rows][:, None]
         recon = q * sc
@@ -130,7 +139,7 @@ def test_reset_blocks(ctx, kv):
     ctx.check_device_status()
     kp = host(dev_arrays[0]).reshape(nb, -1)
     assert not kp[[1, 6]].any() and kp[[0, 2, 3, 4, 5, 7]].any()
-    if kv == oracle.KV_INT8:
+    if kv in (oracle.KV_INT8, oracle.KV_FP8):
         ks = host(dev_arrays[2]).view(np.float32).reshape(nb, -1)
         assert (ks[[1, 6]] == 1.0).all()
     if kv == oracle.KV_Q8_0:

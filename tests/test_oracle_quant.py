@@ -207,3 +207,115 @@ def test_quantized_weights_round_trip_and_batch():
     assert np.abs(dense4 - wf).max() < 0.02
     y4 = oracle.gemv_q4_k(w4, x, rows, cols, nthreads=2).reshape(batch, rows)
     np.testing.assert_allclose(y4, x.astype(np.float64) @ dense4.T, rtol=1e-4, atol=1e-4)
+
+
+# ---------------------------------------------------------------- FP8 (E4M3FN) KV
+
+def _e4m3_table():
+    return np.array([oracle.e4m3_to_f32(b) for b in range(256)], np.float32)
+
+
+def test_e4m3_decode_closed_form():
+    # OCP E4M3FN: bias 7, 3 mantissa bits, subnormal step 2^-9, NaN = S.1111.111.
+    dec = _e4m3_table()
+    assert dec[0x00] == 0.0 and dec[0x01] == 2.0 ** -9 and dec[0x07] == 7 * 2.0 ** -9
+    assert dec[0x08] == 2.0 ** -6 and dec[0x38] == 1.0 and dec[0x39] == 1.125
+    assert dec[0x7e] == 448.0 and dec[0xfe] == -448.0 and dec[0xb8] == -1.0
+    assert np.isnan(dec[0x7f]) and np.isnan(dec[0xff])
+    assert dec[0x80] == 0.0 and np.signbit(dec[0x80])
+    finite = dec[~np.isnan(dec)]
+    assert finite.size == 254 and np.unique(finite[finite > 0]).size == 126
+
+
+def test_e4m3_encode_is_round_to_nearest_even():
+    """Pinned by brute force: the nearest of the 254 finite codes, ties to the even
+    mantissa, for random values, every exact code and every midpoint between codes."""
+    dec = _e4m3_table()
+    for b in range(256):
+        if not np.isnan(dec[b]):
+            assert oracle.f32_to_e4m3(dec[b]) == b or (dec[b] == 0 and b in (0, 0x80))
+    pos = np.array(sorted({float(dec[b]) for b in range(0x7f)}), np.float64)
+    mids = ((pos[1:] + pos[:-1]) / 2).astype(np.float32)
+    rng = np.random.default_rng(5)
+    xs = np.concatenate([mids, -mids] + [rng.standard_normal(3000).astype(np.float32) * s
+                                         for s in (1e-3, 0.05, 1.0, 20.0, 60.0)])
+    fin = [b for b in range(256) if not np.isnan(dec[b])]
+    fvals = dec[fin].astype(np.float64)
+    for x in xs:
+        d = np.abs(fvals - float(x))
+        cands = [fin[i] for i in np.nonzero(d == d.min())[0]]
+        cands = [c for c in cands if (c >> 7) == int(np.signbit(x))] or cands
+        want = min(cands, key=lambda c: (c & 1, c))
+        assert oracle.f32_to_e4m3(float(x)) == want, (x, cands)
+
+
+def test_fp8_head_quantizer_scale_rule_and_reference_kat():
+    # scale = 2^ceil(log2(amax / 64)), 1 for amax = 0 (quantized_storage.rs:470-486)
+    for amax, want in ((64.0, 1.0), (64.0001, 2.0), (32.0, 0.5), (33.0, 1.0), (1.0, 2.0 ** -6),
+                       (448.0, 8.0)):
+        x = np.zeros(64, np.float32)
+        x[7] = -amax
+        q, s = oracle.quantize_head_fp8(x)
+        assert s == np.float32(want)
+        assert q[7] == oracle.f32_to_e4m3(np.float32(-amax) * np.float32(1.0 / want))
+    q, s = oracle.quantize_head_fp8(np.zeros(64, np.float32))
+    assert s == 1.0 and not q.any()
+    # tests/test_quantized_kv_cache.rs:88-166 inputs (4 heads x 64): these values are
+    # exact in E4M3 after scaling, so reconstruction is exact (the test asks <= 1%).
+    i = np.arange(4 * 64)
+    k = ((i % 16) * 0.5 - 3.5).astype(np.float32)
+    k[k == 0] = 1.0
+    v = ((i % 8) * 1.0 + 0.5).astype(np.float32)
+    dec = _e4m3_table()
+    for raw in (k, v):
+        recon = np.zeros_like(raw)
+        for h in range(4):
+            q, s = oracle.quantize_head_fp8(raw[h * 64:(h + 1) * 64])
+            recon[h * 64:(h + 1) * 64] = dec[q] * s
+        np.testing.assert_array_equal(recon, raw)
+    # random rows: within half a step of E4M3 (1/16 relative, or half of 2^-9 * scale)
+    rng = np.random.default_rng(6)
+    for _ in range(200):
+        x = (rng.standard_normal(64) * rng.uniform(1e-3, 100)).astype(np.float32)
+        q, s = oracle.quantize_head_fp8(x)
+        assert np.abs(x).max() / s <= 64.0
+        assert np.all(np.abs(dec[q] * s - x) <= np.abs(x) / 16 + s * 2.0 ** -10 + 1e-7)
+
+
+def test_fp8_pool_layout_is_the_int8_layout():
+    rng = np.random.default_rng(7)
+    nb, bs, h, d = 4, 4, 2, 64
+    slots = np.array([3, 9], np.int64)
+    k = rng.standard_normal((2, h * d)).astype(np.float32)
+    kq, vq, ks, vs = oracle.kv_pool_arrays(oracle.KV_FP8, nb, bs, h, d)
+    assert kq.nbytes + vq.nbytes + ks.nbytes + vs.nbytes == (2 * h * d + 8 * h) * nb * bs
+    oracle.kv_append(oracle.KV_FP8, k, k, slots, nb, bs, h, d, kq, vq, ks, vs)
+    for t, s in enumerate(slots):
+        for hh in range(h):
+            q, sc = oracle.quantize_head_fp8(k[t, hh * d:(hh + 1) * d])
+            r = s * h + hh
+            np.testing.assert_array_equal(kq.reshape(-1, d)[r].view(np.uint8), q)
+            assert ks[r] == sc
+
+
+def test_fp8_pool_attention_is_f32_attention_over_the_dequantized_pool():
+    from kanso_infer_amd import workloads
+    b = workloads.small_mixed(1)
+    rng = np.random.default_rng(8)
+    rows, width = b.num_blocks * b.block_size, b.num_kv_heads * b.head_dim
+    k = rng.standard_normal((rows, width), dtype=np.float32)
+    v = rng.standard_normal((rows, width), dtype=np.float32)
+    kp, vp, ks, vs = oracle.kv_pool_arrays(oracle.KV_FP8, b.num_blocks, b.block_size,
+                                           b.num_kv_heads, b.head_dim)
+    oracle.kv_append(oracle.KV_FP8, k, v, np.arange(rows), b.num_blocks, b.block_size,
+                     b.num_kv_heads, b.head_dim, kp, vp, ks, vs)
+    q = rng.standard_normal(b.total_q * b.num_heads * b.head_dim).astype(np.float32)
+    args = dict(num_heads=b.num_heads, num_kv_heads=b.num_kv_heads, head_dim=b.head_dim,
+                block_size=b.block_size, scale=b.scale, num_blocks=b.num_blocks)
+    got = oracle.ragged_attention(q, kp, vp, b.block_tables, b.cu_seqlens, b.context_lens,
+                                  kv_dtype=oracle.KV_FP8, k_scales=ks, v_scales=vs, **args)
+    dec = _e4m3_table()
+    kf = (dec[kp.view(np.uint8)].reshape(-1, b.head_dim) * ks[:, None]).ravel()
+    vf = (dec[vp.view(np.uint8)].reshape(-1, b.head_dim) * vs[:, None]).ravel()
+    want = oracle.ragged_attention(q, kf, vf, b.block_tables, b.cu_seqlens, b.context_lens, **args)
+    np.testing.assert_array_equal(got, want)
