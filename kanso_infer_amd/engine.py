@@ -80,6 +80,19 @@ class ModelConfig:
         return (per_layer * self.num_hidden_layers + tables) // 32 * 34
 
 
+def quantize_q8_0_rows(ctx: Context, x: np.ndarray) -> np.ndarray:
+    """f32 [rows, in] -> GGUF Q8_0 rows ([rows][in/32] x 34 B) with the device
+    quantizer (kanso_quantize_q8_0, BlockQ8_0::from_f32_slice rounding)."""
+    a = np.ascontiguousarray(x, dtype=np.float32)
+    if a.size == 0 or a.shape[-1] % 32:
+        raise EngineError(-2, f"Q8_0 rows need a multiple of 32 columns (shape {a.shape})")
+    xd = torch.from_numpy(a.ravel()).to("cuda:0")
+    out = torch.empty(a.size // 32 * 34, dtype=torch.uint8, device="cuda:0")
+    _check(ctx._lib.kanso_quantize_q8_0(ctx.handle, xd.data_ptr(), a.size, out.data_ptr(),
+                                        _stream(None)))
+    return out.cpu().numpy()
+
+
 class Model:
     """The device decoder (kanso_model): packed Q8_0 projections, F32 paged KV pool."""
 
@@ -122,6 +135,17 @@ class Model:
         for li, layer in enumerate(weights["layers"]):
             for name, kind in kinds.items():
                 self.set_weight(kind, li, layer[name])
+
+    @classmethod
+    def from_gguf(cls, ctx: Context, path, max_position: int = 8192) -> "Model":
+        """A model with the shape and weights of a llama GGUF file
+        (ModelWeights::load_from_gguf, src/weights.rs:328-486)."""
+        from . import gguf
+        g = gguf.GGUFFile(path)
+        cfg = gguf.model_config(g, max_position=max_position)
+        model = cls(ctx, cfg)
+        model.load_weights(gguf.load_weights(g, cfg, lambda a: quantize_q8_0_rows(ctx, a)))
+        return model
 
     def init_random(self, seed: int = 0x5EED0057, std: float = 0.02) -> None:
         _check(self._lib.kanso_model_init_random(self.handle, seed, std))

@@ -164,3 +164,30 @@ def test_engine_checksum_matches_oracle(ctx, cfg, budget, total_blocks):
     gen_a, gen_b = run_both(eng, ref, reqs)
     assert fnv1a_64(gen_a) == R.fnv1a_64(gen_b) == oracle.fnv1a_64(gen_b)
     assert len(gen_a) == sum(g for _, g, _ in reqs)
+
+
+def test_model_from_gguf_matches_oracle(ctx, tmp_path):
+    """A llama GGUF (Q8_0 matrices with llama.cpp's interleaved Q/K rows, one F16
+    matrix quantized on load, F32 norms) through Model.from_gguf: logits equal the
+    oracle model's on the weights the host reader maps from the same file."""
+    from gguf_writer import llama_file
+    from kanso_infer_amd import gguf
+    bs, nblocks = 16, 40
+    w = random_weights(SMALL, seed=21)
+    path = tmp_path / "small.gguf"
+    llama_file(path, SMALL, w, dense=("blk.1.ffn_down.weight",))
+    gm = Model.from_gguf(ctx, path, max_position=4096)
+    gm.alloc_kv(nblocks, bs, 512, 64)
+    g = gguf.GGUFFile(path)
+    w_host = gguf.load_weights(g, gguf.model_config(g),
+                               lambda a: oracle.quantize_row_q8_0(np.ascontiguousarray(a, np.float32)))
+    om = OracleModel(SMALL, w_host, nblocks, bs)
+    rng = np.random.default_rng(12)
+    for step, plan in enumerate(mixed_plans(rng, bs, SMALL["vocab"], nblocks)):
+        rows, toks, tabs = compact(plan, bs)
+        S = rows.shape[0]
+        logits = torch.empty(S * SMALL["vocab"], device="cuda:0")
+        gm.forward(rows, toks, tabs, logits=logits)
+        ctx.check_device_status()
+        assert_close(host(logits).reshape(S, SMALL["vocab"]), om.logits(plan),
+                     what=f"gguf logits step {step}")
