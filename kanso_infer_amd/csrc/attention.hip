@@ -785,6 +785,216 @@ __device__ __forceinline__ floatx4 mfma3(const Bf16Split& a, const Bf16Split& b,
     return c;
 }
 
+// ---------------------------------------------------------------- decode rows, 1-byte pools, S on MFMA
+//
+// head_dim 64, GQA groups of at most 4 heads: S = Q K^T of a decode row runs on
+// v_mfma_f32_16x16x32_bf16. Q (query heads x 32 dims, split into bf16 hi + lo) is
+// the A operand, built once per item; K^T (32 dims x 16 keys) is the B operand, and
+// lane l's share of it is exactly one 8-byte load of its key's row (key l % 16,
+// dims 8 (l / 16) .. +7 of a 32-dim half): int8 and E4M3 values are exact in bf16, so
+// K is not split. C lands as S[head 4 (l / 16) + r][key l % 16]: the 16 lanes of the
+// first row hold every head's score of their key, so the softmax runs once per key,
+// not once per lane of a key. P V stays on the vector ALU: lane l accumulates its
+// key's V row (16 of the dims) with that key's probabilities, fetched from the
+// first-row lane of the key by one shuffle per head and 16-key group; the 16 keys of
+// a row are summed once per item. Scales as in the vector path: the K scale of a
+// key (per 32-dim half for Q8_0) multiplies its score, the V scale its probability.
+// Used for FP8 pools, whose byte conversion made the vector path instruction-bound
+// (config 3: 38.0 -> 33.7 us); INT8 and Q8_0 pools measured slower here (32.0 -> 34.1
+// and 33.1 -> 37.5 us: their cost is the chain of dependent loads, not the ALU), so
+// they keep the vector path.
+constexpr int kMqGroups = 3;  // 16-key groups per tile (4 spills with FP8 and Q8_0)
+
+template <int NG>
+struct MqTile {
+    uint2 k[NG][2], v[NG][2];     // [group][32-dim half]: 8 bytes of key (16 gi + l % 16)
+    float ks[NG][2], vs[NG][2];   // row scales ([gi][0] only for INT8 / FP8)
+};
+
+template <int KVT, int NG>
+__device__ __forceinline__ void mq_load(const AttnArgs& a, const PoolRsrc& rs, const PartView& pv, uint32_t tile0,
+                                        uint32_t kvh, int c, int j, MqTile<NG>& tl) {
+#pragma unroll
+    for (int gi = 0; gi < NG; ++gi) {
+        const uint32_t key = tile0 + 16 * gi + c;
+        const bool ok = key < pv.t_end;
+        const uint32_t r = static_cast<uint32_t>(pool_row(a, pv, ok ? key : tile0, kvh));
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+            const uint32_t off = ok ? r * 64u + static_cast<uint32_t>(32 * h + 8 * j) : kOffNone;
+            tl.k[gi][h] = __builtin_bit_cast(uint2, __builtin_amdgcn_raw_buffer_load_b64(rs.k, off, 0, 0));
+            tl.v[gi][h] = __builtin_bit_cast(uint2, __builtin_amdgcn_raw_buffer_load_b64(rs.v, off, 0, 0));
+            if (KVT == KANSO_KV_Q8_0 || h == 0) {
+                tl.ks[gi][h] = load_row_scale<KVT>(rs.ks, r, ok, 64, 32 * h);
+                tl.vs[gi][h] = load_row_scale<KVT>(rs.vs, r, ok, 64, 32 * h);
+            }
+        }
+    }
+}
+
+template <int KVT>
+__device__ __forceinline__ bf16x8 bytes8_to_bf16(uint2 w) {
+    float f[kQE];
+    bytes8_to_f32<KVT>(w, f);
+    bf16x8 r;
+#pragma unroll
+    for (int e = 0; e < kQE; ++e) r[e] = static_cast<__bf16>(f[e]);  // exact: 8 significant bits at most
+    return r;
+}
+
+template <int GMAX, int KVT, int NG>
+__device__ __forceinline__ void mq_compute(const AttnArgs& a, const PartView& pv, uint32_t tile0, int lane,
+                                           const Bf16Split (&qa)[2], float (&acc)[GMAX][2][kQE],
+                                           float (&m)[GMAX], float (&l)[GMAX], const MqTile<NG>& tl) {
+    const int c = lane & 15;
+    const uint32_t G = a.group;
+    float sc[NG][4];  // S[head r][key 16 gi + c] (first row of lanes)
+#pragma unroll
+    for (int gi = 0; gi < NG; ++gi) {
+        const bf16x8 k0 = bytes8_to_bf16<KVT>(tl.k[gi][0]), k1 = bytes8_to_bf16<KVT>(tl.k[gi][1]);
+        const floatx4 z = {0.f, 0.f, 0.f, 0.f};
+        floatx4 s0 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(qa[0].hi, k0, z, 0, 0, 0);
+        s0 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(qa[0].lo, k0, s0, 0, 0, 0);
+        floatx4 s1 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(qa[1].hi, k1, z, 0, 0, 0);
+        s1 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(qa[1].lo, k1, s1, 0, 0, 0);
+        const bool ok = tile0 + 16 * gi + c < pv.t_end;
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            const float sv = KVT == KANSO_KV_Q8_0 ? s0[r] * tl.ks[gi][0] + s1[r] * tl.ks[gi][1]
+                                                  : (s0[r] + s1[r]) * tl.ks[gi][0];
+            sc[gi][r] = ok ? sv : -INFINITY;
+        }
+    }
+    float alpha[GMAX];
+#pragma unroll
+    for (int g = 0; g < GMAX; ++g) {
+        if (g >= static_cast<int>(G)) break;
+        float mt = -INFINITY;
+#pragma unroll
+        for (int gi = 0; gi < NG; ++gi) mt = fmaxf(mt, sc[gi][g]);
+        mt = __shfl(group_max<16>(mt), 0, kWave);  // the first row holds the heads
+        const float mn = fmaxf(m[g], mt);          // finite: every tile holds a live key
+        alpha[g] = fast_exp2(m[g] - mn);
+        m[g] = mn;
+        float ps = 0.f;
+#pragma unroll
+        for (int gi = 0; gi < NG; ++gi) {
+            sc[gi][g] = fast_exp2(sc[gi][g] - mn);
+            ps += sc[gi][g];
+        }
+        ps = __shfl(group_sum<16>(ps), 0, kWave);
+        l[g] = l[g] * alpha[g] + ps;
+#pragma unroll
+        for (int h = 0; h < 2; ++h)
+#pragma unroll
+            for (int e = 0; e < kQE; ++e) acc[g][h][e] *= alpha[g];
+    }
+#pragma unroll
+    for (int gi = 0; gi < NG; ++gi) {
+        float v0[kQE], v1[kQE];
+        bytes8_to_f32<KVT>(tl.v[gi][0], v0);
+        bytes8_to_f32<KVT>(tl.v[gi][1], v1);
+#pragma unroll
+        for (int g = 0; g < GMAX; ++g) {
+            if (g >= static_cast<int>(G)) break;
+            const float p = __shfl(sc[gi][g], c, kWave);  // key c's probability for head g
+            const float p0 = p * tl.vs[gi][0];
+            const float p1 = KVT == KANSO_KV_Q8_0 ? p * tl.vs[gi][1] : p0;
+#pragma unroll
+            for (int e = 0; e < kQE; ++e) {
+                acc[g][0][e] += p0 * v0[e];
+                acc[g][1][e] += p1 * v1[e];
+            }
+        }
+    }
+}
+
+template <int GMAX, int KVT, int NB>
+__device__ void decode_item_mq(const AttnArgs& a, const SeqTable& st, const PoolRsrc& rs, uint32_t row,
+                               uint32_t part, uint32_t P, uint32_t seq, uint32_t kvh, int lane) {
+    constexpr int NG = kMqGroups;
+    constexpr int TT = 16 * NG;
+    const int c = lane & 15, j = lane >> 4;
+    const uint32_t G = a.group;
+    const int32_t ql = st.cu[seq + 1] - st.cu[seq];
+    const uint32_t limit = row_limit(st.ctx[seq], ql, static_cast<int32_t>(row) - st.cu[seq], a.capacity);
+    const uint32_t t_begin = part * P;
+    const uint32_t t_end = min(t_begin + P, limit);
+    const PartView pv = load_part(a, seq, t_begin, t_end, lane);
+
+    Bf16Split qa[2];  // A operand: head c, dims 32 h + 8 j .. +7 (zero rows past the group)
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+        float x[kQE] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+        if (c < static_cast<int>(G)) {
+            const float4* src = reinterpret_cast<const float4*>(
+                a.q + (static_cast<size_t>(row) * a.num_heads + kvh * G + c) * 64 + 32 * h + 8 * j);
+            const float4 x0 = src[0], x1 = src[1];
+            const float xs[kQE] = {x0.x, x0.y, x0.z, x0.w, x1.x, x1.y, x1.z, x1.w};
+#pragma unroll
+            for (int e = 0; e < kQE; ++e) x[e] = xs[e] * a.scale_log2;
+        }
+        qa[h] = split8(x);
+    }
+    float acc[GMAX][2][kQE], m[GMAX], l[GMAX];
+#pragma unroll
+    for (int g = 0; g < GMAX; ++g) {
+        m[g] = -INFINITY;
+        l[g] = 0.f;
+#pragma unroll
+        for (int h = 0; h < 2; ++h)
+#pragma unroll
+            for (int e = 0; e < kQE; ++e) acc[g][h][e] = 0.f;
+    }
+
+    MqTile<NG> ring[NB];
+#pragma unroll
+    for (int i = 0; i + 1 < NB; ++i)
+        if (t_begin + i * TT < t_end) mq_load<KVT, NG>(a, rs, pv, t_begin + i * TT, kvh, c, j, ring[i]);
+    for (uint32_t t0 = t_begin; t0 < t_end; t0 += NB * TT) {
+#pragma unroll
+        for (int i = 0; i < NB; ++i) {
+            const uint32_t ti = t0 + i * TT;
+            if (ti >= t_end) break;
+            const uint32_t nxt = ti + (NB - 1) * TT;
+            if (nxt < t_end) mq_load<KVT, NG>(a, rs, pv, nxt, kvh, c, j, ring[(i + NB - 1) % NB]);
+            mq_compute<GMAX, KVT, NG>(a, pv, ti, lane, qa, acc, m, l, ring[i]);
+        }
+    }
+
+    // sum the 16 keys of each row; lane c == 0 of row j then holds dims 32 h + 8 j .. +7
+    const bool single = t_begin == 0 && t_end == limit;
+#pragma unroll
+    for (int g = 0; g < GMAX; ++g) {
+        if (g >= static_cast<int>(G)) break;
+#pragma unroll
+        for (int h = 0; h < 2; ++h)
+#pragma unroll
+            for (int e = 0; e < kQE; ++e) acc[g][h][e] = group_sum<16>(acc[g][h][e]);
+        const size_t head = static_cast<size_t>(row) * a.num_heads + kvh * G + g;
+        if (single) {
+            const float inv = l[g] > 0.f ? 1.0f / l[g] : 0.f;
+            if (c == 0)
+#pragma unroll
+                for (int h = 0; h < 2; ++h) {
+                    float4* d4 = reinterpret_cast<float4*>(a.out + head * 64 + 32 * h + 8 * j);
+                    d4[0] = make_float4(acc[g][h][0] * inv, acc[g][h][1] * inv, acc[g][h][2] * inv, acc[g][h][3] * inv);
+                    d4[1] = make_float4(acc[g][h][4] * inv, acc[g][h][5] * inv, acc[g][h][6] * inv, acc[g][h][7] * inv);
+                }
+            continue;
+        }
+        const size_t slot = head * a.max_parts + part;
+        if (c == 0)
+#pragma unroll
+            for (int h = 0; h < 2; ++h) {
+                float4* d4 = reinterpret_cast<float4*>(a.part_out + slot * 64 + 32 * h + 8 * j);
+                d4[0] = make_float4(acc[g][h][0], acc[g][h][1], acc[g][h][2], acc[g][h][3]);
+                d4[1] = make_float4(acc[g][h][4], acc[g][h][5], acc[g][h][6], acc[g][h][7]);
+            }
+        if (lane == 0) a.part_stats[slot] = make_float2(m[g], l[g]);
+    }
+}
+
 // ---- chunk workgroup: 4 waves x 16 query rows share every K/V tile
 //
 // A 32-key tile is loaded once per workgroup with coalesced 16 B loads (each
@@ -1086,7 +1296,9 @@ __global__ __launch_bounds__(kThreads, 2) void attn_main(AttnArgs a) {
             }
         }
         const uint32_t row = static_cast<uint32_t>(st.cu[s] + i);
-        if constexpr (KVT != KANSO_KV_F32 && BUF && D >= kQE)
+        if constexpr (KVT == KANSO_KV_FP8 && BUF && D == 64 && GMAX <= 4)
+            decode_item_mq<GMAX, KVT, 2>(a, st, rs, row, local, a.part_size, s, kvh, lane);
+        else if constexpr (KVT != KANSO_KV_F32 && BUF && D >= kQE)
             decode_item_q<D, GMAX, KVT, (GMAX <= 4 ? 8 : 4), 2>(a, st, rs, row, local, a.part_size, s, kvh, lane);
         else
             decode_item<D, GMAX, KVT, NL, NB, BUF>(a, st, rs, row, local, a.part_size, s, kvh, lane);
