@@ -391,9 +391,10 @@ def profiled_traffic():
     return None
 
 
-def cpu_baseline(batch, seconds=12.0):
-    """Oracle (C++ restatement of the reference CPU path) on the headline batch,
-    single-threaded, over a pool compacted to exactly the blocks the batch reads."""
+def cpu_baseline(batch, seconds=12.0, nthreads=1):
+    """Oracle (C++ restatement of the reference CPU path) on the headline batch, on
+    `nthreads` host threads (OpenMP over (row, KV head)), over a pool compacted to
+    exactly the blocks the batch reads."""
     sys.path.insert(0, str(ROOT / "oracle"))
     import oracle as oracle_mod
     ids = np.unique(batch.block_tables)
@@ -411,16 +412,89 @@ def cpu_baseline(batch, seconds=12.0):
     calls, t0 = 0, time.perf_counter()
     while True:
         oracle_mod.ragged_attention(q, k, v, tables, batch.cu_seqlens, batch.context_lens,
-                                    nthreads=1, **kw)
+                                    nthreads=nthreads, **kw)
         calls += 1
         el = time.perf_counter() - t0
         if el >= seconds or calls >= 100:
             break
     per_call = el / calls
-    return dict(value=round(batch.total_q / per_call, 1), unit="tokens/s", cores=1, kind="port",
+    who = "single thread" if nthreads == 1 else f"{nthreads} threads"
+    return dict(value=round(batch.total_q / per_call, 1), unit="tokens/s", cores=nthreads, kind="port",
                 sample=f"{calls} oracle calls on the headline batch ({batch.total_q} query rows, "
-                       f"{batch.num_seqs} sequences), single thread, {el:.1f} s",
+                       f"{batch.num_seqs} sequences), {who}, {el:.1f} s",
                 ms_per_call=round(per_call * 1e3, 2))
+
+
+def reference_probes(ctx, torch, K, copy_gbps, copies=32, calls=200):
+    """The reference's own budget probes (src/bench/probes.rs), on this device.
+
+    paged_attn_ctx4096_b1: kanso_paged_attention_v2 at ctx 4096 / batch 1 with the
+    SmolLM2 geometry (heads = KV heads = 5, D = 64, probes.rs:112-139, q / K / V = 0.01),
+    time per call over the floor 2 * ctx * Hkv * D * 4 B / peak (the gate asks <= 2.0).
+    gemv_q8_0_1024: 1024 x 1024 Q8_0 GEMV of d = 0.01, qs = 1 blocks with x = 1
+    (probes.rs:59-87): weight bytes / time as a share of peak (the gate asks >= 60%).
+    Both rotate over distinct buffers (no Infinity Cache reuse) and divide by the
+    nominal 8 TB/s and by the copy bandwidth measured in this run."""
+    dev = torch.device("cuda:0")
+    ctx_len, hkv, d, bs = 4096, 5, 64, 16
+    blocks = ctx_len // bs
+    params = K.PagedAttentionParams(1, hkv, hkv, d, bs, blocks, 1.0 / np.sqrt(d))
+    per = blocks * bs * hkv * d
+    kp = torch.full((copies * per,), 0.01, device=dev)
+    vp = torch.full_like(kp, 0.01)
+    q = torch.full((hkv * d,), 0.01, device=dev)
+    out = torch.empty_like(q)
+    lens = torch.tensor([ctx_len], dtype=torch.int32, device=dev)
+    tabs = [torch.arange(i * blocks, (i + 1) * blocks, dtype=torch.int32, device=dev) for i in range(copies)]
+    for i in range(4):
+        K.paged_attention_v2(ctx, params, q, kp, vp, tabs[i], lens, out)
+    torch.cuda.synchronize()
+    s_ev, e_ev = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    s_ev.record()
+    for i in range(calls):
+        K.paged_attention_v2(ctx, params, q, kp, vp, tabs[i % copies], lens, out)
+    e_ev.record()
+    torch.cuda.synchronize()
+    attn_us = s_ev.elapsed_time(e_ev) / calls * 1e3
+    floor_bytes = 2 * ctx_len * hkv * d * 4
+    del kp, vp
+    # GEMV probe
+    blk = np.concatenate([np.array([0.01], np.float16).view(np.uint8), np.ones(32, np.uint8)])
+    wbytes = 1024 * 1024 // 32 * 34
+    ncopy = int(1.1e9 // wbytes) + 1
+    arena = torch.from_numpy(np.tile(blk, 1024 * 1024 // 32)).to(dev).repeat(ncopy)
+    x = torch.ones(1024, device=dev)
+    y = torch.empty(1024, device=dev)
+    for i in range(4):
+        K.gemv_q8_0(ctx, arena[i * wbytes:(i + 1) * wbytes], x, y, 1024, 1024)
+    torch.cuda.synchronize()
+    ctx.set_profiling(True)
+    for i in range(calls):
+        K.gemv_q8_0(ctx, arena[(i % ncopy) * wbytes:((i % ncopy) + 1) * wbytes], x, y, 1024, 1024)
+    g_ms, g_n = ctx.kernel_time("gemv")
+    ctx.set_profiling(False)
+    gemv_us = g_ms / max(g_n, 1) * 1e3
+    assert abs(float(y[0]) - float(np.float16(0.01)) * 1024) < 1e-2  # probes.rs closed form
+    del arena
+    torch.cuda.empty_cache()
+    return dict(
+        paged_attn_ctx4096_b1=dict(us_per_call=round(attn_us, 2),
+                                   over_floor_8tbs=round(attn_us * 1e-6 / (floor_bytes / HBM_PEAK), 2),
+                                   over_floor_measured=round(attn_us * 1e-6 / (floor_bytes / (copy_gbps * 1e9)), 2),
+                                   gate="<= 2.0", timing="back-to-back calls, one event pair"),
+        gemv_q8_0_1024=dict(us=round(gemv_us, 2),
+                            pct_of_8tbs=round(wbytes / (gemv_us * 1e-6) / HBM_PEAK * 100, 2),
+                            pct_of_measured=round(wbytes / (gemv_us * 1e-6) / (copy_gbps * 1e9) * 100, 2),
+                            gate=">= 60", timing="HIP events around each launch"))
+
+
+def host_bandwidth(threads):
+    """STREAM triad of the host (the oracle library, OpenMP), 1 thread and `threads`."""
+    sys.path.insert(0, str(ROOT / "oracle"))
+    import oracle as oracle_mod
+    return dict(stream_triad_gbps_1_thread=round(oracle_mod.stream_triad_gbps(1 << 26, 1), 1),
+                stream_triad_gbps=round(oracle_mod.stream_triad_gbps(1 << 26, threads), 1),
+                threads=threads, array_mib=512)
 
 
 def main():
@@ -565,6 +639,8 @@ def main():
         if not args.skip_gemv:
             extras["gemv"] = gemv_bench(ctx, torch, K, oracle_mod, quick=False)
         extras["copy_kernel_gbps"] = round(copy_bandwidth(torch), 1)
+        extras["reference_probes"] = reference_probes(ctx, torch, K, extras["copy_kernel_gbps"])
+        log(f"reference probes: {extras['reference_probes']}")
         torch.cuda.empty_cache()
     if not args.quick and not args.skip_config5:
         extras["config5_engine"] = engine_bench(ctx, K, torch)
@@ -578,6 +654,10 @@ def main():
     cpu = None if args.no_cpu else cpu_baseline(head[0])
     if cpu:
         log(f"cpu baseline: {cpu}")
+        threads = min(os.cpu_count() or 1, 16)  # the box's share of host cores
+        extras["cpu_baseline_all_threads"] = cpu_baseline(head[0], seconds=5.0, nthreads=threads)
+        extras["host_memory"] = host_bandwidth(threads)
+        log(f"cpu baseline mt: {extras['cpu_baseline_all_threads']} host {extras['host_memory']}")
 
     achieved = res["stage1_gbps"] * 1e9
     line = {

@@ -697,3 +697,35 @@ uint64_t oracle_fnv1a_64(const uint32_t* tokens, size_t n) {
 }
 
 }  // extern "C"
+
+// ---------------------------------------------------------------- host bandwidth
+
+double oracle_stream_triad(uint64_t n, int nthreads, int reps) {
+    std::vector<double> a(n), b(n), c(n);
+    const double s = 3.0;
+    const int64_t N = static_cast<int64_t>(n);
+#ifdef _OPENMP
+#pragma omp parallel for num_threads(nthreads) schedule(static)
+#endif
+    for (int64_t i = 0; i < N; ++i) {
+        a[i] = 0.0;
+        b[i] = 1.0;
+        c[i] = 2.0;
+    }
+    double best = 0.0;
+    for (int r = 0; r < reps; ++r) {
+#ifdef _OPENMP
+        const double t0 = omp_get_wtime();
+#pragma omp parallel for num_threads(nthreads) schedule(static)
+        for (int64_t i = 0; i < N; ++i) a[i] = b[i] + s * c[i];
+        const double t = omp_get_wtime() - t0;
+#else
+        (void)nthreads;
+        const double t = 1.0;
+#endif
+        best = std::max(best, 24.0 * static_cast<double>(n) / t / 1e9);
+    }
+    volatile double sink = a[n / 2];  // the stores stay observable
+    (void)sink;
+    return best;
+}

@@ -65,6 +65,10 @@ int oracle_pack_step(const kanso_seq_plan* plan, uint32_t num_seqs,
 
 /* quantize_head_slice, INT8 arm (src/kv_cache/quantized_storage.rs:452-469). */
 float oracle_quantize_head_int8(const float* x, uint32_t n, int8_t* q);
+/* Host memory bandwidth, STREAM triad a = b + s c over n doubles per array with
+ * nthreads OpenMP threads (first-touch initialisation by the same threads): best
+ * of `reps` in GB/s, counting 24 bytes per element (src/hardware.rs:436-459). */
+double oracle_stream_triad(uint64_t n, int nthreads, int reps);
 float oracle_quantize_head_fp8(const float* x, uint32_t n, uint8_t* q);
 uint8_t oracle_f32_to_e4m3(float x);
 float oracle_e4m3_to_f32(uint8_t b);

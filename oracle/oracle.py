@@ -46,6 +46,7 @@ def lib() -> C.CDLL:
             "oracle_pack_step": (I, [V, U, V, V, U, V, V, V, V, V, V, V, V]),
             "oracle_quantize_head_int8": (F, [V, U, V]),
             "oracle_quantize_head_fp8": (F, [V, U, V]),
+            "oracle_stream_triad": (C.c_double, [C.c_uint64, I, I]),
             "oracle_f32_to_e4m3": (C.c_uint8, [F]),
             "oracle_e4m3_to_f32": (F, [C.c_uint8]),
             "oracle_quantize_q8_0_block": (F, [V, V]),
@@ -375,3 +376,8 @@ def forward_batch(cfg: dict, weights: dict, k_pools, v_pools, num_blocks, block_
     if rc != 0:
         raise RuntimeError("oracle_forward_batch rejected the batch")
     return logits
+
+
+def stream_triad_gbps(n: int = 1 << 26, nthreads: int = 1, reps: int = 5) -> float:
+    """Host STREAM-triad bandwidth in GB/s (n doubles per array)."""
+    return float(lib().oracle_stream_triad(n, nthreads, reps))
