@@ -488,6 +488,26 @@ def reference_probes(ctx, torch, K, copy_gbps, copies=32, calls=200):
                             gate=">= 60", timing="HIP events around each launch"))
 
 
+def gemm_probe(ctx, torch, K, oracle_mod, launches=10):
+    """Launches only, for a rocprofv3 counter pass: the packed Q8_0 product at the
+    SmolLM2 shapes (q, gate+up, down) at 16, 32 and 512 tokens, and the GGUF-layout
+    GEMV at batch 32, `launches` times each."""
+    dev = torch.device("cuda:0")
+    for name, rows, cols in (("q", 960, 960), ("gate_up", 5120, 960), ("down", 960, 2560)):
+        rng = np.random.default_rng(rows)
+        w = oracle_mod.quantize_row_q8_0((rng.standard_normal((rows, cols)) * 0.02).astype(np.float32))
+        wd = torch.from_numpy(w).to(dev)
+        pk = K.pack_q8_0_matrix(ctx, wd, rows, cols)
+        for T in (16, 32, 512):
+            x, y = torch.randn(T * cols, device=dev), torch.empty(T * rows, device=dev)
+            for _ in range(launches):
+                K.gemm_q8_0(ctx, pk, x, y, rows, cols)
+        x, y = torch.randn(32 * cols, device=dev), torch.empty(32 * rows, device=dev)
+        for _ in range(launches):
+            K.gemv_q8_0(ctx, wd, x, y, rows, cols)
+        torch.cuda.synchronize()
+
+
 def host_bandwidth(threads):
     """STREAM triad of the host (the oracle library, OpenMP), 1 thread and `threads`."""
     sys.path.insert(0, str(ROOT / "oracle"))
@@ -513,6 +533,8 @@ def main():
                     help="row order inside a KV block for the attention benchmarks")
     ap.add_argument("--config5-only", action="store_true",
                     help="run only the config-5 engine benchmark and print its JSON")
+    ap.add_argument("--gemm-probe", action="store_true",
+                    help="launches of the Q8_0 products only (for a rocprofv3 counter pass)")
     ap.add_argument("--decode-only", action="store_true",
                     help="also time the headline batches' decode rows alone")
     args = ap.parse_args()
@@ -528,6 +550,12 @@ def main():
     from kanso_infer_amd import workloads
 
     ctx = K.Context(0)
+    if args.gemm_probe:
+        sys.path.insert(0, str(ROOT / "oracle"))
+        import oracle as oracle_mod
+        gemm_probe(ctx, torch, K, oracle_mod)
+        ctx.close()
+        return
     if args.config5_only:
         r5 = engine_bench(ctx, K, torch)
         r5["checksum_parity"] = config5_checksum_parity(ctx, K, torch)

@@ -74,11 +74,12 @@ def test_gemv_gguf_any_batch(ctx, T):
 
 
 @pytest.mark.parametrize("cols", [960, 2560])
-def test_batch_invariance(ctx, cols):
+@pytest.mark.parametrize("rows", [960, 5120])
+def test_batch_invariance(ctx, rows, cols):
     """A token's output does not depend on the rest of the batch: every batch size
-    assigns k-blocks to the same waves and sums them in the same order."""
-    sizes = (1, 7, 16, 17, 32, 33, 40, 64, 200, 512)
-    rows = 960
+    (16- and 64-token tiles alike) assigns k-blocks to the same waves and sums them
+    in the same order."""
+    sizes = (1, 7, 16, 17, 32, 33, 40, 64, 200, 256, 257, 300, 512, 700)
     w = q8_weights(rows, cols, 9)
     packed = K.pack_q8_0_matrix(ctx, dev(w), rows, cols)
     x = np.random.default_rng(1).standard_normal((max(sizes), cols)).astype(np.float32)
@@ -87,12 +88,13 @@ def test_batch_invariance(ctx, cols):
         y = torch.empty(T * rows, dtype=torch.float32, device="cuda:0")
         K.gemm_q8_0(ctx, packed, dev(x[:T]), y, rows, cols)
         outs.append(host(y).reshape(T, rows)[0])
-    for o in outs[1:]:
-        assert np.array_equal(o, outs[0])
+    for T, o in zip(sizes[1:], outs[1:]):
+        assert np.array_equal(o, outs[0]), T
 
 
-def test_gemm_residual(ctx):
-    rows, cols, T = 960, 2560, 37
+@pytest.mark.parametrize("T", [37, 300])
+def test_gemm_residual(ctx, T):
+    rows, cols = 960, 2560
     w = q8_weights(rows, cols, 11)
     packed = K.pack_q8_0_matrix(ctx, dev(w), rows, cols)
     rng = np.random.default_rng(2)
@@ -142,7 +144,7 @@ def _qkv_case(T, H=15, HKV=5, hidden=960, seed=0, num_blocks=64, bs=16):
                 positions=positions, slots=slots, num_blocks=num_blocks, bs=bs)
 
 
-@pytest.mark.parametrize("T", [1, 20, 70])
+@pytest.mark.parametrize("T", [1, 20, 70, 300])
 def test_qkv_rope_append(ctx, T):
     c = _qkv_case(T, seed=T)
     H, HKV, hidden, D = c["H"], c["HKV"], c["hidden"], 64
@@ -177,7 +179,7 @@ def test_qkv_rope_append(ctx, T):
     assert not kpool[untouched].any() and not vpool[untouched].any()
 
 
-@pytest.mark.parametrize("T", [1, 33, 130])
+@pytest.mark.parametrize("T", [1, 33, 130, 300])
 def test_gate_up_swiglu(ctx, T):
     hidden, inter = 960, 2560
     wg = q8_weights(inter, hidden, 21)

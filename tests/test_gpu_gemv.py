@@ -44,7 +44,7 @@ def test_q8_0(ctx, name, rows, cols, batch):
     assert_close(got, want, what=f"q8_0 {name} b{batch}")
 
 
-@pytest.mark.parametrize("batch", BATCHES + [64, 100])
+@pytest.mark.parametrize("batch", BATCHES + [64, 100, 300])
 @pytest.mark.parametrize("name,rows,cols", [("down", 960, 2560), ("q_padded", 960, 1024),
                                             ("kv_padded", 320, 1024),
                                             ("gate_up_padded", 2560, 1024)])
