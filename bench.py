@@ -37,6 +37,7 @@ HBM_PEAK = 8.0e12
 PMC_COPY_BYTES = 512 << 20
 METRIC = "ragged paged-attn tokens/s + % HBM peak; batched decode tok/s at 1 MI355X"
 POOL_LAYOUT = 0  # KANSO_POOL_TOKEN_MAJOR unless --pool-layout head
+PARTITION = 0  # 0: kanso_ragged_partition_size per batch; -1: the library's choice; > 0: fixed
 
 
 def log(msg: str) -> None:
@@ -92,20 +93,43 @@ class AttnBench:
                 lens=torch.from_numpy(b.context_lens.astype(np.int32)).to(dev)))
         torch.cuda.synchronize()
 
+    def partition(self, b):
+        """The split-K partition the caller passes: PARTITION if set (-1 = the library's
+        own choice), else kanso_ragged_partition_size from the batch's host-side
+        lengths, as the engine computes it from its plan."""
+        if PARTITION:
+            return max(PARTITION, 0)
+        return self.K.ragged_partition_size(
+            self.ctx, q_lens=b.q_lens, context_lens=b.context_lens, num_heads=b.num_heads,
+            num_kv_heads=b.num_kv_heads, head_dim=b.head_dim, block_size=b.block_size,
+            max_blocks=b.max_blocks, kv_dtype=self.kv_dtype, num_blocks=self.num_blocks)
+
     def call(self, i):
         b, d = self.batches[i % len(self.batches)], self.dev_batches[i % len(self.batches)]
+        if "P" not in d:
+            d["P"] = self.partition(b)
         self.K.ragged_paged_attention(
             self.ctx, q=d["q"], k_pool=self.k, v_pool=self.v, k_scales=self.ks, v_scales=self.vs,
             block_tables=d["tables"], cu_seqlens=d["cu"], context_lens=d["lens"], out=d["out"],
             num_heads=b.num_heads, num_kv_heads=b.num_kv_heads, head_dim=b.head_dim,
             block_size=b.block_size, scale=b.scale, kv_dtype=self.kv_dtype,
             num_blocks=self.num_blocks, max_q_len=int(b.q_lens.max()),
-            pool_layout=POOL_LAYOUT)
+            pool_layout=POOL_LAYOUT, partition_size=d["P"])
 
     def run(self, steps, warmup):
         torch = self.torch
         for i in range(warmup):
             self.call(i)
+        # then at least ~0.3 s of the same work untimed, so clocks and caches are in
+        # their steady state whatever the order of the measurements
+        torch.cuda.synchronize()
+        t_end = time.perf_counter() + 0.3
+        i = warmup
+        while time.perf_counter() < t_end:
+            for _ in range(20):
+                self.call(i)
+                i += 1
+            torch.cuda.synchronize()
         self.ctx.check_device_status()
         torch.cuda.synchronize()
         # throughput: the calls alone, no per-kernel events in the timed region
@@ -533,13 +557,17 @@ def main():
                     help="row order inside a KV block for the attention benchmarks")
     ap.add_argument("--config5-only", action="store_true",
                     help="run only the config-5 engine benchmark and print its JSON")
+    ap.add_argument("--partition", type=int, default=0,
+                    help="split-K partition of the attention benchmarks: 0 = from the batch's "
+                         "lengths (kanso_ragged_partition_size), -1 = the library's own choice")
     ap.add_argument("--gemm-probe", action="store_true",
                     help="launches of the Q8_0 products only (for a rocprofv3 counter pass)")
     ap.add_argument("--decode-only", action="store_true",
                     help="also time the headline batches' decode rows alone")
     args = ap.parse_args()
-    global POOL_LAYOUT
+    global POOL_LAYOUT, PARTITION
     POOL_LAYOUT = 1 if args.pool_layout == "head" else 0
+    PARTITION = args.partition
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print("bench.py measures one GPU: this path has no multi-GPU component in this build "
               "(see DESIGN.md for how it would shard); run with --gpus 1", file=sys.stderr)
@@ -586,6 +614,20 @@ def main():
     log(f"config2: {res}")
 
     extras = {}
+    extras["partitions"] = [d["P"] for d in hb.dev_batches]
+    if not args.quick and PARTITION == 0:
+        # the same batches with the library's own partition (no host lengths)
+        PARTITION = -1
+        lib = AttnBench.__new__(AttnBench)
+        lib.__dict__.update(hb.__dict__)
+        lib.dev_batches = [{k: v for k, v in d.items() if k != "P"} for d in hb.dev_batches]
+        rl = lib.run(args.steps, args.warmup)
+        PARTITION = 0
+        extras["headline_library_partition"] = dict(
+            tokens_per_s=round(rl["tokens_per_s"], 1), ms_per_step=round(rl["ms_per_step"], 5),
+            stage1_gbps=round(rl["stage1_gbps"], 1),
+            partitions=[d["P"] for d in lib.dev_batches])
+        log(f"config2, library partition: {extras['headline_library_partition']}")
     if args.decode_only:
         dec = [workloads.config2_mixed(num_chunks=0, num_blocks=nb, seed_offset=i) for i in range(8)]
         hd = AttnBench.__new__(AttnBench)
@@ -708,6 +750,8 @@ def main():
             "query_rows": int(np.mean([b.total_q for b in head])),
             "sequences": int(np.mean([b.num_seqs for b in head])),
             "rotation": "8 batches",
+            "partition": "per batch from its host-side lengths (kanso_ragged_partition_size), "
+                         "as the engine passes it from its plan",
         },
         "roofline": {
             "bound": "hbm",

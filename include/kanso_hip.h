@@ -117,7 +117,9 @@ typedef struct {
     uint32_t max_q_len;  /* upper bound of any sequence's query rows (0 = total_q)  */
     uint32_t pool_layout; /* KANSO_POOL_*                                           */
     uint32_t partition_size; /* split-K partition of decode rows in tokens: 0 = chosen
-                                from the shape; else a power of two in [32, 512]   */
+                                from the shape; else a multiple of 32 in
+                                [32, min(992, 62 * block_size)]
+                                (kanso_ragged_partition_size picks one)           */
 } kanso_ragged_attention_params;
 
 /* One planned sequence of a step, as Engine::step plans it (src/engine.rs:221-226). */
@@ -174,6 +176,17 @@ int kanso_paged_attention_v2(kanso_ctx* ctx, const kanso_paged_attention_params*
  * mask of src/model.rs:1510-1527; a decode row attends its whole context).
  * q and out are [total_q][num_heads][head_dim] f32. k_scales/v_scales are unused
  * for KANSO_KV_F32. Query head h reads KV head h / (num_heads/num_kv_heads). */
+/* The split-K partition for kanso_ragged_paged_attention's partition_size, from the
+ * step's host-side query and context lengths (num_seqs entries each), which the
+ * caller that planned the step holds (Engine::step's query_lens / context_lens,
+ * src/engine.rs:376-402): the smallest multiple of 32 (<= 512) for which every
+ * decode item (row x KV head x partition) gets a resident wave in one pass, with
+ * chunk items on their own partition of at least 512 keys. No counterpart in the
+ * reference (its Metal kernel uses a fixed PARTITION_SIZE of 256). Returns 0 (=
+ * let the library choose) for unusable arguments. Host-only; launches nothing. */
+uint32_t kanso_ragged_partition_size(const kanso_ctx* ctx, const kanso_ragged_attention_params* p,
+                                     const uint32_t* q_lens, const uint32_t* context_lens);
+
 int kanso_ragged_paged_attention(kanso_ctx* ctx, const kanso_ragged_attention_params* p,
                                  const float* q, const void* k_pool, const void* v_pool,
                                  const void* k_scales, const void* v_scales,

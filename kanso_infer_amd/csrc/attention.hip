@@ -1438,6 +1438,36 @@ uint32_t choose_partition(const kanso_ctx* ctx, uint32_t seqs, uint32_t kv_heads
     return P;
 }
 
+// Launch geometry shared by run_ragged and the host partition helper.
+bool pool_fits_rsrc(const kanso_ragged_attention_params* p) {
+    const uint64_t elem = p->kv_dtype == KANSO_KV_F32 ? 4 : 1;
+    const uint64_t rows = static_cast<uint64_t>(p->num_blocks) * p->block_size * p->num_kv_heads;
+    return p->num_blocks != 0 && rows * p->head_dim * elem < (1ull << 32);
+}
+
+// Chunk items are 64 rows wide: their partition stays long (at least 512 keys, within
+// 62 table entries), so small decode partitions do not multiply them.
+uint32_t chunk_partition(uint32_t P, uint32_t block_size) {
+    return std::max(P, std::min(512u, 62u * block_size / 32u * 32u));
+}
+
+// One persistent launch: two workgroups (eight waves) per CU, plus half a CU's worth
+// for batches with chunk items (chunk workgroups hold their slots only briefly; the
+// extra decode workgroups are dispatched into the slots they free).
+uint32_t main_grid(const kanso_ctx* ctx, uint64_t T, uint32_t max_parts, uint32_t HKV, bool mfma) {
+    const uint64_t max_waves = (T * max_parts * HKV + kWaves - 1) / kWaves;
+    uint32_t grid = static_cast<uint32_t>(std::max<uint64_t>(
+        1, std::min<uint64_t>(std::max<uint64_t>(max_waves, mfma ? ctx->num_cus : 1),
+                              static_cast<uint64_t>(ctx->num_cus) * 2)));
+    if (mfma) grid += ctx->num_cus / 2;
+    return grid;
+}
+
+uint32_t host_row_limit(uint32_t ctx_len, uint32_t q_len, uint32_t i, uint32_t cap) {
+    const int64_t lim = static_cast<int64_t>(ctx_len) - q_len + i + 1;
+    return static_cast<uint32_t>(std::min<int64_t>(std::max<int64_t>(lim, 0), cap));
+}
+
 int run_ragged(kanso_ctx* ctx, const kanso_ragged_attention_params* p, const float* q,
                const void* kp, const void* vp, const void* ks, const void* vs,
                const uint32_t* tables, const int32_t* cu, const uint32_t* ctx_lens, float* out,
@@ -1492,11 +1522,11 @@ int run_ragged(kanso_ctx* ctx, const kanso_ragged_attention_params* p, const flo
     }
     const uint32_t capacity = static_cast<uint32_t>(cap64);
     const uint32_t T = p->total_q;
-    if (p->partition_size && (p->partition_size < 32 || p->partition_size > 512 ||
-                              (p->partition_size & (p->partition_size - 1)) != 0 ||
+    if (p->partition_size && (p->partition_size < 32 || p->partition_size > 992 ||
+                              p->partition_size % 32 != 0 ||
                               p->partition_size > 62u * p->block_size)) {
-        set_error("%s: partition_size %u must be 0 or a power of two in [32, min(512, 62 * block_size)]", who,
-                  p->partition_size);
+        set_error("%s: partition_size %u must be 0 or a multiple of 32 in [32, min(992, 62 * block_size)]",
+                  who, p->partition_size);
         return KANSO_E_INVALID_SHAPE;
     }
     const uint32_t P = p->partition_size ? p->partition_size
@@ -1542,7 +1572,7 @@ int run_ragged(kanso_ctx* ctx, const kanso_ragged_attention_params* p, const flo
     a.max_blocks = p->max_num_blocks_per_seq;
     a.num_blocks = p->num_blocks ? p->num_blocks : 0xffffffffu;
     a.part_size = P;
-    a.chunk_part = P;  // chunk items are 64 rows wide: the longest partition
+    a.chunk_part = chunk_partition(P, p->block_size);
     a.max_parts = max_parts;
     a.total_q = T;
     a.capacity = capacity;
@@ -1554,7 +1584,7 @@ int run_ragged(kanso_ctx* ctx, const kanso_ragged_attention_params* p, const flo
     const uint64_t pool_bytes = rows * D * elem;
     const uint64_t scale_bytes = p->kv_dtype == KANSO_KV_INT8 || p->kv_dtype == KANSO_KV_FP8 ? rows * 4
                                  : p->kv_dtype == KANSO_KV_Q8_0 ? rows * (D / 32) * 2 : 0;
-    const bool buf = p->num_blocks != 0 && pool_bytes < (1ull << 32);
+    const bool buf = pool_fits_rsrc(p);
     a.pool_bytes = buf ? static_cast<uint32_t>(pool_bytes) : 0u;
     a.scale_bytes = buf ? static_cast<uint32_t>(scale_bytes) : 0u;
     // MFMA chunk items exist only when some sequence has more than one query row; the
@@ -1570,16 +1600,9 @@ int run_ragged(kanso_ctx* ctx, const kanso_ragged_attention_params* p, const flo
         return KANSO_E_INVALID_SHAPE;
     }
 
-    // One persistent launch: two workgroups (eight waves) per CU; nothing in the grid
-    // depends on device data.
+    // nothing in the grid depends on device data
     hipEvent_t ev;
-    const uint64_t max_waves = (static_cast<uint64_t>(T) * max_parts * HKV + kWaves - 1) / kWaves;
-    uint32_t grid = static_cast<uint32_t>(
-        std::max<uint64_t>(1, std::min<uint64_t>(std::max<uint64_t>(max_waves, a.use_mfma ? ctx->num_cus : 1),
-                                                 static_cast<uint64_t>(ctx->num_cus) * 2)));
-    // Chunk workgroups hold their slots only briefly; extra decode workgroups are
-    // dispatched into the slots they free, keeping bytes in flight.
-    if (a.use_mfma) grid += ctx->num_cus / 2;
+    const uint32_t grid = main_grid(ctx, T, max_parts, HKV, a.use_mfma != 0);
     if ((rc = prof_begin(ctx, "attention", stream, &ev))) return rc;
     hipLaunchKernelGGL(main_fn, dim3(grid), dim3(kThreads), 0, stream, a);
     KANSO_LAUNCH_CHECK();
@@ -1605,6 +1628,55 @@ uint32_t kanso_paged_attention_num_partitions(const kanso_paged_attention_params
     const uint64_t capacity = static_cast<uint64_t>(p->max_num_blocks_per_seq) * p->block_size;
     const uint64_t parts = (std::min<uint64_t>(capacity, 0xffffffffu) + kRefPartition - 1) / kRefPartition;
     return static_cast<uint32_t>(std::max<uint64_t>(parts, 1));
+}
+
+uint32_t kanso_ragged_partition_size(const kanso_ctx* ctx, const kanso_ragged_attention_params* p,
+                                     const uint32_t* q_lens, const uint32_t* context_lens) {
+    // The smallest partition (a multiple of 32) whose decode items (row x KV head x
+    // partition) all get a resident wave of their own in one pass: shorter items
+    // finish sooner, while items beyond the resident waves would run in a second
+    // round. Chunk items (64 rows, their own partition of at least 512) hold one
+    // resident workgroup each; a partition that gives them every one is not taken.
+    // Measured on the BASELINE batches: the optimum of a sweep over multiples of 32
+    // is where the decode items just fit (config 2: 448; 48 decodes alone: 320;
+    // config 1: 32; config 3: 160-192).
+    if (!ctx || !p || !q_lens || !context_lens || p->num_seqs == 0 || p->num_kv_heads == 0 ||
+        p->num_heads % p->num_kv_heads != 0 || p->block_size == 0)
+        return 0;
+    const uint32_t S = p->num_seqs, HKV = p->num_kv_heads, G = p->num_heads / HKV;
+    const uint64_t cap64 = static_cast<uint64_t>(p->max_num_blocks_per_seq) * p->block_size;
+    const uint32_t cap = static_cast<uint32_t>(std::min<uint64_t>(cap64, 1u << 30));
+    uint64_t T = 0;
+    uint32_t max_q = 0;
+    for (uint32_t s = 0; s < S; ++s) {
+        T += q_lens[s];
+        max_q = std::max(max_q, q_lens[s]);
+    }
+    if (T == 0 || cap == 0) return 0;
+    const bool mfma = p->head_dim == 64 && G <= 4 && max_q > 1 && pool_fits_rsrc(p);
+    const uint32_t p_max = std::max(32u, std::min(512u, 62u * p->block_size / 32u * 32u));
+    uint32_t best = p_max;
+    for (uint32_t P = p_max; P >= 32; P -= 32) {
+        const uint32_t cp = chunk_partition(P, p->block_size);
+        uint64_t n_chunk = 0, items = 0;
+        for (uint32_t s = 0; s < S; ++s) {
+            const uint32_t ql = q_lens[s], c = context_lens[s];
+            if (mfma && ql > 1) {
+                for (uint32_t i0 = 0; i0 < ql; i0 += 64)
+                    n_chunk += (host_row_limit(c, ql, std::min(i0 + 64, ql) - 1, cap) + cp - 1) / cp * HKV;
+            } else {
+                for (uint32_t i = 0; i < ql; ++i) items += (host_row_limit(c, ql, i, cap) + P - 1) / P * HKV;
+            }
+        }
+        // resident: two workgroups per CU (the kernel's register budget); chunk
+        // workgroups hold some of them, the extra workgroups of the grid wait
+        const uint64_t resident = std::min<uint64_t>(main_grid(ctx, T, (cap + P - 1) / P, HKV, mfma),
+                                                     2ull * ctx->num_cus);
+        if (n_chunk >= resident) break;
+        if (items > (resident - n_chunk) * kWaves) break;
+        best = P;
+    }
+    return best;
 }
 
 int kanso_validate_paged_attention_params(const kanso_paged_attention_params* p) {

@@ -318,21 +318,16 @@ int model_forward(kanso_model* m, const HostStep& step, float* logits, uint32_t*
     ap.kv_dtype = KANSO_KV_F32;
     ap.num_blocks = m->num_blocks;
     ap.max_q_len = max_q;
-    if (max_q == 1) {
-        // Decode step: the partition from the exact contexts, which the host planned
-        // (the attention library alone only knows the table capacity): the largest
-        // power of two whose items (sequence x KV head x partition) still give every
-        // resident wave (two 4-wave workgroups per CU) one item. Measured on config 5:
-        // 10.96 k tok/s with the capacity-based choice, 11.16-11.23 k with targets of
-        // 4, 8 or 16 items per CU, 7.7 k with 512 always.
-        const uint64_t target = static_cast<uint64_t>(m->ctx->num_cus) * 8;
-        uint32_t P = 512;
-        for (; P > 32; P /= 2) {
-            uint64_t items = 0;
-            for (const auto& p : step.plan) items += (p.start_pos + p.q_len + P - 1) / P;
-            if (items * c.num_kv_heads >= target) break;
+    {
+        // The split-K partition from the step's planned lengths (the attention library
+        // alone only sees the table capacity). Measured on config 5: 10.96 k tok/s with
+        // the capacity-based choice, 11.2 k with the planned lengths.
+        std::vector<uint32_t> ql(S), cl(S);
+        for (uint32_t i = 0; i < S; ++i) {
+            ql[i] = step.plan[i].q_len;
+            cl[i] = step.plan[i].start_pos + step.plan[i].q_len;
         }
-        ap.partition_size = std::min(P, 62u * m->block_size);
+        ap.partition_size = kanso_ragged_partition_size(m->ctx, &ap, ql.data(), cl.data());
     }
     const uint32_t qd = c.num_heads * 64;
     for (uint32_t l = 0; l < c.num_layers; ++l) {

@@ -127,7 +127,7 @@ def test_rejects_bad_partition_size(ctx):
     b = workloads.small_mixed(12)
     kp, vp, ks, vs = fill_pool(b, oracle.KV_F32, 12)
     q = np.zeros(b.total_q * b.num_heads * b.head_dim, np.float32)
-    for bad in (48, 16, 1024):
+    for bad in (48, 16, 1024, 100):
         with pytest.raises(K.EngineError):
             run_ragged_gpu(ctx, b, q, kp, vp, partition_size=bad)
 
@@ -188,3 +188,28 @@ def test_fp8_pool_decodes_every_finite_code(ctx):
     got = run_ragged_gpu(ctx, b, q, kp, vp, ks, vs, oracle.KV_FP8).reshape(S, d)
     dec = np.array([oracle.e4m3_to_f32(c) for c in range(256)], np.float32)
     np.testing.assert_array_equal(got, dec[vrows] * np.float32(0.5))
+
+
+@pytest.mark.parametrize("variant", ["small_mixed", "config1", "config3_q8_0"])
+def test_partition_from_host_lengths(ctx, variant):
+    """kanso_ragged_partition_size: a multiple of 32 in [32, 512] from the batch's
+    host-side lengths, and the call with it gives the oracle's result."""
+    if variant == "small_mixed":
+        b, kv = workloads.small_mixed(13), oracle.KV_F32
+    elif variant == "config1":
+        b, kv = workloads.config1_decode(), oracle.KV_F32
+    else:
+        b, kv = workloads.config3_quant_decode(), oracle.KV_Q8_0
+    P = K.ragged_partition_size(ctx, q_lens=b.q_lens, context_lens=b.context_lens,
+                                num_heads=b.num_heads, num_kv_heads=b.num_kv_heads,
+                                head_dim=b.head_dim, block_size=b.block_size,
+                                max_blocks=b.max_blocks, kv_dtype=kv, num_blocks=b.num_blocks)
+    assert 32 <= P <= 512 and P % 32 == 0
+    kp, vp, ks, vs = fill_pool(b, kv, 14)
+    q = np.random.default_rng(15).standard_normal(
+        b.total_q * b.num_heads * b.head_dim).astype(np.float32)
+    got = run_ragged_gpu(ctx, b, q, kp, vp, ks, vs, kv, partition_size=P)
+    want = run_ragged_oracle(b, q, kp, vp, ks, vs, kv)
+    assert_close(got, want, what=f"{variant} P {P}")
+    assert K.ragged_partition_size(ctx, q_lens=[], context_lens=[], num_heads=15, num_kv_heads=5,
+                                   head_dim=64, block_size=16, max_blocks=4) == 0
