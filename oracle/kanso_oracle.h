@@ -11,9 +11,11 @@
  * library is compiled with -ffp-contract=off, as Rust never contracts).
  *
  * Pinning (what checks each function besides the HIP comparison) is recorded in
- * the tests under tests/test_oracle_*.py; the one unpinned item is the Q4_K
- * quantizer's byte choice (candle's QTensor::quantize is not available), see
- * oracle_quantize_row_q4_k.
+ * the tests under tests/test_oracle_*.py. Unpinned: the Q4_K quantizer's byte
+ * choice (candle's QTensor::quantize is not available, see
+ * oracle_quantize_row_q4_k), and byte parity of the FP8 encoder with the float8
+ * 0.7.0 crate (not vendored; the encoder here is pinned to round-to-nearest-even
+ * by brute force, see oracle_f32_to_e4m3).
  */
 #ifndef KANSO_ORACLE_H
 #define KANSO_ORACLE_H
