@@ -102,12 +102,11 @@ struct WGguf {
             d = 0.f;
             return;
         }
-        // Blocks are 34 B, so qs is only 2-byte aligned: four u16 loads.
-        const uint16_t* p = reinterpret_cast<const uint16_t*>(w + (static_cast<size_t>(row) * nb + b) * 34);
-        d = f16_bits_to_f32(p[0]);
-        const uint16_t* qp = p + 1 + 4 * (lane >> 4);
-        q = static_cast<uint64_t>(qp[0]) | (static_cast<uint64_t>(qp[1]) << 16) |
-            (static_cast<uint64_t>(qp[2]) << 32) | (static_cast<uint64_t>(qp[3]) << 48);
+        // Blocks are 34 B, so qs is only 2-byte aligned; gfx950 serves an unaligned
+        // 8-byte global load as one instruction (global_load_dwordx2).
+        const uint8_t* p = w + (static_cast<size_t>(row) * nb + b) * 34;
+        d = f16_bits_to_f32(*reinterpret_cast<const uint16_t*>(p));
+        __builtin_memcpy(&q, __builtin_assume_aligned(p + 2 + 8 * (lane >> 4), 2), 8);
     }
 };
 
@@ -175,16 +174,22 @@ struct XIn {
 // ---------------------------------------------------------------- the kernel
 
 // Every epilogue provides
-//   groups(p, g0, g1): the two 16-row weight groups of pair p;
-//   apply(p, lane, m0, T, v0, v1): outputs of rows g0*16 + lane%16 (v0) and
-//     g1*16 + lane%16 (v1) for tokens m0 .. m0+3 (skip m >= T).
+//   kGroups: 16-row weight groups per epilogue unit, 2 (a pair) or 1;
+//   groups(p, g0, g1): the weight groups of unit p (kGroups = 1: g0 = p);
+//   pre(p, lane, m0, T): its own operands for outputs of unit p, tokens m0 .. m0+3,
+//     requested before the main loop;
+//   apply(p, lane, m0, T, v0, v1, pre): outputs of rows g0*16 + lane%16 (v0) and
+//     g1*16 + lane%16 (v1, unused when kGroups = 1) for tokens m0 .. m0+3 (skip
+//     m >= T).
 //
-// A workgroup of KS waves owns one pair of weight groups and 16*MT tokens; wave w
-// takes k-blocks w, w + KS, ... and issues the loads of U such blocks (weights,
-// x, norm weights) before any arithmetic, so a matrix is requested in one or a few
-// rounds: at decode sizes the time is load latency, not bandwidth. The KS partial
-// sums meet in LDS in a fixed order (results do not depend on T beyond the choice
-// of MT).
+// A workgroup of KS waves owns NU epilogue units (NG = NU * kGroups weight groups)
+// and 16*MT tokens; wave w takes k-blocks w, w + KS, ... and issues the loads of U
+// such blocks (weights of every group, x, norm weights) before any arithmetic, so
+// a matrix is requested in one or a few rounds: at decode sizes the time is load
+// latency, not bandwidth. Each x load feeds the products of all NG groups, so
+// wider workgroups (NU > 1) re-read x from L2 less often, at the cost of fewer
+// workgroups. The KS partial sums meet in LDS in a fixed order: a token's result
+// does not depend on T, MT or NU.
 //
 // RMSNorm prologue folded into the product: RMSNorm(x) W = (1 / rms) ((x * w) W),
 // and the sum of squares of each token row is accumulated from the very x values
@@ -192,20 +197,31 @@ struct XIn {
 // happens on the reduced outputs.
 //
 // The loads of a round are branch-free (a block past the row is replaced by the
-// last block, its scale forced to 0): a branch around them would make the
-// compiler wait for each block's loads at the join, serialising the round.
-template <int KS, int U, int MT, bool NORM, class WL, class Epi>
-__global__ __launch_bounds__(KS * kWave) void q8_gemm_kernel(WL wl, XIn xa, Epi epi) {
-    __shared__ floatx4 s_part[KS][2][MT][kWave];
+// last block, its scale forced to 0; a unit past `units` by the workgroup's first
+// unit, never stored): a branch around them would make the compiler wait for each
+// block's loads at the join, serialising the round.
+template <int KS, int U, int MT, int NU, bool NORM, class WL, class Epi>
+__global__ __launch_bounds__(KS * kWave) void q8_gemm_kernel(WL wl, XIn xa, Epi epi, uint32_t units) {
+    constexpr int EG = Epi::kGroups;
+    constexpr int NG = NU * EG;
+    constexpr int NC = MT * NU;  // (token tile, unit) combinations of the epilogue
+    static_assert(NG * MT <= 8 && NC <= KS, "partial sums must fit 64 KB of LDS");
+    __shared__ floatx4 s_part[KS][NG][MT][kWave];
     __shared__ float s_ss[KS][MT][16];
     const int lane = threadIdx.x & (kWave - 1), wv = threadIdx.x / kWave;
     const int kq = lane >> 4, mm = lane & 15;
-    const uint32_t p = blockIdx.x;
+    const uint32_t u0 = blockIdx.x * NU;
     const uint32_t t0 = blockIdx.y * 16 * MT;
     const uint32_t nb = xa.in / 32;
     constexpr bool norm = NORM;
-    uint32_t g0, g1;
-    epi.groups(p, g0, g1);
+    uint32_t g[NG];
+#pragma unroll
+    for (int j = 0; j < NU; ++j) {
+        uint32_t ga, gb;
+        epi.groups(u0 + j < units ? u0 + j : u0, ga, gb);
+        g[EG * j] = ga;
+        if constexpr (EG == 2) g[EG * j + 1] = gb;
+    }
     const float* xr[MT];
     bool mok[MT];
 #pragma unroll
@@ -214,29 +230,33 @@ __global__ __launch_bounds__(KS * kWave) void q8_gemm_kernel(WL wl, XIn xa, Epi 
         mok[i] = m < xa.T;
         xr[i] = xa.row(mok[i] ? m : t0);
     }
-    // the epilogue's own operands (residual rows, RoPE tables, slots) are requested
-    // now, so their latency hides under the main loop
+    // wave c < NC stores combination c = (tile c % MT, unit c / MT); the epilogue's
+    // own operands (residual rows, RoPE tables, slots) are requested now, so their
+    // latency hides under the main loop
+    const int ci = wv % MT, cj = wv / MT;
+    const uint32_t cunit = u0 + cj;
+    const bool cstore = wv < NC && cunit < units;
     typename Epi::Pre pre{};
-    if (wv < MT) pre = epi.pre(p, lane, t0 + 16 * wv + 4 * kq, xa.T);
-    floatx4 acc[2][MT];
+    if (cstore) pre = epi.pre(cunit, lane, t0 + 16 * ci + 4 * kq, xa.T);
+    floatx4 acc[NG][MT];
     float ss[MT];
 #pragma unroll
     for (int i = 0; i < MT; ++i) {
-        acc[0][i] = floatx4{0.f, 0.f, 0.f, 0.f};
-        acc[1][i] = floatx4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int n = 0; n < NG; ++n) acc[n][i] = floatx4{0.f, 0.f, 0.f, 0.f};
         ss[i] = 0.f;
     }
     for (uint32_t b0 = wv; b0 < nb; b0 += KS * U) {
-        uint64_t q0[U], q1[U];
-        float d0[U], d1[U], m0[U], m1[U];
+        uint64_t q[NG][U];
+        float d[NG][U], mn[NG][U];
         float4 xv[U][MT][2], nv[U][2];
         bool live[U];
 #pragma unroll
         for (int u = 0; u < U; ++u) {
             live[u] = b0 + u * KS < nb;
             const uint32_t b = live[u] ? b0 + u * KS : nb - 1;
-            wl.load(g0, b, lane, q0[u], d0[u], m0[u]);
-            wl.load(g1, b, lane, q1[u], d1[u], m1[u]);
+#pragma unroll
+            for (int n = 0; n < NG; ++n) wl.load(g[n], b, lane, q[n][u], d[n][u], mn[n][u]);
             const uint32_t k = 32 * b + 8 * kq;
 #pragma unroll
             for (int i = 0; i < MT; ++i) {
@@ -256,12 +276,14 @@ __global__ __launch_bounds__(KS * kWave) void q8_gemm_kernel(WL wl, XIn xa, Epi 
 #pragma unroll
         for (int u = 0; u < U; ++u) {
             // a repeated block contributes nothing: zero scale and min, no squares
-            d0[u] = live[u] ? d0[u] : 0.f;
-            d1[u] = live[u] ? d1[u] : 0.f;
-            m0[u] = live[u] ? m0[u] : 0.f;
-            m1[u] = live[u] ? m1[u] : 0.f;
+            bf16x8 w[NG];
+#pragma unroll
+            for (int n = 0; n < NG; ++n) {
+                d[n][u] = live[u] ? d[n][u] : 0.f;
+                mn[n][u] = live[u] ? mn[n][u] : 0.f;
+                w[n] = i8x8_to_bf16(q[n][u]);
+            }
             const float sq = live[u] ? 1.f : 0.f;
-            const bf16x8 w0 = i8x8_to_bf16(q0[u]), w1 = i8x8_to_bf16(q1[u]);
             const float nw[8] = {nv[u][0].x, nv[u][0].y, nv[u][0].z, nv[u][0].w,
                                  nv[u][1].x, nv[u][1].y, nv[u][1].z, nv[u][1].w};
 #pragma unroll
@@ -282,29 +304,30 @@ __global__ __launch_bounds__(KS * kWave) void q8_gemm_kernel(WL wl, XIn xa, Epi 
                 }
                 const Bf16Pair a = split_bf16(xs);
                 const floatx4 z = {0.f, 0.f, 0.f, 0.f};
-                floatx4 t = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a.hi, w0, z, 0, 0, 0);
-                t = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a.lo, w0, t, 0, 0, 0);
-                floatx4 t1 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a.hi, w1, z, 0, 0, 0);
-                t1 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a.lo, w1, t1, 0, 0, 0);
+                floatx4 sx = z;
                 if constexpr (WL::kHasMin) {
                     // block-wise affine weights w = d q - m: sum w x = d (sum q x) - m (sum x);
                     // sum x per token comes out of one more product, against ones, already
                     // in the accumulator layout.
-                    floatx4 sx = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a.hi, bf16_ones(), z, 0, 0, 0);
+                    sx = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a.hi, bf16_ones(), z, 0, 0, 0);
                     sx = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a.lo, bf16_ones(), sx, 0, 0, 0);
-                    acc[0][i] += d0[u] * t - m0[u] * sx;
-                    acc[1][i] += d1[u] * t1 - m1[u] * sx;
-                } else {
-                    acc[0][i] += d0[u] * t;
-                    acc[1][i] += d1[u] * t1;
+                }
+#pragma unroll
+                for (int n = 0; n < NG; ++n) {
+                    floatx4 t = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a.hi, w[n], z, 0, 0, 0);
+                    t = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a.lo, w[n], t, 0, 0, 0);
+                    if constexpr (WL::kHasMin)
+                        acc[n][i] += d[n][u] * t - mn[n][u] * sx;
+                    else
+                        acc[n][i] += d[n][u] * t;
                 }
             }
         }
     }
 #pragma unroll
     for (int i = 0; i < MT; ++i) {
-        s_part[wv][0][i][lane] = acc[0][i];
-        s_part[wv][1][i][lane] = acc[1][i];
+#pragma unroll
+        for (int n = 0; n < NG; ++n) s_part[wv][n][i][lane] = acc[n][i];
         if (norm) {
             // the four lanes holding a token's k-chunks: lane ^ 16, lane ^ 32
             float s = ss[i] + wave_xor(ss[i], 16);
@@ -313,40 +336,43 @@ __global__ __launch_bounds__(KS * kWave) void q8_gemm_kernel(WL wl, XIn xa, Epi 
         }
     }
     __syncthreads();
-    if (wv < MT) {
-        const int i = wv;
-        floatx4 v0 = s_part[0][0][i][lane], v1 = s_part[0][1][i][lane];
+    if (cstore) {
+        const int ga = EG * cj, gb = EG * cj + EG - 1;
+        floatx4 v0 = s_part[0][ga][ci][lane], v1 = {0.f, 0.f, 0.f, 0.f};
+        if constexpr (EG == 2) v1 = s_part[0][gb][ci][lane];
 #pragma unroll
         for (int w = 1; w < KS; ++w) {
-            v0 += s_part[w][0][i][lane];
-            v1 += s_part[w][1][i][lane];
+            v0 += s_part[w][ga][ci][lane];
+            if constexpr (EG == 2) v1 += s_part[w][gb][ci][lane];
         }
         if (norm) {
 #pragma unroll
             for (int r = 0; r < 4; ++r) {
-                float s = s_ss[0][i][4 * kq + r];
+                float s = s_ss[0][ci][4 * kq + r];
 #pragma unroll
-                for (int w = 1; w < KS; ++w) s += s_ss[w][i][4 * kq + r];
+                for (int w = 1; w < KS; ++w) s += s_ss[w][ci][4 * kq + r];
                 const float rms = sqrtf(s / static_cast<float>(xa.in) + xa.eps);
                 v0[r] /= rms;
                 v1[r] /= rms;
             }
         }
-        epi.apply(p, lane, t0 + 16 * i + 4 * kq, xa.T, v0, v1, pre);
+        epi.apply(cunit, lane, t0 + 16 * ci + 4 * kq, xa.T, v0, v1, pre);
     }
 }
 
 // ---------------------------------------------------------------- epilogues
 
-// y[m][row] (= or +=) for rows < rows; pair p = groups 2p, 2p+1.
-template <bool ADD>
+// y[m][row] (= or +=) for rows < rows. NG = 2: pair p = groups 2p, 2p+1; NG = 1:
+// workgroup p owns group p alone (twice the workgroups, half the bytes each).
+template <bool ADD, int NG = 2>
 struct EpiStore {
+    static constexpr int kGroups = NG;
     float* y;
     uint32_t ldy;
     uint32_t rows;
     __device__ __forceinline__ void groups(uint32_t p, uint32_t& g0, uint32_t& g1) const {
-        g0 = 2 * p;
-        g1 = 2 * p + 1;
+        g0 = NG * p;
+        g1 = NG * p + 1;
     }
     struct Pre {
         float a0[4], a1[4];  // residual values (ADD)
@@ -354,28 +380,28 @@ struct EpiStore {
     __device__ __forceinline__ Pre pre(uint32_t p, int lane, uint32_t m0, uint32_t T) const {
         Pre r{};
         if constexpr (ADD) {
-            const uint32_t r0 = 32 * p + (lane & 15), r1 = r0 + 16;
+            const uint32_t r0 = 16 * NG * p + (lane & 15), r1 = r0 + 16;
 #pragma unroll
             for (int i = 0; i < 4; ++i) {
                 const uint32_t m = m0 + i;
                 if (m >= T) break;
                 const float* yr = y + static_cast<size_t>(m) * ldy;
                 if (r0 < rows) r.a0[i] = yr[r0];
-                if (r1 < rows) r.a1[i] = yr[r1];
+                if (NG == 2 && r1 < rows) r.a1[i] = yr[r1];
             }
         }
         return r;
     }
     __device__ __forceinline__ void apply(uint32_t p, int lane, uint32_t m0, uint32_t T, const floatx4& v0,
                                           const floatx4& v1, const Pre& pr) const {
-        const uint32_t r0 = 32 * p + (lane & 15), r1 = r0 + 16;
+        const uint32_t r0 = 16 * NG * p + (lane & 15), r1 = r0 + 16;
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
             const uint32_t m = m0 + r;
             if (m >= T) break;
             float* yr = y + static_cast<size_t>(m) * ldy;
             if (r0 < rows) yr[r0] = ADD ? pr.a0[r] + v0[r] : v0[r];
-            if (r1 < rows) yr[r1] = ADD ? pr.a1[r] + v1[r] : v1[r];
+            if (NG == 2 && r1 < rows) yr[r1] = ADD ? pr.a1[r] + v1[r] : v1[r];
         }
     }
 };
@@ -384,6 +410,7 @@ struct EpiStore {
 // 2j+1: up rows 16j..): h[m][16p + lane%16] = silu(gate) * up, silu(g) =
 // g / (1 + exp(-g)) (src/model.rs:375-378).
 struct EpiSwiGLU {
+    static constexpr int kGroups = 2;
     float* h;
     uint32_t ldh;
     uint32_t inter;
@@ -414,6 +441,7 @@ struct EpiSwiGLU {
 // Q heads go to q[m][h][64]; K heads (rotated) and V heads go straight into the
 // F32 pool row slot_mapping[m] (write_kv_slots, src/kv_cache/storage.rs:219-254).
 struct EpiQkvRope {
+    static constexpr int kGroups = 2;
     float* q;
     float* k_pool;
     float* v_pool;
@@ -503,6 +531,7 @@ __device__ __forceinline__ unsigned long long argmax_key(float v, uint32_t idx) 
 // workgroup and token serialises on the token's address); a second kernel takes
 // the maximum over the pairs.
 struct EpiArgmax {
+    static constexpr int kGroups = 2;
     float* logits;  // may be null
     uint32_t ld;
     uint32_t rows;
@@ -542,28 +571,74 @@ struct EpiArgmax {
 
 // Launch helper: K split over 8 waves (so a token's result never depends on the
 // batch size), U blocks of loads in flight per wave so that a whole row (960 or
-// 2560 wide) is requested in one round. Up to 256 tokens a workgroup takes 16 of
-// them (MT = 1): at decode sizes more workgroups in flight beat the weight reuse
-// of wider token tiles (re-reads hit L2 / MALL); above, 64 (MT = 4).
-template <int MT, bool NORM, class WL, class Epi>
-inline void launch_mt(const WL& wl, const XIn& xa, const Epi& epi, uint32_t pairs, uint32_t nb, hipStream_t s) {
-    const dim3 grid(pairs, (xa.T + 16 * MT - 1) / (16 * MT));
+// 2560 wide) is requested in one round where the registers allow. Up to 256
+// tokens a workgroup takes 16 of them (MT = 1): at decode sizes more workgroups
+// in flight beat the weight reuse of wider token tiles (re-reads hit L2 / MALL);
+// above, 64 (MT = 4).
+template <int U, int MT, int NU, bool NORM, class WL, class Epi>
+inline void launch_u(const WL& wl, const XIn& xa, const Epi& epi, uint32_t units, hipStream_t s) {
+    const dim3 grid((units + NU - 1) / NU, (xa.T + 16 * MT - 1) / (16 * MT));
+    hipLaunchKernelGGL((q8_gemm_kernel<8, U, MT, NU, NORM, WL, Epi>), grid, dim3(8 * kWave), 0, s, wl, xa, epi,
+                       units);
+}
+
+template <int MT, int NU, bool NORM, class WL, class Epi>
+inline void launch_mt(const WL& wl, const XIn& xa, const Epi& epi, uint32_t units, uint32_t nb, hipStream_t s) {
+    constexpr int NG = NU * Epi::kGroups;
     if constexpr (MT == 4)  // 64 tokens of x per block already fill the registers
-        hipLaunchKernelGGL((q8_gemm_kernel<8, 2, MT, NORM, WL, Epi>), grid, dim3(8 * kWave), 0, s, wl, xa, epi);
+        launch_u<2, MT, NU, NORM>(wl, xa, epi, units, s);
+    else if constexpr (NG >= 8)
+        launch_u<2, MT, NU, NORM>(wl, xa, epi, units, s);
     else if (nb <= 32)
-        hipLaunchKernelGGL((q8_gemm_kernel<8, 4, MT, NORM, WL, Epi>), grid, dim3(8 * kWave), 0, s, wl, xa, epi);
-    else if (NORM || nb <= 40)  // (the norm weights of 10 blocks would not fit the registers)
-        hipLaunchKernelGGL((q8_gemm_kernel<8, 5, MT, NORM, WL, Epi>), grid, dim3(8 * kWave), 0, s, wl, xa, epi);
-    else if constexpr (!NORM)  // 2560-wide rows (the down projection) in one round
-        hipLaunchKernelGGL((q8_gemm_kernel<8, 10, MT, NORM, WL, Epi>), grid, dim3(8 * kWave), 0, s, wl, xa, epi);
+        launch_u<4, MT, NU, NORM>(wl, xa, epi, units, s);
+    else if (NORM || nb <= 40 || NG > 2)  // (the norm weights of 10 blocks would not fit the registers)
+        launch_u<5, MT, NU, NORM>(wl, xa, epi, units, s);
+    else if constexpr (!NORM && NG <= 2)  // 2560-wide rows (the down projection) in one round
+        launch_u<10, MT, NU, NORM>(wl, xa, epi, units, s);
+}
+
+// Plain stores need no partner group: with 16-token tiles a unit is one 16-row
+// group, so narrow products get twice the workgroups (960 rows: 30 pairs would
+// keep 30 CUs busy at batch 1, each pulling a whole pair's weights).
+template <class Epi>
+struct SingleGroup {
+    static constexpr bool kOk = false;
+};
+template <bool ADD>
+struct SingleGroup<EpiStore<ADD, 2>> {
+    static constexpr bool kOk = true;
+    static EpiStore<ADD, 1> make(const EpiStore<ADD, 2>& e) { return {e.y, e.ldy, e.rows}; }
+};
+
+// Units per workgroup for 16-token tiles: the widest of 1, 2, 4 that still leaves
+// kMinWgs workgroups (each x load then feeds NU units' products).
+constexpr uint32_t kMinWgs = 512;
+
+inline uint32_t pick_nu(uint32_t units, uint32_t tiles) {
+    uint32_t nu = 1;
+    while (nu < 4 && (units + 2 * nu - 1) / (2 * nu) * tiles >= kMinWgs) nu *= 2;
+    return nu;
+}
+
+template <bool NORM, class WL, class Epi>
+inline void launch_mt1(const WL& wl, const XIn& xa, const Epi& epi, uint32_t units, uint32_t nb, hipStream_t s) {
+    const uint32_t nu = pick_nu(units, (xa.T + 15) / 16);
+    if (nu >= 4)
+        launch_mt<1, 4, NORM>(wl, xa, epi, units, nb, s);
+    else if (nu == 2)
+        launch_mt<1, 2, NORM>(wl, xa, epi, units, nb, s);
+    else
+        launch_mt<1, 1, NORM>(wl, xa, epi, units, nb, s);
 }
 
 template <bool NORM, class WL, class Epi>
 inline void launch_norm(const WL& wl, const XIn& xa, const Epi& epi, uint32_t pairs, uint32_t nb, hipStream_t s) {
-    if (xa.T <= 256)
-        launch_mt<1, NORM>(wl, xa, epi, pairs, nb, s);
+    if (xa.T > 256)
+        launch_mt<4, 1, NORM>(wl, xa, epi, pairs, nb, s);
+    else if constexpr (SingleGroup<Epi>::kOk)
+        launch_mt1<NORM>(wl, xa, SingleGroup<Epi>::make(epi), (epi.rows + 15) / 16, nb, s);
     else
-        launch_mt<4, NORM>(wl, xa, epi, pairs, nb, s);
+        launch_mt1<NORM>(wl, xa, epi, pairs, nb, s);
 }
 
 template <class WL, class Epi>
