@@ -307,6 +307,53 @@ def engine_bench(ctx, K, torch, num_requests=64):
     return out
 
 
+def verify_bench(ctx, K, torch, num_seqs=16, context=1000, rows=5, reps=20):
+    """Speculative verify rows (forward_batch_all_rows, src/model.rs:1382-1410) on the
+    config-5 model: num_seqs sequences with `context` cached tokens each score `rows`
+    candidate tokens in one step (every row through the lm_head and greedy argmax),
+    against a plain decode step of the same sequences (one row each)."""
+    from kanso_infer_amd.engine import Model, ModelConfig
+    cfg = ModelConfig.smollm2_360m(max_position=4096)
+    model = Model(ctx, cfg)
+    model.init_random(seed=0x5EED0057, std=0.02)
+    per_seq = -(-(context + rows) // 16)
+    model.alloc_kv(num_seqs * per_seq, 16, 512, 65)
+    rng = np.random.default_rng(0x5EED0090)
+    tables = [np.arange(s * per_seq, (s + 1) * per_seq, dtype=np.uint32) for s in range(num_seqs)]
+    toks = [rng.integers(0, cfg.vocab_size, context + rows).astype(np.uint32) for _ in range(num_seqs)]
+
+    def step(seqs):  # seqs: (s, start, q_len)
+        plan, arena, tabs = [], [], []
+        for s, start, ql in seqs:
+            plan.append([start, ql, len(tabs), per_seq, (len(arena) - start) % (1 << 32)])
+            arena.extend(toks[s][start:start + ql])
+            tabs.extend(tables[s])
+        return np.array(plan, np.uint32), np.array(arena, np.uint32), np.array(tabs, np.uint32)
+
+    for s in range(num_seqs):  # prefill in chunks under the 512-token budget
+        for lo in range(0, context, 500):
+            model.forward(*step([(s, lo, min(500, context - lo))]))
+    dec = step([(s, context, 1) for s in range(num_seqs)])
+    ver = step([(s, context, rows) for s in range(num_seqs)])
+
+    def timed(fn, args):
+        for _ in range(3):
+            fn(*args)
+        t0 = time.perf_counter()
+        for _ in range(reps):
+            fn(*args)
+        return (time.perf_counter() - t0) / reps
+
+    t_dec = timed(model.forward, dec)
+    t_ver = timed(model.forward_all_rows, ver)
+    model.close()
+    return dict(sequences=num_seqs, context=context, rows_per_sequence=rows,
+                decode_step_ms=round(t_dec * 1e3, 3), verify_step_ms=round(t_ver * 1e3, 3),
+                verify_rows_per_s=round(num_seqs * rows / t_ver, 1),
+                verify_over_decode=round(t_ver / t_dec, 3),
+                timing="host wall clock per synchronous forward (the entry point synchronises)")
+
+
 def config5_cpu_baseline(threads=None):
     """The oracle (C++ restatement of the reference CPU path, OpenMP) running the full
     SmolLM2-360M-shape model: one decode step of 16 sequences with contexts
@@ -713,6 +760,8 @@ def main():
         log(f"reference probes: {extras['reference_probes']}")
         torch.cuda.empty_cache()
     if not args.quick and not args.skip_config5:
+        extras["verify_rows"] = verify_bench(ctx, K, torch)
+        log(f"verify rows: {extras['verify_rows']}")
         extras["config5_engine"] = engine_bench(ctx, K, torch)
         log(f"config5: {extras['config5_engine']}")
         extras["config5_engine"]["checksum_parity"] = config5_checksum_parity(ctx, K, torch)

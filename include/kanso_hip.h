@@ -407,6 +407,16 @@ int kanso_model_forward(kanso_model* model, const kanso_seq_plan* plan, uint32_t
                         const uint32_t* table_arena, uint32_t table_arena_len, float* logits,
                         uint32_t* next_tokens, kanso_stream_t stream);
 
+/* Model::forward_batch_all_rows (src/model.rs:1382-1410, RowSelection::EveryToken):
+ * the same forward, but the final norm, lm_head and greedy argmax run on every new
+ * token, the rows a speculative verifier scores its candidates with. next_tokens
+ * (host) has T = sum of q_len entries, in plan order; logits [T][vocab] (device)
+ * when non-NULL. Synchronises `stream`. */
+int kanso_model_forward_all_rows(kanso_model* model, const kanso_seq_plan* plan, uint32_t num_seqs,
+                                 const uint32_t* token_arena, uint32_t token_arena_len,
+                                 const uint32_t* table_arena, uint32_t table_arena_len, float* logits,
+                                 uint32_t* next_tokens, kanso_stream_t stream);
+
 /* Engine::new_with_budget (src/engine.rs:46-125): a block pool of total_blocks,
  * a prefix cache, max_running sequences, token_budget tokens per step. model may be
  * NULL: the engine then plans and commits with a deterministic stand-in token

@@ -172,6 +172,7 @@ SIGNATURES: dict[str, tuple] = {
     "kanso_model_reset_blocks": (_I, [_P, _P, _U, _P]),
     "kanso_model_read_kv_rows": (_I, [_P, _U, _P, _U, _P, _P]),
     "kanso_model_forward": (_I, [_P, _P, _U, _P, _U, _P, _U, _P, _P, _P]),
+    "kanso_model_forward_all_rows": (_I, [_P, _P, _U, _P, _U, _P, _U, _P, _P, _P]),
     "kanso_engine_create": (_I, [_P, _U, _U, _U, _U, _U, C.POINTER(_P)]),
     "kanso_engine_destroy": (_I, [_P]),
     "kanso_engine_add_request": (_I, [_P, _P, _U, _U, _P, _U, C.POINTER(C.c_uint64)]),

@@ -247,7 +247,11 @@ int model_reset_blocks(kanso_model* m, const uint32_t* blocks, uint32_t n, hipSt
     return KANSO_OK;
 }
 
-int model_forward(kanso_model* m, const HostStep& step, float* logits, uint32_t* next, hipStream_t s) {
+// all_rows: RowSelection::EveryToken (src/model.rs:1382-1410): the lm_head and the
+// greedy argmax run on every new token (next / logits have T rows), not only on each
+// sequence's last one.
+int model_forward(kanso_model* m, const HostStep& step, float* logits, uint32_t* next, hipStream_t s,
+                  bool all_rows) {
     const kanso_model_config& c = m->cfg;
     const uint32_t S = static_cast<uint32_t>(step.plan.size());
     if (S == 0) {
@@ -274,8 +278,9 @@ int model_forward(kanso_model* m, const HostStep& step, float* logits, uint32_t*
         }
         max_blocks = std::max(max_blocks, std::max((ctx + m->block_size - 1) / m->block_size, 1u));
     }
-    int rc = ensure_step_buffers(m, T, S, S * max_blocks, static_cast<uint32_t>(step.token_arena.size() +
-                                                                                   step.table_arena.size()));
+    const uint32_t R = all_rows ? T : S;  // rows through the lm_head
+    int rc = ensure_step_buffers(m, T, std::max(S, R), S * max_blocks,
+                                 static_cast<uint32_t>(step.token_arena.size() + step.table_arena.size()));
     if (rc) return rc;
     // Stage: plan | token arena + table arena | last rows.
     char* h = static_cast<char*>(m->h_stage);
@@ -286,12 +291,16 @@ int model_forward(kanso_model* m, const HostStep& step, float* logits, uint32_t*
     std::memcpy(h + off_arena, step.token_arena.data(), step.token_arena.size() * 4);
     std::memcpy(h + off_arena + step.token_arena.size() * 4, step.table_arena.data(), step.table_arena.size() * 4);
     int32_t* last = reinterpret_cast<int32_t*>(h + off_last);
-    int32_t run = 0;
-    for (uint32_t i = 0; i < S; ++i) {
-        run += static_cast<int32_t>(step.plan[i].q_len);
-        last[i] = run - 1;
+    if (all_rows) {
+        for (uint32_t i = 0; i < T; ++i) last[i] = static_cast<int32_t>(i);
+    } else {
+        int32_t run = 0;
+        for (uint32_t i = 0; i < S; ++i) {
+            run += static_cast<int32_t>(step.plan[i].q_len);
+            last[i] = run - 1;
+        }
     }
-    KANSO_HIP_TRY(hipMemcpyAsync(m->d_stage, h, off_last + S * 4, hipMemcpyHostToDevice, s));
+    KANSO_HIP_TRY(hipMemcpyAsync(m->d_stage, h, off_last + R * 4ull, hipMemcpyHostToDevice, s));
     char* d = static_cast<char*>(m->d_stage);
     const auto* d_plan = reinterpret_cast<const kanso_seq_plan*>(d);
     const auto* d_tok_arena = reinterpret_cast<const uint32_t*>(d + off_arena);
@@ -346,12 +355,12 @@ int model_forward(kanso_model* m, const HostStep& step, float* logits, uint32_t*
             return rc;
         if ((rc = op_gemm_residual(L.down, m->act, m->hidden, c.hidden, c.intermediate, T, s))) return rc;
     }
-    if ((rc = op_lm_head_argmax(m->ctx, m->lm_head, m->hidden, d_last, m->final_norm, c.eps, S, c.hidden, c.vocab,
+    if ((rc = op_lm_head_argmax(m->ctx, m->lm_head, m->hidden, d_last, m->final_norm, c.eps, R, c.hidden, c.vocab,
                                 logits, m->next, s)))
         return rc;
-    KANSO_HIP_TRY(hipMemcpyAsync(m->h_next, m->next, S * 4ull, hipMemcpyDeviceToHost, s));
+    KANSO_HIP_TRY(hipMemcpyAsync(m->h_next, m->next, R * 4ull, hipMemcpyDeviceToHost, s));
     KANSO_HIP_TRY(hipStreamSynchronize(s));
-    std::memcpy(next, m->h_next, S * 4ull);
+    std::memcpy(next, m->h_next, R * 4ull);
     ++m->forward_calls;
     return KANSO_OK;
 }
@@ -578,13 +587,16 @@ int kanso_model_reset_blocks(kanso_model* m, const uint32_t* blocks, uint32_t n,
     return model_reset_blocks(m, blocks, n, as_stream(stream));
 }
 
-int kanso_model_forward(kanso_model* m, const kanso_seq_plan* plan, uint32_t num_seqs, const uint32_t* token_arena,
-                        uint32_t token_arena_len, const uint32_t* table_arena, uint32_t table_arena_len,
-                        float* logits, uint32_t* next_tokens, kanso_stream_t stream) {
-    int rc = model_check(m, "kanso_model_forward");
+namespace {
+
+int model_forward_entry(kanso_model* m, const char* name, const kanso_seq_plan* plan, uint32_t num_seqs,
+                        const uint32_t* token_arena, uint32_t token_arena_len, const uint32_t* table_arena,
+                        uint32_t table_arena_len, float* logits, uint32_t* next_tokens, kanso_stream_t stream,
+                        bool all_rows) {
+    int rc = model_check(m, name);
     if (rc) return rc;
     if (!plan || !token_arena || !table_arena || !next_tokens || num_seqs == 0) {
-        set_error("kanso_model_forward: null argument or empty plan");
+        set_error("%s: null argument or empty plan", name);
         return KANSO_E_INVALID_ARG;
     }
     HostStep hs;
@@ -593,16 +605,33 @@ int kanso_model_forward(kanso_model* m, const kanso_seq_plan* plan, uint32_t num
     hs.table_arena.assign(table_arena, table_arena + table_arena_len);
     for (const auto& p : hs.plan) {
         if (static_cast<uint64_t>(p.table_offset) + p.table_len > table_arena_len) {
-            set_error("kanso_model_forward: table range outside the table arena");
+            set_error("%s: table range outside the table arena", name);
             return KANSO_E_OUT_OF_BOUNDS;
         }
         for (uint32_t i = 0; i < p.q_len; ++i)
             if (static_cast<uint32_t>(p.token_offset + p.start_pos + i) >= token_arena_len) {
-                set_error("kanso_model_forward: token outside the token arena");
+                set_error("%s: token outside the token arena", name);
                 return KANSO_E_OUT_OF_BOUNDS;
             }
     }
-    return model_forward(m, hs, logits, next_tokens, as_stream(stream));
+    return model_forward(m, hs, logits, next_tokens, as_stream(stream), all_rows);
+}
+
+}  // namespace
+
+int kanso_model_forward(kanso_model* m, const kanso_seq_plan* plan, uint32_t num_seqs, const uint32_t* token_arena,
+                        uint32_t token_arena_len, const uint32_t* table_arena, uint32_t table_arena_len,
+                        float* logits, uint32_t* next_tokens, kanso_stream_t stream) {
+    return model_forward_entry(m, "kanso_model_forward", plan, num_seqs, token_arena, token_arena_len, table_arena,
+                               table_arena_len, logits, next_tokens, stream, false);
+}
+
+int kanso_model_forward_all_rows(kanso_model* m, const kanso_seq_plan* plan, uint32_t num_seqs,
+                                 const uint32_t* token_arena, uint32_t token_arena_len, const uint32_t* table_arena,
+                                 uint32_t table_arena_len, float* logits, uint32_t* next_tokens,
+                                 kanso_stream_t stream) {
+    return model_forward_entry(m, "kanso_model_forward_all_rows", plan, num_seqs, token_arena, token_arena_len,
+                               table_arena, table_arena_len, logits, next_tokens, stream, true);
 }
 
 }  // extern "C"

@@ -77,6 +77,7 @@ namespace kanso {
 int model_reset_blocks(kanso_model* m, const uint32_t* blocks, uint32_t n, hipStream_t s);
 // One batched forward; next[s] = greedy token of sequence s's last row. logits
 // (device, [S][vocab]) is written when non-null.
-int model_forward(kanso_model* m, const HostStep& step, float* logits, uint32_t* next, hipStream_t s);
+int model_forward(kanso_model* m, const HostStep& step, float* logits, uint32_t* next, hipStream_t s,
+                  bool all_rows = false);
 
 }  // namespace kanso

@@ -186,6 +186,24 @@ class Model:
             _stream(None)))
         return out
 
+    def forward_all_rows(self, plan: np.ndarray, token_arena: np.ndarray, table_arena: np.ndarray,
+                         logits: torch.Tensor | None = None) -> np.ndarray:
+        """Model::forward_batch_all_rows (src/model.rs:1382-1410): the same forward,
+        returning the greedy token of every new token (plan order, T entries) and,
+        when `logits` is given, writing [T, vocab] into it."""
+        plan = np.ascontiguousarray(plan, dtype=np.uint32)
+        toks = np.ascontiguousarray(token_arena, dtype=np.uint32)
+        tabs = np.ascontiguousarray(table_arena, dtype=np.uint32)
+        S = plan.shape[0]
+        T = int(plan[:, 1].sum())
+        out = np.zeros(T, np.uint32)
+        _check(self._lib.kanso_model_forward_all_rows(
+            self.handle, plan.ctypes.data_as(C.c_void_p), S, toks.ctypes.data_as(C.c_void_p),
+            toks.size, tabs.ctypes.data_as(C.c_void_p), tabs.size,
+            None if logits is None else logits.data_ptr(), out.ctypes.data_as(C.c_void_p),
+            _stream(None)))
+        return out
+
 
 @dataclass
 class StepOutput:

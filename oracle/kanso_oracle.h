@@ -179,6 +179,17 @@ int oracle_forward_batch(const oracle_model_config* cfg, const oracle_model_weig
                          const int32_t* cu_seqlens, const uint32_t* context_lens, uint32_t S,
                          float* logits, int nthreads);
 
+/* The shared body of forward_batch / forward_batch_all_rows (src/model.rs:1382-1410,
+ * RowSelection): all_rows = 0 gives logits [S][vocab] of each sequence's last row,
+ * all_rows = 1 logits [T][vocab] of every new token (the speculative verifier's rows). */
+int oracle_forward_batch_rows(const oracle_model_config* cfg, const oracle_model_weights* w,
+                              const uint32_t* tokens, const int32_t* positions,
+                              const int64_t* slot_mapping, uint32_t T, float* const* k_pools,
+                              float* const* v_pools, uint32_t num_blocks, uint32_t block_size,
+                              const uint32_t* block_tables, uint32_t max_blocks,
+                              const int32_t* cu_seqlens, const uint32_t* context_lens, uint32_t S,
+                              int all_rows, float* logits, int nthreads);
+
 #ifdef __cplusplus
 }
 #endif

@@ -17,13 +17,13 @@
 
 extern "C" {
 
-int oracle_forward_batch(const oracle_model_config* cfg, const oracle_model_weights* w,
-                         const uint32_t* tokens, const int32_t* positions,
-                         const int64_t* slot_mapping, uint32_t T, float* const* k_pools,
-                         float* const* v_pools, uint32_t num_blocks, uint32_t block_size,
-                         const uint32_t* block_tables, uint32_t max_blocks,
-                         const int32_t* cu_seqlens, const uint32_t* context_lens, uint32_t S,
-                         float* logits, int nthreads) {
+int oracle_forward_batch_rows(const oracle_model_config* cfg, const oracle_model_weights* w,
+                              const uint32_t* tokens, const int32_t* positions,
+                              const int64_t* slot_mapping, uint32_t T, float* const* k_pools,
+                              float* const* v_pools, uint32_t num_blocks, uint32_t block_size,
+                              const uint32_t* block_tables, uint32_t max_blocks,
+                              const int32_t* cu_seqlens, const uint32_t* context_lens, uint32_t S,
+                              int all_rows, float* logits, int nthreads) {
     const uint32_t Hd = cfg->hidden, H = cfg->num_heads, HKV = cfg->num_kv_heads;
     const uint32_t D = cfg->head_dim, I = cfg->intermediate, V = cfg->vocab;
     if (T == 0 || S == 0 || H % HKV != 0 || Hd % 32 != 0 || I % 32 != 0 || D % 2 != 0) return -1;
@@ -89,15 +89,31 @@ int oracle_forward_batch(const oracle_model_config* cfg, const oracle_model_weig
         oracle_gemv_q8_0(w->w_down[l], act.data(), proj.data(), Hd, I, T, nthreads);
         for (size_t i = 0; i < hidden.size(); ++i) hidden[i] = hidden[i] + proj[i];
     }
-    // final norm, then lm_head on each sequence's last row (src/model.rs:1726-1738)
-    std::vector<float> last(static_cast<size_t>(S) * Hd);
-    for (uint32_t s = 0; s < S; ++s)
-        std::memcpy(&last[static_cast<size_t>(s) * Hd],
-                    &hidden[static_cast<size_t>(cu_seqlens[s + 1] - 1) * Hd], Hd * sizeof(float));
+    // final norm, then lm_head on every row (RowSelection::EveryToken) or on each
+    // sequence's last row (LastPerSequence), src/model.rs:1726-1738. The norm is per
+    // row, so normalising only the selected rows gives the same values.
+    const uint32_t R = all_rows ? T : S;
+    std::vector<float> last(static_cast<size_t>(R) * Hd);
+    for (uint32_t r = 0; r < R; ++r) {
+        const size_t src = all_rows ? r : static_cast<size_t>(cu_seqlens[r + 1] - 1);
+        std::memcpy(&last[static_cast<size_t>(r) * Hd], &hidden[src * Hd], Hd * sizeof(float));
+    }
     std::vector<float> last_normed(last.size());
-    oracle_rmsnorm(last.data(), w->final_norm, last_normed.data(), S, Hd, cfg->eps);
-    oracle_gemv_q8_0(w->lm_head, last_normed.data(), logits, V, Hd, S, nthreads);
+    oracle_rmsnorm(last.data(), w->final_norm, last_normed.data(), R, Hd, cfg->eps);
+    oracle_gemv_q8_0(w->lm_head, last_normed.data(), logits, V, Hd, R, nthreads);
     return 0;
+}
+
+int oracle_forward_batch(const oracle_model_config* cfg, const oracle_model_weights* w,
+                         const uint32_t* tokens, const int32_t* positions,
+                         const int64_t* slot_mapping, uint32_t T, float* const* k_pools,
+                         float* const* v_pools, uint32_t num_blocks, uint32_t block_size,
+                         const uint32_t* block_tables, uint32_t max_blocks,
+                         const int32_t* cu_seqlens, const uint32_t* context_lens, uint32_t S,
+                         float* logits, int nthreads) {
+    return oracle_forward_batch_rows(cfg, w, tokens, positions, slot_mapping, T, k_pools, v_pools,
+                                     num_blocks, block_size, block_tables, max_blocks, cu_seqlens,
+                                     context_lens, S, 0, logits, nthreads);
 }
 
 }  // extern "C"

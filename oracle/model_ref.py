@@ -50,7 +50,9 @@ class OracleModel:
         for a in self.k + self.v:
             a[block * w:(block + 1) * w] = 0.0
 
-    def logits(self, plan) -> np.ndarray:
+    def logits(self, plan, all_rows: bool = False) -> np.ndarray:
+        """[S, vocab] of each sequence's last row, or with all_rows [T, vocab] of every
+        new token (forward_batch_all_rows, src/model.rs:1382-1410)."""
         bs = self.block_size
         ctx = np.asarray(plan.context_lens, np.int64)
         max_blocks = int(max(1, ((ctx + bs - 1) // bs).max()))
@@ -62,7 +64,7 @@ class OracleModel:
         cu = np.concatenate([[0], np.cumsum(plan.query_lens)]).astype(np.int32)
         return oracle.forward_batch(self.cfg, self.weights, self.k, self.v, self.num_blocks, bs,
                                     plan.tokens, plan.positions, plan.slot_mapping, tables,
-                                    max_blocks, cu, ctx, nthreads=self.nthreads)
+                                    max_blocks, cu, ctx, nthreads=self.nthreads, all_rows=all_rows)
 
     def forward(self, plan) -> list:
         """engine_ref forward: greedy_token (src/sampler.rs:7-17) of each sequence."""

@@ -338,9 +338,10 @@ class ModelWeightsC(C.Structure):
 
 def forward_batch(cfg: dict, weights: dict, k_pools, v_pools, num_blocks, block_size, tokens,
                   positions, slot_mapping, block_tables, max_blocks, cu_seqlens, context_lens,
-                  nthreads=8) -> np.ndarray:
-    """oracle_forward_batch: logits [S, vocab] of each sequence's last row. k_pools /
-    v_pools are per-layer float32 arrays updated in place (write_kv_slots)."""
+                  nthreads=8, all_rows=False) -> np.ndarray:
+    """oracle_forward_batch_rows: logits [S, vocab] of each sequence's last row, or with
+    all_rows [T, vocab] of every new token (forward_batch_all_rows). k_pools / v_pools
+    are per-layer float32 arrays updated in place (write_kv_slots)."""
     L = cfg["num_layers"]
     c = ModelConfigC(cfg["hidden"], cfg["num_heads"], cfg["num_kv_heads"], cfg["head_dim"], L,
                      cfg["intermediate"], cfg["vocab"], cfg.get("eps", 1e-5),
@@ -366,13 +367,14 @@ def forward_batch(cfg: dict, weights: dict, k_pools, v_pools, num_blocks, block_
     cu = np.ascontiguousarray(cu_seqlens, dtype=np.int32)
     ctx = _u32(context_lens)
     S = ctx.size
-    logits = np.zeros((S, cfg["vocab"]), np.float32)
-    fn = lib().oracle_forward_batch
+    logits = np.zeros((tokens.size if all_rows else S, cfg["vocab"]), np.float32)
+    fn = lib().oracle_forward_batch_rows
     fn.restype = C.c_int
     rc = fn(C.byref(c), C.byref(w), _p(tokens), _p(positions), _p(slots), C.c_uint32(tokens.size),
             C.cast(kp, C.POINTER(C.c_void_p)), C.cast(vp, C.POINTER(C.c_void_p)),
             C.c_uint32(num_blocks), C.c_uint32(block_size), _p(tables), C.c_uint32(max_blocks),
-            _p(cu), _p(ctx), C.c_uint32(S), _p(logits), C.c_int(nthreads))
+            _p(cu), _p(ctx), C.c_uint32(S), C.c_int(1 if all_rows else 0), _p(logits),
+            C.c_int(nthreads))
     if rc != 0:
         raise RuntimeError("oracle_forward_batch rejected the batch")
     return logits

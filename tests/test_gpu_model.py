@@ -86,6 +86,40 @@ def test_forward_logits_match_oracle(ctx, cfg):
             assert_close(v, om.v[layer].reshape(-1, width)[slots], what=f"V pool layer {layer}")
 
 
+@pytest.mark.parametrize("cfg", [SMALL, SMOL4], ids=["small", "smollm2_width_4_layers"])
+def test_forward_all_rows_match_oracle(ctx, cfg):
+    """kanso_model_forward_all_rows (forward_batch_all_rows, src/model.rs:1382-1410):
+    logits and greedy tokens of every new token of mixed steps, against the oracle's
+    EveryToken rows; each sequence's last row is also what kanso_model_forward gives."""
+    bs, nblocks = 16, 40
+    rng = np.random.default_rng(12)
+    w = random_weights(cfg, seed=6)
+    gm = gpu_model(ctx, cfg, w, nblocks, bs)
+    om = OracleModel(cfg, w, nblocks, bs)
+    for step, plan in enumerate(mixed_plans(rng, bs, cfg["vocab"], nblocks)):
+        rows, toks, tabs = compact(plan, bs)
+        T = int(rows[:, 1].sum())
+        logits = torch.empty(T * cfg["vocab"], device="cuda:0")
+        got_tok = gm.forward_all_rows(rows, toks, tabs, logits=logits)
+        ctx.check_device_status()
+        assert got_tok.shape == (T,)
+        want = om.logits(plan, all_rows=True)
+        got = host(logits).reshape(T, cfg["vocab"])
+        assert_close(got, want, what=f"all-row logits step {step}")
+        for t in range(T):
+            assert got_tok[t] == oracle.greedy(got[t])
+    # a second model, same steps through kanso_model_forward: its tokens are the
+    # all-row tokens at each sequence's last row
+    gm2 = gpu_model(ctx, cfg, w, nblocks, bs)
+    gm3 = gpu_model(ctx, cfg, w, nblocks, bs)
+    rng = np.random.default_rng(12)
+    for plan in mixed_plans(rng, bs, cfg["vocab"], nblocks):
+        rows, toks, tabs = compact(plan, bs)
+        last = np.cumsum(rows[:, 1]) - 1
+        np.testing.assert_array_equal(gm3.forward_all_rows(rows, toks, tabs)[last],
+                                      gm2.forward(rows, toks, tabs))
+
+
 def test_quantize_q8_0_bit_exact(ctx):
     rng = np.random.default_rng(3)
     x = (rng.standard_normal(32 * 4096) * np.repeat(rng.uniform(0, 3, 4096), 32)).astype(np.float32)

@@ -58,6 +58,32 @@ def test_batched_equals_per_sequence(weights):
         np.testing.assert_allclose(batched[s], alone[0], atol=1e-5, rtol=1e-5)
 
 
+def test_all_rows(weights):
+    """RowSelection::EveryToken (src/model.rs:1382-1410, 1730-1732). Row i of a
+    sequence is the distribution after its first i+1 new tokens: by causality it equals
+    the last-row logits of a forward over that prefix alone (fresh pools), and each
+    sequence's final row equals the LastPerSequence result of the same batch."""
+    bs = 4
+    rng = np.random.default_rng(2)
+    seqs = [(list(rng.integers(0, CFG["vocab"], n)), 0, tab)
+            for n, tab in [(6, [3, 4]), (1, [8]), (9, [0, 1, 2])]]
+    every = OracleModel(CFG, weights, 16, bs).logits(plan_of(seqs, bs), all_rows=True)
+    assert every.shape == (16, CFG["vocab"])
+    last = OracleModel(CFG, weights, 16, bs).logits(plan_of(seqs, bs))
+    cu = np.cumsum([0] + [len(t) for t, _, _ in seqs])
+    np.testing.assert_array_equal(every[cu[1:] - 1], last)
+    for s, (toks, _, tab) in enumerate(seqs):
+        for i in range(len(toks)):
+            prefix = OracleModel(CFG, weights, 16, bs).logits(plan_of([(toks[:i + 1], 0, tab)], bs))
+            np.testing.assert_allclose(every[cu[s] + i], prefix[0], atol=1e-5, rtol=1e-5)
+    # a continuation chunk: rows after a cached prefix
+    m = OracleModel(CFG, weights, 16, bs)
+    toks, _, tab = seqs[2]
+    m.logits(plan_of([(toks[:4], 0, tab)], bs))
+    cont = m.logits(plan_of([(toks[4:], 4, tab)], bs), all_rows=True)
+    np.testing.assert_allclose(cont, every[cu[2] + 4:cu[3]], atol=1e-5, rtol=1e-5)
+
+
 def _f64_forward(cfg, w, tokens):
     """One sequence from position 0, every op in float64 numpy (no paging)."""
     h, H, KV, D = cfg["hidden"], cfg["num_heads"], cfg["num_kv_heads"], cfg["head_dim"]
