@@ -602,6 +602,8 @@ def main():
                          "headline attention calls; prints nothing else")
     ap.add_argument("--pool-layout", choices=("token", "head"), default="token",
                     help="row order inside a KV block for the attention benchmarks")
+    ap.add_argument("--verify-only", action="store_true",
+                    help="only the speculative verify-step timing (one JSON line)")
     ap.add_argument("--config5-only", action="store_true",
                     help="run only the config-5 engine benchmark and print its JSON")
     ap.add_argument("--partition", type=int, default=0,
@@ -629,6 +631,10 @@ def main():
         sys.path.insert(0, str(ROOT / "oracle"))
         import oracle as oracle_mod
         gemm_probe(ctx, torch, K, oracle_mod)
+        ctx.close()
+        return
+    if args.verify_only:
+        print(json.dumps(verify_bench(ctx, K, torch)), flush=True)
         ctx.close()
         return
     if args.config5_only:
