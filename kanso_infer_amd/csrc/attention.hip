@@ -1176,22 +1176,28 @@ __device__ void chunk_block(const AttnArgs& a, const SeqTable& st, const PoolRsr
         }
     }
 
+    // Two raw tiles ping-pong in fixed registers (the loop is unrolled by two, so no
+    // register copy waits on a load in flight), and every load is issued without a
+    // branch: keys past the partition read out of range (zeros, no traffic). Tile
+    // i + 2 is then in flight while tile i is scored and tile i + 1 is staged,
+    // instead of every iteration waiting for all outstanding loads.
     const uint32_t n_tiles = ceil_div(t_end - t_begin, kChunkKeys);
     RawTile ra, rb;
     chunk_load_raw<KVT>(a, rs, pv, t_begin, kvh, ra);
-    if (n_tiles > 1) chunk_load_raw<KVT>(a, rs, pv, t_begin + kChunkKeys, kvh, rb);
+    chunk_load_raw<KVT>(a, rs, pv, t_begin + kChunkKeys, kvh, rb);
     chunk_store(ra, stage[0]);
     __syncthreads();
-    for (uint32_t i = 0; i < n_tiles; ++i) {
-        // rb holds tile i + 1 (in flight); ra is free for tile i + 2.
-        if (i + 2 < n_tiles) chunk_load_raw<KVT>(a, rs, pv, t_begin + kChunkKeys * (i + 2), kvh, ra);
-        if (nrows > 0)
-            chunk_compute<G>(a, stage[i & 1], t_begin + kChunkKeys * i, t_end, lane, lim, qs, o, m, l);
-        if (i + 1 < n_tiles) chunk_store(rb, stage[(i + 1) & 1]);
+    for (uint32_t i = 0; i < n_tiles; i += 2) {
+        chunk_load_raw<KVT>(a, rs, pv, t_begin + kChunkKeys * (i + 2), kvh, ra);
+        if (nrows > 0) chunk_compute<G>(a, stage[0], t_begin + kChunkKeys * i, t_end, lane, lim, qs, o, m, l);
+        chunk_store(rb, stage[1]);
         __syncthreads();
-        const RawTile t = ra;
-        ra = rb;
-        rb = t;
+        if (i + 1 >= n_tiles) break;
+        chunk_load_raw<KVT>(a, rs, pv, t_begin + kChunkKeys * (i + 3), kvh, rb);
+        if (nrows > 0)
+            chunk_compute<G>(a, stage[1], t_begin + kChunkKeys * (i + 1), t_end, lane, lim, qs, o, m, l);
+        chunk_store(ra, stage[0]);
+        __syncthreads();
     }
 
     // Lane holds O^T[d = 16(lane/16) + 4r + nb][query qi] in o[g][nb][r].
