@@ -144,15 +144,19 @@ __device__ void load_seq_table(const AttnArgs& a, SeqTable& st) {
         st.pre[s + 1] = run;  // inclusive within this thread's segment
     }
     if (!CHUNK && flags && blockIdx.x == 0) raise_status(a.status, flags);
-    st.part_sums[tid] = run;
-    __syncthreads();
-    for (uint32_t off = 1; off < kThreads; off <<= 1) {
-        const uint32_t v = tid >= off ? st.part_sums[tid - off] : 0;
-        __syncthreads();
-        st.part_sums[tid] += v;
-        __syncthreads();
+    // exclusive prefix of the per-thread totals: a shuffle scan inside each wave,
+    // then the wave totals through LDS (one barrier instead of two per step)
+    const uint32_t lane = tid & (kWave - 1), wv = tid / kWave;
+    uint32_t incl = run;
+#pragma unroll
+    for (uint32_t off = 1; off < kWave; off <<= 1) {
+        const uint32_t v = __shfl_up(incl, off, kWave);
+        if (lane >= off) incl += v;
     }
-    const uint32_t base = st.part_sums[tid] - run;
+    if (lane == kWave - 1) st.part_sums[wv] = incl;
+    __syncthreads();
+    uint32_t base = incl - run;
+    for (uint32_t w = 0; w < wv; ++w) base += st.part_sums[w];
     for (uint32_t s = s0; s < s1; ++s) st.pre[s + 1] += base;
     if (tid == 0) st.pre[0] = 0;
     __syncthreads();
