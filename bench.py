@@ -108,13 +108,19 @@ class AttnBench:
         b, d = self.batches[i % len(self.batches)], self.dev_batches[i % len(self.batches)]
         if "P" not in d:
             d["P"] = self.partition(b)
+            # the chunk partition from the same lengths (non-zero only for batches
+            # without decode rows), unless a fixed or library partition is asked for
+            d["CP"] = 0 if PARTITION else self.K.ragged_chunk_partition_size(
+                self.ctx, q_lens=b.q_lens, context_lens=b.context_lens, num_heads=b.num_heads,
+                num_kv_heads=b.num_kv_heads, head_dim=b.head_dim, block_size=b.block_size,
+                max_blocks=b.max_blocks, kv_dtype=self.kv_dtype, num_blocks=self.num_blocks)
         self.K.ragged_paged_attention(
             self.ctx, q=d["q"], k_pool=self.k, v_pool=self.v, k_scales=self.ks, v_scales=self.vs,
             block_tables=d["tables"], cu_seqlens=d["cu"], context_lens=d["lens"], out=d["out"],
             num_heads=b.num_heads, num_kv_heads=b.num_kv_heads, head_dim=b.head_dim,
             block_size=b.block_size, scale=b.scale, kv_dtype=self.kv_dtype,
             num_blocks=self.num_blocks, max_q_len=int(b.q_lens.max()),
-            pool_layout=POOL_LAYOUT, partition_size=d["P"])
+            pool_layout=POOL_LAYOUT, partition_size=d["P"], chunk_partition_size=d["CP"])
 
     def run(self, steps, warmup):
         torch = self.torch

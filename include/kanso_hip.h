@@ -120,6 +120,11 @@ typedef struct {
                                 from the shape; else a multiple of 32 in
                                 [32, min(992, 62 * block_size)]
                                 (kanso_ragged_partition_size picks one)           */
+    uint32_t chunk_partition_size; /* split-K partition of the rows of sequences with
+                                more than one query row (matrix-core chunk items):
+                                0 = max(partition, 512, within 62 blocks); else a
+                                multiple of 32 in [32, min(992, 62 * block_size)]
+                                (kanso_ragged_chunk_partition_size picks one)     */
 } kanso_ragged_attention_params;
 
 /* One planned sequence of a step, as Engine::step plans it (src/engine.rs:221-226). */
@@ -186,6 +191,16 @@ int kanso_paged_attention_v2(kanso_ctx* ctx, const kanso_paged_attention_params*
  * let the library choose) for unusable arguments. Host-only; launches nothing. */
 uint32_t kanso_ragged_partition_size(const kanso_ctx* ctx, const kanso_ragged_attention_params* p,
                                      const uint32_t* q_lens, const uint32_t* context_lens);
+
+/* The chunk partition for chunk_partition_size, from the same host-side lengths.
+ * A batch with a decode row returns 0 (chunk items keep long partitions, so they
+ * hold few of the CU slots the decode waves stream in). A batch of multi-row
+ * sequences only (prefill chunks, speculative verify rows) returns the smallest
+ * multiple of 32 (at least 64) for which the chunk items fit the resident
+ * workgroups in one pass: shorter items, run side by side. No counterpart in the
+ * reference. Returns 0 for unusable arguments. Host-only; launches nothing. */
+uint32_t kanso_ragged_chunk_partition_size(const kanso_ctx* ctx, const kanso_ragged_attention_params* p,
+                                           const uint32_t* q_lens, const uint32_t* context_lens);
 
 int kanso_ragged_paged_attention(kanso_ctx* ctx, const kanso_ragged_attention_params* p,
                                  const float* q, const void* k_pool, const void* v_pool,

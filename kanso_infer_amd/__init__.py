@@ -37,7 +37,7 @@ __all__ = [
     "EngineError", "Context", "PagedAttentionParams", "paged_attention_num_partitions",
     "validate_paged_attention_params", "gpu_paged_attention_v2", "paged_attention_v2",
     "ragged_paged_attention", "pack_step", "kv_append", "kv_reset_blocks", "gemv_q8_0",
-    "gemv_q4_k", "KANSO_KV_F32", "KANSO_KV_INT8", "KANSO_KV_Q8_0", "KANSO_KV_FP8", "ragged_partition_size", "q8_0_packed_bytes",
+    "gemv_q4_k", "KANSO_KV_F32", "KANSO_KV_INT8", "KANSO_KV_Q8_0", "KANSO_KV_FP8", "ragged_partition_size", "ragged_chunk_partition_size", "q8_0_packed_bytes",
     "q8_0_pack", "gemm_q8_0", "gemm_q8_0_residual", "embed_q8_0", "qkv_rope_append",
     "gate_up_swiglu", "lm_head_argmax",
 ]
@@ -205,6 +205,7 @@ def ragged_paged_attention(ctx: Context, *, q: torch.Tensor, k_pool: torch.Tenso
                            k_scales: torch.Tensor | None = None,
                            v_scales: torch.Tensor | None = None, num_blocks: int = 0,
                            max_q_len: int = 0, pool_layout: int = 0, partition_size: int = 0,
+                           chunk_partition_size: int = 0,
                            stream: torch.cuda.Stream | None = None) -> None:
     """Mixed prefill + decode attention over the paged pool (kanso_ragged_paged_attention)."""
     num_seqs = cu_seqlens.numel() - 1
@@ -212,11 +213,21 @@ def ragged_paged_attention(ctx: Context, *, q: torch.Tensor, k_pool: torch.Tenso
     total_q = q.numel() // (num_heads * head_dim)
     p = RaggedAttentionParamsC(num_seqs, num_heads, num_kv_heads, head_dim, block_size, max_blocks,
                                scale, total_q, kv_dtype, num_blocks, max_q_len, pool_layout,
-                               partition_size)
+                               partition_size, chunk_partition_size)
     _check(ctx._lib.kanso_ragged_paged_attention(
         ctx.handle, C.byref(p), _ptr(q), _ptr(k_pool), _ptr(v_pool), _ptr(k_scales),
         _ptr(v_scales), _ptr(block_tables), _ptr(cu_seqlens), _ptr(context_lens), _ptr(out),
         _stream(stream)))
+
+
+def _lengths_call(fn, q_lens, context_lens, num_heads, num_kv_heads, head_dim, block_size,
+                  max_blocks, kv_dtype, num_blocks, ctx) -> int:
+    ql = np.ascontiguousarray(np.asarray(q_lens, dtype=np.uint32))
+    cl = np.ascontiguousarray(np.asarray(context_lens, dtype=np.uint32))
+    p = RaggedAttentionParamsC(ql.size, num_heads, num_kv_heads, head_dim, block_size, max_blocks,
+                               1.0, int(ql.sum()), kv_dtype, num_blocks, int(ql.max(initial=0)), 0, 0, 0)
+    return int(fn(ctx.handle, C.byref(p), ql.ctypes.data_as(C.c_void_p),
+                  cl.ctypes.data_as(C.c_void_p)))
 
 
 def ragged_partition_size(ctx: Context, *, q_lens, context_lens, num_heads: int,
@@ -224,13 +235,19 @@ def ragged_partition_size(ctx: Context, *, q_lens, context_lens, num_heads: int,
                           kv_dtype: int = KANSO_KV_F32, num_blocks: int = 0) -> int:
     """The split-K partition for ragged_paged_attention from the step's host-side
     query / context lengths (kanso_ragged_partition_size); 0 = the library's choice."""
-    ql = np.ascontiguousarray(np.asarray(q_lens, dtype=np.uint32))
-    cl = np.ascontiguousarray(np.asarray(context_lens, dtype=np.uint32))
-    p = RaggedAttentionParamsC(ql.size, num_heads, num_kv_heads, head_dim, block_size, max_blocks,
-                               1.0, int(ql.sum()), kv_dtype, num_blocks, int(ql.max(initial=0)), 0, 0)
-    return int(ctx._lib.kanso_ragged_partition_size(ctx.handle, C.byref(p),
-                                                    ql.ctypes.data_as(C.c_void_p),
-                                                    cl.ctypes.data_as(C.c_void_p)))
+    return _lengths_call(ctx._lib.kanso_ragged_partition_size, q_lens, context_lens, num_heads,
+                         num_kv_heads, head_dim, block_size, max_blocks, kv_dtype, num_blocks, ctx)
+
+
+def ragged_chunk_partition_size(ctx: Context, *, q_lens, context_lens, num_heads: int,
+                                num_kv_heads: int, head_dim: int, block_size: int,
+                                max_blocks: int, kv_dtype: int = KANSO_KV_F32,
+                                num_blocks: int = 0) -> int:
+    """The chunk partition (kanso_ragged_chunk_partition_size): non-zero only for
+    batches whose sequences all have more than one query row; 0 = automatic."""
+    return _lengths_call(ctx._lib.kanso_ragged_chunk_partition_size, q_lens, context_lens,
+                         num_heads, num_kv_heads, head_dim, block_size, max_blocks, kv_dtype,
+                         num_blocks, ctx)
 
 
 # ---------------------------------------------------------------- packing

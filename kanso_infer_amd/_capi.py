@@ -66,6 +66,7 @@ class RaggedAttentionParamsC(C.Structure):
         ("max_q_len", C.c_uint32),
         ("pool_layout", C.c_uint32),
         ("partition_size", C.c_uint32),
+        ("chunk_partition_size", C.c_uint32),
     ]
 
 
@@ -146,6 +147,7 @@ SIGNATURES: dict[str, tuple] = {
     "kanso_validate_paged_attention_params": (_I, [C.POINTER(PagedAttentionParamsC)]),
     "kanso_paged_attention_v2": (_I, [_P, C.POINTER(PagedAttentionParamsC), _P, _P, _P, _P, _P, _P, _P]),
     "kanso_ragged_partition_size": (C.c_uint32, [_P, C.POINTER(RaggedAttentionParamsC), _P, _P]),
+    "kanso_ragged_chunk_partition_size": (C.c_uint32, [_P, C.POINTER(RaggedAttentionParamsC), _P, _P]),
     "kanso_ragged_paged_attention": (
         _I, [_P, C.POINTER(RaggedAttentionParamsC), _P, _P, _P, _P, _P, _P, _P, _P, _P, _P]),
     "kanso_pack_step": (_I, [_P, _P, _U, _P, _P, _U, _U, _U, C.POINTER(PackedStepC), _P]),

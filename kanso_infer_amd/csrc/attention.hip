@@ -1455,6 +1455,13 @@ bool pool_fits_rsrc(const kanso_ragged_attention_params* p) {
     return p->num_blocks != 0 && rows * p->head_dim * elem < (1ull << 32);
 }
 
+// Whether a batch takes the kernel with the MFMA chunk path: some sequence has more
+// than one query row, head_dim 64, GQA groups up to 4, the pool within buffer range.
+bool use_mfma_path(const kanso_ragged_attention_params* p, uint32_t max_q) {
+    const uint32_t G = p->num_heads / p->num_kv_heads;
+    return p->head_dim == 64 && G <= 4 && max_q > 1 && pool_fits_rsrc(p);
+}
+
 // Chunk items are 64 rows wide: their partition stays long (at least 512 keys, within
 // 62 table entries), so small decode partitions do not multiply them.
 uint32_t chunk_partition(uint32_t P, uint32_t block_size) {
@@ -1532,17 +1539,21 @@ int run_ragged(kanso_ctx* ctx, const kanso_ragged_attention_params* p, const flo
     }
     const uint32_t capacity = static_cast<uint32_t>(cap64);
     const uint32_t T = p->total_q;
-    if (p->partition_size && (p->partition_size < 32 || p->partition_size > 992 ||
-                              p->partition_size % 32 != 0 ||
-                              p->partition_size > 62u * p->block_size)) {
-        set_error("%s: partition_size %u must be 0 or a multiple of 32 in [32, min(992, 62 * block_size)]",
-                  who, p->partition_size);
+    const auto bad_partition = [&](uint32_t v) {
+        return v && (v < 32 || v > 992 || v % 32 != 0 || v > 62u * p->block_size);
+    };
+    if (bad_partition(p->partition_size) || bad_partition(p->chunk_partition_size)) {
+        set_error("%s: partition_size %u / chunk_partition_size %u must be 0 or a multiple of 32 in "
+                  "[32, min(992, 62 * block_size)]",
+                  who, p->partition_size, p->chunk_partition_size);
         return KANSO_E_INVALID_SHAPE;
     }
     const uint32_t P = p->partition_size ? p->partition_size
                                          : choose_partition(ctx, S, HKV, capacity, p->block_size,
                                                             p->kv_dtype == KANSO_KV_F32 ? 4 : 1);
-    const uint32_t max_parts = (capacity + P - 1) / P;
+    const uint32_t CP = p->chunk_partition_size ? p->chunk_partition_size : chunk_partition(P, p->block_size);
+    // partials are indexed by partition: the shorter of the two partitions sets the count
+    const uint32_t max_parts = (capacity + std::min(P, CP) - 1) / std::min(P, CP);
     const uint64_t partial_elems = static_cast<uint64_t>(T) * H * max_parts * D;
     if (partial_elems > (1ull << 31)) {
         set_error("%s: %llu partial elements exceed the scratch limit", who,
@@ -1582,7 +1593,7 @@ int run_ragged(kanso_ctx* ctx, const kanso_ragged_attention_params* p, const flo
     a.max_blocks = p->max_num_blocks_per_seq;
     a.num_blocks = p->num_blocks ? p->num_blocks : 0xffffffffu;
     a.part_size = P;
-    a.chunk_part = chunk_partition(P, p->block_size);
+    a.chunk_part = CP;
     a.max_parts = max_parts;
     a.total_q = T;
     a.capacity = capacity;
@@ -1600,7 +1611,7 @@ int run_ragged(kanso_ctx* ctx, const kanso_ragged_attention_params* p, const flo
     // MFMA chunk items exist only when some sequence has more than one query row; the
     // chunk kernel reads the pool through buffer resources (pool below 4 GiB).
     const uint32_t max_q = p->max_q_len ? p->max_q_len : T;
-    a.use_mfma = (D == 64 && G <= 4 && max_q > 1 && buf) ? 1u : 0u;
+    a.use_mfma = use_mfma_path(p, max_q) ? 1u : 0u;
     a.head_major = p->pool_layout == KANSO_POOL_HEAD_MAJOR ? 1u : 0u;
     Stage1Fn main_fn = pick_main_kv(p->kv_dtype, D, G, buf, a.use_mfma != 0);
     const bool wide_merge = max_parts > 16;
@@ -1653,7 +1664,7 @@ uint32_t kanso_ragged_partition_size(const kanso_ctx* ctx, const kanso_ragged_at
     if (!ctx || !p || !q_lens || !context_lens || p->num_seqs == 0 || p->num_kv_heads == 0 ||
         p->num_heads % p->num_kv_heads != 0 || p->block_size == 0)
         return 0;
-    const uint32_t S = p->num_seqs, HKV = p->num_kv_heads, G = p->num_heads / HKV;
+    const uint32_t S = p->num_seqs, HKV = p->num_kv_heads;
     const uint64_t cap64 = static_cast<uint64_t>(p->max_num_blocks_per_seq) * p->block_size;
     const uint32_t cap = static_cast<uint32_t>(std::min<uint64_t>(cap64, 1u << 30));
     uint64_t T = 0;
@@ -1663,7 +1674,7 @@ uint32_t kanso_ragged_partition_size(const kanso_ctx* ctx, const kanso_ragged_at
         max_q = std::max(max_q, q_lens[s]);
     }
     if (T == 0 || cap == 0) return 0;
-    const bool mfma = p->head_dim == 64 && G <= 4 && max_q > 1 && pool_fits_rsrc(p);
+    const bool mfma = use_mfma_path(p, max_q);
     const uint32_t p_max = std::max(32u, std::min(512u, 62u * p->block_size / 32u * 32u));
     uint32_t best = p_max;
     for (uint32_t P = p_max; P >= 32; P -= 32) {
@@ -1687,6 +1698,40 @@ uint32_t kanso_ragged_partition_size(const kanso_ctx* ctx, const kanso_ragged_at
         best = P;
     }
     return best;
+}
+
+uint32_t kanso_ragged_chunk_partition_size(const kanso_ctx* ctx, const kanso_ragged_attention_params* p,
+                                           const uint32_t* q_lens, const uint32_t* context_lens) {
+    // Only batches without decode rows shorten their chunk partitions: the chunk
+    // items then have the machine to themselves, and an item's tiles run one after
+    // another (latency-bound), so more, shorter items finish sooner. Measured on
+    // config 2's four prefill chunks alone: 44.9 us at 512 keys, 28.8 at 96-128.
+    if (!ctx || !p || !q_lens || !context_lens || p->num_seqs == 0 || p->num_kv_heads == 0 ||
+        p->num_heads % p->num_kv_heads != 0 || p->block_size == 0)
+        return 0;
+    const uint32_t S = p->num_seqs, HKV = p->num_kv_heads;
+    const uint64_t cap64 = static_cast<uint64_t>(p->max_num_blocks_per_seq) * p->block_size;
+    const uint32_t cap = static_cast<uint32_t>(std::min<uint64_t>(cap64, 1u << 30));
+    uint64_t T = 0;
+    uint32_t max_q = 0;
+    for (uint32_t s = 0; s < S; ++s) {
+        if (q_lens[s] == 1) return 0;
+        T += q_lens[s];
+        max_q = std::max(max_q, q_lens[s]);
+    }
+    if (T == 0 || cap == 0 || !use_mfma_path(p, max_q)) return 0;
+    const uint32_t p_max = std::max(32u, std::min(512u, 62u * p->block_size / 32u * 32u));
+    const uint64_t resident = std::min<uint64_t>(main_grid(ctx, T, 1, HKV, true), 2ull * ctx->num_cus);
+    for (uint32_t cp = std::min(64u, p_max); cp <= p_max; cp += 32) {
+        uint64_t n_chunk = 0;
+        for (uint32_t s = 0; s < S; ++s) {
+            const uint32_t ql = q_lens[s], c = context_lens[s];
+            for (uint32_t i0 = 0; i0 < ql; i0 += 64)
+                n_chunk += (host_row_limit(c, ql, std::min(i0 + 64, ql) - 1, cap) + cp - 1) / cp * HKV;
+        }
+        if (n_chunk <= resident) return cp;
+    }
+    return p_max;
 }
 
 int kanso_validate_paged_attention_params(const kanso_paged_attention_params* p) {

@@ -337,6 +337,7 @@ int model_forward(kanso_model* m, const HostStep& step, float* logits, uint32_t*
             cl[i] = step.plan[i].start_pos + step.plan[i].q_len;
         }
         ap.partition_size = kanso_ragged_partition_size(m->ctx, &ap, ql.data(), cl.data());
+        ap.chunk_partition_size = kanso_ragged_chunk_partition_size(m->ctx, &ap, ql.data(), cl.data());
     }
     const uint32_t qd = c.num_heads * 64;
     for (uint32_t l = 0; l < c.num_layers; ++l) {

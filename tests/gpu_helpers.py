@@ -56,7 +56,8 @@ def fill_pool(batch, kv_dtype: int, seed: int):
     return kp, vp, ks, vs
 
 
-def run_ragged_gpu(ctx, batch, q, kp, vp, ks=None, vs=None, kv_dtype=0, partition_size=0):
+def run_ragged_gpu(ctx, batch, q, kp, vp, ks=None, vs=None, kv_dtype=0, partition_size=0,
+                   chunk_partition_size=0):
     out = torch.empty(batch.total_q * batch.num_heads * batch.head_dim, dtype=torch.float32,
                       device="cuda:0")
     K.ragged_paged_attention(
@@ -67,7 +68,7 @@ def run_ragged_gpu(ctx, batch, q, kp, vp, ks=None, vs=None, kv_dtype=0, partitio
         num_heads=batch.num_heads, num_kv_heads=batch.num_kv_heads, head_dim=batch.head_dim,
         block_size=batch.block_size, scale=batch.scale, kv_dtype=kv_dtype,
         num_blocks=batch.num_blocks, max_q_len=int(batch.q_lens.max()),
-        partition_size=partition_size)
+        partition_size=partition_size, chunk_partition_size=chunk_partition_size)
     ctx.check_device_status()
     return host(out)
 

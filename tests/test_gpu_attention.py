@@ -132,6 +132,54 @@ def test_rejects_bad_partition_size(ctx):
             run_ragged_gpu(ctx, b, q, kp, vp, partition_size=bad)
 
 
+@pytest.mark.parametrize("cp", [32, 64, 96, 160])
+@pytest.mark.parametrize("P", [0, 64])
+@pytest.mark.parametrize("kv_dtype", [oracle.KV_F32, oracle.KV_Q8_0])
+@pytest.mark.parametrize("decodes", [5, 0])
+def test_explicit_chunk_partition_size(ctx, cp, P, kv_dtype, decodes):
+    """A caller-chosen chunk partition (shorter or longer than the decode one) gives
+    the oracle's result, with and without decode rows in the batch."""
+    b = workloads.small_mixed(16, num_decodes=decodes, num_chunks=3, chunk_max=70)
+    kp, vp, ks, vs = fill_pool(b, kv_dtype, 16)
+    q = np.random.default_rng(62).standard_normal(
+        b.total_q * b.num_heads * b.head_dim).astype(np.float32)
+    got = run_ragged_gpu(ctx, b, q, kp, vp, ks, vs, kv_dtype, partition_size=P,
+                         chunk_partition_size=cp)
+    want = run_ragged_oracle(b, q, kp, vp, ks, vs, kv_dtype)
+    assert_close(got, want, what=f"{b.label} P {P} CP {cp} kv {kv_dtype}")
+
+
+def test_rejects_bad_chunk_partition_size(ctx):
+    b = workloads.small_mixed(12)
+    kp, vp, ks, vs = fill_pool(b, oracle.KV_F32, 12)
+    q = np.zeros(b.total_q * b.num_heads * b.head_dim, np.float32)
+    for bad in (48, 16, 1024, 100):
+        with pytest.raises(K.EngineError):
+            run_ragged_gpu(ctx, b, q, kp, vp, chunk_partition_size=bad)
+
+
+@pytest.mark.parametrize("decodes", [0, 4])
+def test_chunk_partition_from_host_lengths(ctx, decodes):
+    """kanso_ragged_chunk_partition_size: 0 when the batch has a decode row, else a
+    multiple of 32 in [64, 512]; the call with it gives the oracle's result."""
+    b = workloads.small_mixed(17, num_decodes=decodes, num_chunks=4, chunk_max=90)
+    args = dict(q_lens=b.q_lens, context_lens=b.context_lens, num_heads=b.num_heads,
+                num_kv_heads=b.num_kv_heads, head_dim=b.head_dim, block_size=b.block_size,
+                max_blocks=b.max_blocks, num_blocks=b.num_blocks)
+    cp = K.ragged_chunk_partition_size(ctx, **args)
+    if decodes:
+        assert cp == 0
+    else:
+        assert 64 <= cp <= 512 and cp % 32 == 0
+    P = K.ragged_partition_size(ctx, **args)
+    kp, vp, ks, vs = fill_pool(b, oracle.KV_F32, 18)
+    q = np.random.default_rng(19).standard_normal(
+        b.total_q * b.num_heads * b.head_dim).astype(np.float32)
+    got = run_ragged_gpu(ctx, b, q, kp, vp, partition_size=P, chunk_partition_size=cp)
+    want = run_ragged_oracle(b, q, kp, vp)
+    assert_close(got, want, what=f"{b.label} P {P} CP {cp}")
+
+
 @pytest.mark.parametrize("variant", ["config1", "config2_small_pool", "config3_int8",
                                      "config3_q8_0", "config3_fp8"])
 def test_baseline_shapes(ctx, variant):
