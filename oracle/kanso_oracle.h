@@ -144,12 +144,16 @@ uint64_t oracle_fnv1a_64(const uint32_t* tokens, size_t n);
 
 /* ---- batched llama forward (config 5), kanso_oracle_model.cpp ------------ */
 
+/* weight_format: 0 = GGUF Q8_0 matrices; 1 = F32 row-major [rows][in] matrices and
+ * embedding (the F32 LinearWeight of the reference's mock models, src/model.rs:509-587,
+ * computed as x @ W^T in f32 with a sequential sum). */
 typedef struct {
     uint32_t hidden, num_heads, num_kv_heads, head_dim, num_layers, intermediate, vocab;
     float eps, rope_theta;
+    uint32_t weight_format;
 } oracle_model_config;
 
-/* GGUF Q8_0 matrices ([rows][in/32] x 34 B) and f32 norm weights; per-layer
+/* Matrices in the config's weight_format and f32 norm weights; per-layer
  * fields are arrays of num_layers pointers. lm_head may alias embed (tied). */
 typedef struct {
     const void* embed;

@@ -26,12 +26,35 @@ int oracle_forward_batch_rows(const oracle_model_config* cfg, const oracle_model
                               int all_rows, float* logits, int nthreads) {
     const uint32_t Hd = cfg->hidden, H = cfg->num_heads, HKV = cfg->num_kv_heads;
     const uint32_t D = cfg->head_dim, I = cfg->intermediate, V = cfg->vocab;
-    if (T == 0 || S == 0 || H % HKV != 0 || Hd % 32 != 0 || I % 32 != 0 || D % 2 != 0) return -1;
+    const bool f32w = cfg->weight_format == 1;
+    if (cfg->weight_format > 1) return -1;
+    if (T == 0 || S == 0 || H % HKV != 0 || D % 2 != 0) return -1;
+    if (!f32w && (Hd % 32 != 0 || I % 32 != 0)) return -1;
     if (static_cast<uint32_t>(cu_seqlens[S]) != T) return -1;
-    // Model::embed (src/model.rs:425-431): dequantized table rows.
+    // y[t] = x[t] @ W^T for every token (LinearWeight::forward, src/weights.rs:43-45)
+    const auto linear = [&](const void* m, const float* x, float* y, uint32_t rows, uint32_t cols) {
+        if (!f32w) {
+            oracle_gemv_q8_0(m, x, y, rows, cols, T, nthreads);
+            return;
+        }
+        const float* wm = static_cast<const float*>(m);
+        for (uint32_t t = 0; t < T; ++t)
+            for (uint32_t r = 0; r < rows; ++r) {
+                float acc = 0.f;
+                for (uint32_t c = 0; c < cols; ++c)
+                    acc += x[static_cast<size_t>(t) * cols + c] * wm[static_cast<size_t>(r) * cols + c];
+                y[static_cast<size_t>(t) * rows + r] = acc;
+            }
+    };
+    // Model::embed (src/model.rs:425-431): table rows (dequantized for Q8_0).
     std::vector<float> hidden(static_cast<size_t>(T) * Hd);
     for (uint32_t t = 0; t < T; ++t) {
         if (tokens[t] >= V) return -1;
+        if (f32w) {
+            std::memcpy(&hidden[static_cast<size_t>(t) * Hd],
+                        static_cast<const float*>(w->embed) + static_cast<size_t>(tokens[t]) * Hd, Hd * sizeof(float));
+            continue;
+        }
         const uint8_t* blocks = static_cast<const uint8_t*>(w->embed) + static_cast<size_t>(tokens[t]) * (Hd / 32) * 34;
         oracle_dequant_row_q8_0(blocks, Hd, &hidden[static_cast<size_t>(t) * Hd]);
     }
@@ -66,9 +89,9 @@ int oracle_forward_batch_rows(const oracle_model_config* cfg, const oracle_model
 
     for (uint32_t l = 0; l < cfg->num_layers; ++l) {
         oracle_rmsnorm(hidden.data(), w->attn_norm[l], normed.data(), T, Hd, cfg->eps);
-        oracle_gemv_q8_0(w->wq[l], normed.data(), q.data(), H * D, Hd, T, nthreads);
-        oracle_gemv_q8_0(w->wk[l], normed.data(), k.data(), HKV * D, Hd, T, nthreads);
-        oracle_gemv_q8_0(w->wv[l], normed.data(), v.data(), HKV * D, Hd, T, nthreads);
+        linear(w->wq[l], normed.data(), q.data(), H * D, Hd);
+        linear(w->wk[l], normed.data(), k.data(), HKV * D, Hd);
+        linear(w->wv[l], normed.data(), v.data(), HKV * D, Hd);
         oracle_rope_apply(q.data(), T, H, D, positions, cos_t.data(), sin_t.data());
         oracle_rope_apply(k.data(), T, HKV, D, positions, cos_t.data(), sin_t.data());
         // write_kv_slots (src/model.rs:1673; storage.rs:219-254)
@@ -79,14 +102,14 @@ int oracle_forward_batch_rows(const oracle_model_config* cfg, const oracle_model
                                     cu_seqlens, context_lens, &ap, attn.data(), nthreads) != 0)
             return -1;
         // hidden = hidden + attn_output(attn) (src/model.rs:1716-1717)
-        oracle_gemv_q8_0(w->wo[l], attn.data(), proj.data(), Hd, H * D, T, nthreads);
+        linear(w->wo[l], attn.data(), proj.data(), Hd, H * D);
         for (size_t i = 0; i < hidden.size(); ++i) hidden[i] = hidden[i] + proj[i];
         // ffn: rmsnorm, gate/up, silu * up, down, residual (src/model.rs:1719-1721, 367-380)
         oracle_rmsnorm(hidden.data(), w->ffn_norm[l], normed.data(), T, Hd, cfg->eps);
-        oracle_gemv_q8_0(w->w_gate[l], normed.data(), gate.data(), I, Hd, T, nthreads);
-        oracle_gemv_q8_0(w->w_up[l], normed.data(), up.data(), I, Hd, T, nthreads);
+        linear(w->w_gate[l], normed.data(), gate.data(), I, Hd);
+        linear(w->w_up[l], normed.data(), up.data(), I, Hd);
         oracle_silu_mul(gate.data(), up.data(), act.data(), T * I);
-        oracle_gemv_q8_0(w->w_down[l], act.data(), proj.data(), Hd, I, T, nthreads);
+        linear(w->w_down[l], act.data(), proj.data(), Hd, I);
         for (size_t i = 0; i < hidden.size(); ++i) hidden[i] = hidden[i] + proj[i];
     }
     // final norm, then lm_head on every row (RowSelection::EveryToken) or on each
@@ -100,7 +123,18 @@ int oracle_forward_batch_rows(const oracle_model_config* cfg, const oracle_model
     }
     std::vector<float> last_normed(last.size());
     oracle_rmsnorm(last.data(), w->final_norm, last_normed.data(), R, Hd, cfg->eps);
-    oracle_gemv_q8_0(w->lm_head, last_normed.data(), logits, V, Hd, R, nthreads);
+    if (f32w) {
+        const float* wm = static_cast<const float*>(w->lm_head);
+        for (uint32_t r = 0; r < R; ++r)
+            for (uint32_t o = 0; o < V; ++o) {
+                float acc = 0.f;
+                for (uint32_t c = 0; c < Hd; ++c)
+                    acc += last_normed[static_cast<size_t>(r) * Hd + c] * wm[static_cast<size_t>(o) * Hd + c];
+                logits[static_cast<size_t>(r) * V + o] = acc;
+            }
+    } else {
+        oracle_gemv_q8_0(w->lm_head, last_normed.data(), logits, V, Hd, R, nthreads);
+    }
     return 0;
 }
 

@@ -327,7 +327,7 @@ def available() -> bool:
 class ModelConfigC(C.Structure):
     _fields_ = [(n, C.c_uint32) for n in ("hidden", "num_heads", "num_kv_heads", "head_dim",
                                           "num_layers", "intermediate", "vocab")] + [
-        ("eps", C.c_float), ("rope_theta", C.c_float)]
+        ("eps", C.c_float), ("rope_theta", C.c_float), ("weight_format", C.c_uint32)]
 
 
 class ModelWeightsC(C.Structure):
@@ -345,7 +345,7 @@ def forward_batch(cfg: dict, weights: dict, k_pools, v_pools, num_blocks, block_
     L = cfg["num_layers"]
     c = ModelConfigC(cfg["hidden"], cfg["num_heads"], cfg["num_kv_heads"], cfg["head_dim"], L,
                      cfg["intermediate"], cfg["vocab"], cfg.get("eps", 1e-5),
-                     cfg.get("rope_theta", 10000.0))
+                     cfg.get("rope_theta", 10000.0), cfg.get("weight_format", 0))
     keep = []
 
     def arr(name):

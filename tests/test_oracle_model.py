@@ -84,6 +84,42 @@ def test_all_rows(weights):
     np.testing.assert_allclose(cont, every[cu[2] + 4:cu[3]], atol=1e-5, rtol=1e-5)
 
 
+def test_chacha_block_known_answer():
+    """The ChaCha block function of the mock-weight restatement against the published
+    ChaCha20 keystream for the all-zero key and nonce (blocks 0 and 1)."""
+    import mock_rng
+    want = ("76b8e0ada0f13d90405d6ae55386bd28bdd219b8a08ded1aa836efcc8b770dc7"
+            "da41597c5157488d7724e03fb8d84a376a43b8f41518a11cc387b669b2ee6586",
+            "9f07e7be5551387a98ba977c732d080dcb0f29a048e3656912c6533e32ee7aed"
+            "29b721769ce64e43d57133b074d839d531ed1f28510afb45ace10a1f4b794d6f")
+    for counter, hexs in enumerate(want):
+        words = mock_rng.chacha_block([0] * 8, counter, 0, rounds=20)
+        assert b"".join(x.to_bytes(4, "little") for x in words).hex() == hexs
+
+
+def test_golden_logits_fixture():
+    """The reference's own golden fixture (tests/fixtures/golden_logits.json of the
+    reference, copied as tests/golden/golden_logits.json): last-token logits of a full
+    prefill of three prompts on Model::create_mock_tiny(16, 4, 2, 2, 50)
+    (tests/test_golden_logits.rs:23-91). The mock's weights come from the restated
+    rand 0.9 StdRng stream (oracle/mock_rng.py) and the forward is the oracle's, with
+    F32 weights; tolerance and top-5 check as the reference's test."""
+    import json
+    from pathlib import Path
+    import mock_rng
+    cfg, w = mock_rng.mock_tiny_weights(16, 4, 2, 2, 50)
+    gold = json.loads((Path(__file__).parent / "golden" / "golden_logits.json").read_text())
+    assert len(gold) == 3
+    for key, exp in gold.items():
+        toks = [int(t) for t in key.split(",")]
+        got = OracleModel(cfg, w, 4, 16, nthreads=1).logits(plan_of([(toks, 0, [1, 2])], 16))[0]
+        exp = np.asarray(exp, np.float32)
+        assert got.shape == exp.shape
+        assert np.abs(got - exp).max() <= 1e-4, key
+        top = lambda v: list(np.argsort(-v, kind="stable")[:5])
+        assert top(got) == top(exp), key
+
+
 def _f64_forward(cfg, w, tokens):
     """One sequence from position 0, every op in float64 numpy (no paging)."""
     h, H, KV, D = cfg["hidden"], cfg["num_heads"], cfg["num_kv_heads"], cfg["head_dim"]
