@@ -177,3 +177,29 @@ def test_cancel_and_drain():
     while cpp.has_unfinished_requests():
         assert_same_step(cpp, ref)
     assert cpp.drain_finished() == ref.drain_finished() == 2
+
+
+def test_continuous_batching_staggered_arrival():
+    """tests/test_continuous_batching.rs:1-40: max_running 2, 20 blocks of 4, no
+    budget (Engine::new, src/engine.rs:36-43). A request arriving mid-generation is
+    admitted beside the running one, and every block returns to the pool."""
+    cpp, ref = pair(2, 20, 4, (1 << 31) - 1)
+    id1 = cpp.add_request([1, 2], 3)
+    ref.add_request([1, 2], 3)
+    assert cpp.stats()["waiting"] == 1 and cpp.stats()["running"] == 0
+    out1 = assert_same_step(cpp, ref)
+    assert len(out1) == 1 and out1[0].request_id == id1
+    assert cpp.stats()["running"] == 1
+    cpp.add_request([3, 4], 2)
+    ref.add_request([3, 4], 2)
+    assert cpp.stats()["waiting"] == 1
+    out2 = assert_same_step(cpp, ref)
+    assert len(out2) == 2 and cpp.stats()["running"] == 2
+    steps = 0
+    while cpp.has_unfinished_requests() and steps < 10:
+        assert_same_step(cpp, ref)
+        steps += 1
+    assert not cpp.has_unfinished_requests()
+    st = cpp.stats()
+    assert st["running"] == 0 and st["waiting"] == 0
+    assert cpp.free_blocks_count() == 20 == ref.block_pool.free_blocks_count()
