@@ -121,8 +121,8 @@ __device__ uint32_t seq_items(const AttnArgs& a, int32_t ql, int32_t ctx, bool c
     return n;
 }
 
-// Fills the workgroup's SeqTable (all threads participate). Workgroup 0 of the
-// decode kernel also raises the input-validation flags.
+// Fills the workgroup's SeqTable (all threads participate). Workgroup 0 also
+// raises the input-validation flags.
 template <bool CHUNK>
 __device__ void load_seq_table(const AttnArgs& a, SeqTable& st) {
     const uint32_t tid = threadIdx.x, S = a.num_seqs;
@@ -143,7 +143,9 @@ __device__ void load_seq_table(const AttnArgs& a, SeqTable& st) {
         run += chunk == CHUNK ? seq_items(a, ql, ctx, chunk, CHUNK ? a.chunk_part : a.part_size) : 0u;
         st.pre[s + 1] = run;  // inclusive within this thread's segment
     }
-    if (!CHUNK && flags && blockIdx.x == 0) raise_status(a.status, flags);
+    // workgroup 0 reports: it loads the chunk table when the batch has chunk items
+    // (and may then stop before the decode table), else the decode table
+    if (flags && blockIdx.x == 0 && (CHUNK || !a.use_mfma)) raise_status(a.status, flags);
     // exclusive prefix of the per-thread totals: a shuffle scan inside each wave,
     // then the wave totals through LDS (one barrier instead of two per step)
     const uint32_t lane = tid & (kWave - 1), wv = tid / kWave;
@@ -1227,10 +1229,11 @@ __device__ void chunk_block(const AttnArgs& a, const SeqTable& st, const PoolRsr
 // ---------------------------------------------------------------- kernels
 
 // Rows with no key (an empty context, or more query rows than context) get zeros,
-// cpu_paged_attention's output for an empty context. Grid-stride over sequences.
-__device__ void zero_empty_rows(const AttnArgs& a, const SeqTable& st, uint32_t D) {
-    const uint32_t n_threads = gridDim.x * kThreads;
-    for (uint32_t s = blockIdx.x * kThreads + threadIdx.x; s < a.num_seqs; s += n_threads) {
+// cpu_paged_attention's output for an empty context. Grid-stride over sequences,
+// by the workgroups from first_wg on (the ones that run the decode phase).
+__device__ void zero_empty_rows(const AttnArgs& a, const SeqTable& st, uint32_t D, uint32_t first_wg) {
+    const uint32_t n_threads = (gridDim.x - first_wg) * kThreads;
+    for (uint32_t s = (blockIdx.x - first_wg) * kThreads + threadIdx.x; s < a.num_seqs; s += n_threads) {
         const int32_t ql = st.cu[s + 1] - st.cu[s];
         for (int32_t i = 0; i < ql; ++i)
             if (row_limit(st.ctx[s], ql, i, a.capacity) == 0) {
@@ -1287,7 +1290,7 @@ __global__ __launch_bounds__(kThreads, 2) void attn_main(AttnArgs a) {
         }
     }
     load_seq_table<false>(a, st);
-    zero_empty_rows(a, st, D);
+    zero_empty_rows(a, st, D, n_chunk_wg);
     const int lane = threadIdx.x & (kWave - 1);
     const uint32_t wave = (blockIdx.x - n_chunk_wg) * kWaves + threadIdx.x / kWave;
     const uint32_t n_waves = (gridDim.x - n_chunk_wg) * kWaves;

@@ -95,6 +95,32 @@ def test_device_flags_raise(ctx):
     ctx.check_device_status()  # cleared
 
 
+def test_rows_without_keys_are_zero_in_mixed_batches(ctx):
+    """A query row with no key (more query rows than context) is flagged and written as
+    zeros (cpu_paged_attention's empty-context output), also when the batch has
+    matrix-core chunk items, whose workgroups come first in the grid."""
+    H, HKV, D, bs = 15, 5, 64, 16
+    q_lens = np.array([20, 1, 3])
+    ctx_lens = np.array([100, 50, 2])
+    tables = np.array([[0, 1, 2, 3, 4, 5, 6], [7, 8, 9, 9, 9, 9, 9], [10, 10, 10, 10, 10, 10, 10]],
+                      np.uint32)
+    cu = np.concatenate([[0], np.cumsum(q_lens)]).astype(np.int32)
+    T = int(q_lens.sum())
+    rng = np.random.default_rng(70)
+    pool = dev(rng.standard_normal(16 * bs * HKV * D).astype(np.float32))
+    q = dev(rng.standard_normal(T * H * D).astype(np.float32))
+    out = torch.full((T * H * D,), float("nan"), device="cuda:0")
+    K.ragged_paged_attention(ctx, q=q, k_pool=pool, v_pool=pool, block_tables=dev(tables.ravel()),
+                             cu_seqlens=dev(cu), context_lens=dev(ctx_lens.astype(np.uint32)),
+                             out=out, num_heads=H, num_kv_heads=HKV, head_dim=D, block_size=bs,
+                             scale=0.125, num_blocks=16, max_q_len=20)
+    with pytest.raises(K.EngineError):
+        ctx.check_device_status()
+    got = host(out).reshape(T, H * D)
+    np.testing.assert_array_equal(got[21], np.zeros(H * D, np.float32))  # no key
+    assert np.isfinite(got[:21]).all() and np.isfinite(got[22:]).all()
+
+
 @pytest.mark.parametrize("seed", range(4))
 @pytest.mark.parametrize("kv_dtype", [oracle.KV_F32, oracle.KV_INT8, oracle.KV_Q8_0, oracle.KV_FP8])
 def test_ragged_small(ctx, seed, kv_dtype):
