@@ -574,7 +574,7 @@ struct EpiArgmax {
 // 2560 wide) is requested in one round where the registers allow. Up to 256
 // tokens a workgroup takes 16 of them (MT = 1): at decode sizes more workgroups
 // in flight beat the weight reuse of wider token tiles (re-reads hit L2 / MALL);
-// above, 64 (MT = 4).
+// above, 32 (MT = 2, launch_mt2).
 template <int U, int MT, int NU, bool NORM, class WL, class Epi>
 inline void launch_u(const WL& wl, const XIn& xa, const Epi& epi, uint32_t units, hipStream_t s) {
     const dim3 grid((units + NU - 1) / NU, (xa.T + 16 * MT - 1) / (16 * MT));
@@ -585,7 +585,7 @@ inline void launch_u(const WL& wl, const XIn& xa, const Epi& epi, uint32_t units
 template <int MT, int NU, bool NORM, class WL, class Epi>
 inline void launch_mt(const WL& wl, const XIn& xa, const Epi& epi, uint32_t units, uint32_t nb, hipStream_t s) {
     constexpr int NG = NU * Epi::kGroups;
-    if constexpr (MT == 4)  // 64 tokens of x per block already fill the registers
+    if constexpr (MT >= 2)  // 32-64 tokens of x per block already fill the registers
         launch_u<2, MT, NU, NORM>(wl, xa, epi, units, s);
     else if constexpr (NG >= 8)
         launch_u<2, MT, NU, NORM>(wl, xa, epi, units, s);
@@ -647,10 +647,24 @@ inline void launch_mt1(const WL& wl, const XIn& xa, const Epi& epi, uint32_t uni
         launch_mt<1, 1, NORM>(wl, xa, epi, units, nb, s);
 }
 
+// Above 256 tokens: 32-token tiles and up to two units (four 16-row groups) per
+// workgroup, so each x load feeds 4 groups and each weight load 32 tokens (bytes
+// per output (4 MT + 1.06 NG) / (MT NG): 1.53 at MT = 2, NG = 4 against 2.26 for
+// 64-token tiles of one pair). Four units would halve the x traffic again but need
+// 128 KB of LDS for the partial sums (one workgroup per CU) and measured slower:
+// gate/up at 512 tokens 38.5 us (NU = 2), 52.4 (NU = 4), 60 (64-token tiles).
+template <bool NORM, class WL, class Epi>
+inline void launch_mt2(const WL& wl, const XIn& xa, const Epi& epi, uint32_t units, uint32_t nb, hipStream_t s) {
+    if (pick_nu(units, (xa.T + 31) / 32) >= 2)
+        launch_mt<2, 2, NORM>(wl, xa, epi, units, nb, s);
+    else
+        launch_mt<2, 1, NORM>(wl, xa, epi, units, nb, s);
+}
+
 template <bool NORM, class WL, class Epi>
 inline void launch_norm(const WL& wl, const XIn& xa, const Epi& epi, uint32_t pairs, uint32_t nb, hipStream_t s) {
     if (xa.T > 256)
-        launch_mt<4, 1, NORM>(wl, xa, epi, pairs, nb, s);
+        launch_mt2<NORM>(wl, xa, epi, pairs, nb, s);
     else if constexpr (SingleGroup<Epi>::kOk)
         launch_mt1<NORM>(wl, xa, SingleGroup<Epi>::make(epi), (epi.rows + 15) / 16, nb, s);
     else
