@@ -663,7 +663,14 @@ inline void launch_mt2(const WL& wl, const XIn& xa, const Epi& epi, uint32_t uni
 
 template <bool NORM, class WL, class Epi>
 inline void launch_norm(const WL& wl, const XIn& xa, const Epi& epi, uint32_t pairs, uint32_t nb, hipStream_t s) {
-    if (xa.T > 256)
+    // Paired epilogues (gate/up, QKV, the lm_head) switch to 32-token tiles as soon
+    // as 16-token tiles would need more than four workgroups per CU: the lm_head at
+    // 49 tokens 68 -> 53 us, gate/up at 128 tokens 17.7 -> 16.4. Plain stores keep
+    // their single-group units up to 256 tokens (down at 49 tokens: 9.5 us against
+    // 13.5 with 32-token tiles of pairs).
+    const bool wide = !SingleGroup<Epi>::kOk && xa.T > 16 &&
+                      static_cast<uint64_t>(pairs) * ((xa.T + 15) / 16) >= 4ull * device_cus();
+    if (xa.T > 256 || wide)
         launch_mt2<NORM>(wl, xa, epi, pairs, nb, s);
     else if constexpr (SingleGroup<Epi>::kOk)
         launch_mt1<NORM>(wl, xa, SingleGroup<Epi>::make(epi), (epi.rows + 15) / 16, nb, s);
