@@ -397,6 +397,15 @@ int kanso_model_init_random(kanso_model* model, uint64_t seed, float std);
 int kanso_model_alloc_kv(kanso_model* model, uint32_t num_blocks, uint32_t block_size,
                          uint32_t max_tokens, uint32_t max_seqs);
 
+/* kanso_model_alloc_kv with a pool kind (Engine::new_with_budget_and_kv's kv_mode,
+ * src/engine.rs:62-100): KANSO_KV_F32, or a 1-byte pool (INT8 / FP8 with one f32
+ * scale per token-head row, Q8_0 with one f16 scale per 32 elements). With a
+ * 1-byte pool each layer's new K / V rows go through the fused append + quantize
+ * (kanso_kv_append) and the attention reads the pool in that kind;
+ * kanso_model_kv_pool / kanso_model_read_kv_rows then report an error. */
+int kanso_model_alloc_kv_quant(kanso_model* model, uint32_t num_blocks, uint32_t block_size,
+                               uint32_t max_tokens, uint32_t max_seqs, uint32_t kv_dtype);
+
 /* Device pointers of layer `layer`'s K and V pools ([num_blocks][bs][kv_heads][64]). */
 int kanso_model_kv_pool(kanso_model* model, uint32_t layer, float** k_pool, float** v_pool);
 

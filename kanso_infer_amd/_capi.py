@@ -170,6 +170,7 @@ SIGNATURES: dict[str, tuple] = {
     "kanso_model_set_weight": (_I, [_P, _U, _U, _P, C.c_size_t]),
     "kanso_model_init_random": (_I, [_P, C.c_uint64, C.c_float]),
     "kanso_model_alloc_kv": (_I, [_P, _U, _U, _U, _U]),
+    "kanso_model_alloc_kv_quant": (_I, [_P, _U, _U, _U, _U, _U]),
     "kanso_model_kv_pool": (_I, [_P, _U, C.POINTER(_P), C.POINTER(_P)]),
     "kanso_model_reset_blocks": (_I, [_P, _P, _U, _P]),
     "kanso_model_read_kv_rows": (_I, [_P, _U, _P, _U, _P, _P]),

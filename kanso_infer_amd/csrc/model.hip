@@ -79,6 +79,11 @@ __global__ void reset_blocks_kernel(float* k, float* v, const uint32_t* blocks, 
 
 uint32_t grid_for(uint64_t n) { return static_cast<uint32_t>(std::min<uint64_t>((n + 255) / 256, 8192)); }
 
+__global__ void iota_i64_kernel(int64_t* out, uint64_t n) {
+    for (uint64_t i = blockIdx.x * 256ull + threadIdx.x; i < n; i += static_cast<uint64_t>(gridDim.x) * 256)
+        out[i] = static_cast<int64_t>(i);
+}
+
 template <class T>
 int dev_alloc(kanso_model* m, T** p, size_t bytes) {
     void* q = nullptr;
@@ -204,6 +209,15 @@ int ensure_step_buffers(kanso_model* m, uint32_t T, uint32_t S, uint32_t tables,
         m->cap_seqs = sq;
         // per-pair argmax keys of the lm_head for every sampled row
         if ((rc = ensure_keys(m->ctx, static_cast<size_t>(sq) * ((c.vocab + 31) / 32) * 8))) return rc;
+        if (m->kv_dtype != KANSO_KV_F32) {
+            const size_t kv_row = static_cast<size_t>(c.num_kv_heads) * c.head_dim * 4;
+            if ((rc = dev_alloc(m, &m->k_stage, t * kv_row))) return rc;
+            if ((rc = dev_alloc(m, &m->v_stage, t * kv_row))) return rc;
+            if ((rc = dev_alloc(m, &m->iota, t * 8ull))) return rc;
+            hipLaunchKernelGGL(iota_i64_kernel, dim3(grid_for(t)), dim3(256), 0, 0, m->iota, static_cast<uint64_t>(t));
+            KANSO_LAUNCH_CHECK();
+            KANSO_HIP_TRY(hipDeviceSynchronize());
+        }
     }
     if (tables > m->cap_tables) {
         if ((rc = dev_alloc(m, &m->tables, static_cast<size_t>(tables) * 4))) return rc;
@@ -232,9 +246,31 @@ int model_reset_blocks(kanso_model* m, const uint32_t* blocks, uint32_t n, hipSt
         return KANSO_E_INVALID_ARG;
     }
     int rc;
-    if (n > m->cap_reset) {
-        if ((rc = dev_alloc(m, &m->d_reset, n * 4ull))) return rc;
-        m->cap_reset = n;
+    const uint32_t L = m->cfg.num_layers;
+    const uint32_t need = m->kv_dtype == KANSO_KV_F32 ? n : n * L;
+    if (need > m->cap_reset) {
+        if ((rc = dev_alloc(m, &m->d_reset, need * 4ull))) return rc;
+        m->cap_reset = need;
+    }
+    if (m->kv_dtype != KANSO_KV_F32) {
+        // Every layer's pool is the next num_blocks blocks of one pool of L x num_blocks
+        // blocks, so one erase of the blocks b + l * num_blocks covers all layers
+        // (bytes to 0, scales to their empty value).
+        // (Ids outside the pool are skipped, as in the F32 erase.)
+        std::vector<uint32_t> all;
+        all.reserve(need);
+        for (uint32_t l = 0; l < L; ++l)
+            for (uint32_t i = 0; i < n; ++i)
+                if (blocks[i] < m->num_blocks) all.push_back(blocks[i] + l * m->num_blocks);
+        if (all.empty()) return KANSO_OK;
+        const uint32_t cnt = static_cast<uint32_t>(all.size());
+        KANSO_HIP_TRY(hipMemcpyAsync(m->d_reset, all.data(), cnt * 4ull, hipMemcpyHostToDevice, s));
+        if ((rc = kanso_kv_reset_blocks(m->ctx, m->kv_dtype, m->d_reset, cnt, m->num_blocks * L, m->block_size,
+                                        m->cfg.num_kv_heads, m->cfg.head_dim, m->k_pool, m->v_pool, m->k_scales,
+                                        m->v_scales, reinterpret_cast<kanso_stream_t>(s))))
+            return rc;
+        KANSO_HIP_TRY(hipStreamSynchronize(s));
+        return KANSO_OK;
     }
     // The list is tiny; a synchronous copy keeps the host array's lifetime simple.
     KANSO_HIP_TRY(hipMemcpyAsync(m->d_reset, blocks, n * 4ull, hipMemcpyHostToDevice, s));
@@ -324,7 +360,7 @@ int model_forward(kanso_model* m, const HostStep& step, float* logits, uint32_t*
     ap.max_num_blocks_per_seq = max_blocks;
     ap.scale = static_cast<float>(1.0 / std::sqrt(static_cast<double>(c.head_dim)));  // src/model.rs:757-762
     ap.total_q = T;
-    ap.kv_dtype = KANSO_KV_F32;
+    ap.kv_dtype = m->kv_dtype;
     ap.num_blocks = m->num_blocks;
     ap.max_q_len = max_q;
     {
@@ -340,15 +376,35 @@ int model_forward(kanso_model* m, const HostStep& step, float* logits, uint32_t*
         ap.chunk_partition_size = kanso_ragged_chunk_partition_size(m->ctx, &ap, ql.data(), cl.data());
     }
     const uint32_t qd = c.num_heads * 64;
+    const bool quant = m->kv_dtype != KANSO_KV_F32;
+    // 1-byte pools: the QKV epilogue writes K / V rows to the staging rows 0..T-1, and
+    // the fused append + quantize (kanso_kv_append, write_kv_slots of the quantized
+    // storage) takes them into the pool slots.
+    kanso_qkv_params qs = qp;
+    qs.num_blocks = m->cap_tokens;
+    qs.block_size = 1;
     for (uint32_t l = 0; l < c.num_layers; ++l) {
         const auto& L = m->layers[l];
-        float* kp = m->k_pool + l * m->layer_pool_elems;
-        float* vp = m->v_pool + l * m->layer_pool_elems;
-        if ((rc = op_qkv_rope_append(m->ctx, &qp, L.qkv, m->hidden, L.attn_norm, m->positions, m->slots, m->cos_t,
-                                     m->sin_t, m->q, kp, vp, s)))
-            return rc;
-        if ((rc = kanso_ragged_paged_attention(m->ctx, &ap, m->q, kp, vp, nullptr, nullptr, m->tables,
-                                               m->cu, m->ctx_lens, m->attn, reinterpret_cast<kanso_stream_t>(s))))
+        uint8_t* kp = reinterpret_cast<uint8_t*>(m->k_pool) + l * m->layer_pool_bytes;
+        uint8_t* vp = reinterpret_cast<uint8_t*>(m->v_pool) + l * m->layer_pool_bytes;
+        uint8_t* ks = quant ? m->k_scales + l * m->layer_scale_bytes : nullptr;
+        uint8_t* vs = quant ? m->v_scales + l * m->layer_scale_bytes : nullptr;
+        if (!quant) {
+            if ((rc = op_qkv_rope_append(m->ctx, &qp, L.qkv, m->hidden, L.attn_norm, m->positions, m->slots,
+                                         m->cos_t, m->sin_t, m->q, reinterpret_cast<float*>(kp),
+                                         reinterpret_cast<float*>(vp), s)))
+                return rc;
+        } else {
+            if ((rc = op_qkv_rope_append(m->ctx, &qs, L.qkv, m->hidden, L.attn_norm, m->positions, m->iota,
+                                         m->cos_t, m->sin_t, m->q, m->k_stage, m->v_stage, s)))
+                return rc;
+            if ((rc = kanso_kv_append(m->ctx, m->kv_dtype, m->k_stage, m->v_stage, m->slots, T, m->num_blocks,
+                                      m->block_size, c.num_kv_heads, c.head_dim, kp, vp, ks, vs,
+                                      reinterpret_cast<kanso_stream_t>(s))))
+                return rc;
+        }
+        if ((rc = kanso_ragged_paged_attention(m->ctx, &ap, m->q, kp, vp, ks, vs, m->tables, m->cu, m->ctx_lens,
+                                               m->attn, reinterpret_cast<kanso_stream_t>(s))))
             return rc;
         if ((rc = op_gemm_residual(L.o, m->attn, m->hidden, c.hidden, qd, T, s))) return rc;
         if ((rc = op_gate_up_swiglu(L.gate_up, m->hidden, L.ffn_norm, c.eps, T, c.hidden, c.intermediate, m->act,
@@ -517,8 +573,8 @@ int kanso_model_init_random(kanso_model* m, uint64_t seed, float std) {
     return rc;
 }
 
-int kanso_model_alloc_kv(kanso_model* m, uint32_t num_blocks, uint32_t block_size, uint32_t max_tokens,
-                         uint32_t max_seqs) {
+int kanso_model_alloc_kv_quant(kanso_model* m, uint32_t num_blocks, uint32_t block_size, uint32_t max_tokens,
+                               uint32_t max_seqs, uint32_t kv_dtype) {
     int rc = model_check(m, "kanso_model_alloc_kv");
     if (rc) return rc;
     if (m->k_pool) {
@@ -531,22 +587,58 @@ int kanso_model_alloc_kv(kanso_model* m, uint32_t num_blocks, uint32_t block_siz
                   num_blocks, block_size, max_tokens, max_seqs);
         return KANSO_E_INVALID_SHAPE;
     }
+    if (kv_dtype > KANSO_KV_FP8) {
+        set_error("kanso_model_alloc_kv: unknown kv_dtype %u", kv_dtype);
+        return KANSO_E_INVALID_ARG;
+    }
+    const uint64_t rows = static_cast<uint64_t>(num_blocks) * block_size * m->cfg.num_kv_heads;
+    if (static_cast<uint64_t>(num_blocks) * m->cfg.num_layers >= (1ull << 32)) {
+        set_error("kanso_model_alloc_kv: %u blocks x %u layers too many", num_blocks, m->cfg.num_layers);
+        return KANSO_E_INVALID_SHAPE;
+    }
     m->num_blocks = num_blocks;
     m->block_size = block_size;
-    m->layer_pool_elems = static_cast<size_t>(num_blocks) * block_size * m->cfg.num_kv_heads * m->cfg.head_dim;
-    const size_t bytes = m->layer_pool_elems * m->cfg.num_layers * sizeof(float);
+    m->kv_dtype = kv_dtype;
+    m->layer_pool_elems = rows * m->cfg.head_dim;
+    m->layer_pool_bytes = m->layer_pool_elems * (kv_dtype == KANSO_KV_F32 ? 4 : 1);
+    m->layer_scale_bytes = kv_dtype == KANSO_KV_INT8 || kv_dtype == KANSO_KV_FP8 ? rows * 4
+                           : kv_dtype == KANSO_KV_Q8_0                          ? rows * (m->cfg.head_dim / 32) * 2
+                                                                                : 0;
+    const size_t bytes = m->layer_pool_bytes * m->cfg.num_layers;
     if ((rc = dev_alloc(m, &m->k_pool, bytes))) return rc;
     if ((rc = dev_alloc(m, &m->v_pool, bytes))) return rc;
     KANSO_HIP_TRY(hipMemset(m->k_pool, 0, bytes));
     KANSO_HIP_TRY(hipMemset(m->v_pool, 0, bytes));
+    if (m->layer_scale_bytes) {
+        const size_t sb = m->layer_scale_bytes * m->cfg.num_layers;
+        if ((rc = dev_alloc(m, &m->k_scales, sb))) return rc;
+        if ((rc = dev_alloc(m, &m->v_scales, sb))) return rc;
+        if (kv_dtype == KANSO_KV_Q8_0) {
+            KANSO_HIP_TRY(hipMemset(m->k_scales, 0, sb));
+            KANSO_HIP_TRY(hipMemset(m->v_scales, 0, sb));
+        } else {  // an empty INT8 / FP8 row has scale 1 (quantized_storage.rs:35-40)
+            const uint64_t n = sb / 4;
+            hipLaunchKernelGGL(fill_f32_kernel, dim3(grid_for(n)), dim3(256), 0, 0,
+                               reinterpret_cast<float*>(m->k_scales), n, 1.0f);
+            hipLaunchKernelGGL(fill_f32_kernel, dim3(grid_for(n)), dim3(256), 0, 0,
+                               reinterpret_cast<float*>(m->v_scales), n, 1.0f);
+            KANSO_LAUNCH_CHECK();
+            KANSO_HIP_TRY(hipDeviceSynchronize());
+        }
+    }
     return ensure_step_buffers(m, max_tokens, max_seqs, max_seqs * 64, max_tokens + max_seqs * 64);
+}
+
+int kanso_model_alloc_kv(kanso_model* m, uint32_t num_blocks, uint32_t block_size, uint32_t max_tokens,
+                         uint32_t max_seqs) {
+    return kanso_model_alloc_kv_quant(m, num_blocks, block_size, max_tokens, max_seqs, KANSO_KV_F32);
 }
 
 int kanso_model_kv_pool(kanso_model* m, uint32_t layer, float** k_pool, float** v_pool) {
     int rc = model_check(m, "kanso_model_kv_pool");
     if (rc) return rc;
-    if (!m->k_pool || layer >= m->cfg.num_layers) {
-        set_error("kanso_model_kv_pool: no pool for layer %u", layer);
+    if (!m->k_pool || layer >= m->cfg.num_layers || m->kv_dtype != KANSO_KV_F32) {
+        set_error("kanso_model_kv_pool: no F32 pool for layer %u", layer);
         return KANSO_E_INVALID_ARG;
     }
     if (k_pool) *k_pool = m->k_pool + layer * m->layer_pool_elems;
@@ -558,8 +650,9 @@ int kanso_model_read_kv_rows(kanso_model* m, uint32_t layer, const uint64_t* slo
                              float* v_out) {
     int rc = model_check(m, "kanso_model_read_kv_rows");
     if (rc) return rc;
-    if (!m->k_pool || layer >= m->cfg.num_layers || (n && (!slots || !k_out || !v_out))) {
-        set_error("kanso_model_read_kv_rows: no pool for layer %u or null argument", layer);
+    if (!m->k_pool || layer >= m->cfg.num_layers || m->kv_dtype != KANSO_KV_F32 ||
+        (n && (!slots || !k_out || !v_out))) {
+        set_error("kanso_model_read_kv_rows: no F32 pool for layer %u or null argument", layer);
         return KANSO_E_INVALID_ARG;
     }
     const size_t row = static_cast<size_t>(m->cfg.num_kv_heads) * m->cfg.head_dim;

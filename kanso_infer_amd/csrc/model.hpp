@@ -50,11 +50,23 @@ struct kanso_model {
     float* cos_t = nullptr;  // [max_position][head_dim / 2]
     float* sin_t = nullptr;
     std::vector<void*> allocations;  // every device buffer above, freed at destroy
-    // KV pool: [layers][num_blocks][block_size][kv_heads][head_dim] f32, K and V.
-    float* k_pool = nullptr;
+    // KV pool: [layers][num_blocks][block_size][kv_heads][head_dim], K and V, of kind
+    // kv_dtype: f32 elements, or 1-byte elements with per-row scales (INT8 / FP8: one
+    // f32 per token-head row; Q8_0: one f16 per 32 elements) in k_scales / v_scales.
+    float* k_pool = nullptr;  // (bytes for the 1-byte kinds)
     float* v_pool = nullptr;
+    uint32_t kv_dtype = 0;
+    uint8_t* k_scales = nullptr;
+    uint8_t* v_scales = nullptr;
     uint32_t num_blocks = 0, block_size = 0;
-    size_t layer_pool_elems = 0;
+    size_t layer_pool_elems = 0;   // elements of one layer's K (or V) pool
+    size_t layer_pool_bytes = 0;
+    size_t layer_scale_bytes = 0;
+    // 1-byte kinds: this step's K / V rows before quantization, [tokens][kv_heads][64]
+    // f32, and the identity slot map the QKV epilogue writes them through.
+    float* k_stage = nullptr;
+    float* v_stage = nullptr;
+    int64_t* iota = nullptr;
     // Step buffers sized for max_tokens rows / max_seqs sequences (grow-only).
     uint32_t cap_tokens = 0, cap_seqs = 0, cap_tables = 0, cap_arena = 0;
     float *hidden = nullptr, *q = nullptr, *attn = nullptr, *act = nullptr;

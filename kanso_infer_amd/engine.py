@@ -150,9 +150,12 @@ class Model:
     def init_random(self, seed: int = 0x5EED0057, std: float = 0.02) -> None:
         _check(self._lib.kanso_model_init_random(self.handle, seed, std))
 
-    def alloc_kv(self, num_blocks: int, block_size: int, max_tokens: int, max_seqs: int) -> None:
-        _check(self._lib.kanso_model_alloc_kv(self.handle, num_blocks, block_size, max_tokens,
-                                              max_seqs))
+    def alloc_kv(self, num_blocks: int, block_size: int, max_tokens: int, max_seqs: int,
+                 kv_dtype: int = 0) -> None:
+        """The paged KV pool; kv_dtype (KANSO_KV_*) as Engine::new_with_budget_and_kv's
+        kv_mode (src/engine.rs:62-100): 0 = F32, else a 1-byte pool."""
+        _check(self._lib.kanso_model_alloc_kv_quant(self.handle, num_blocks, block_size,
+                                                    max_tokens, max_seqs, kv_dtype))
 
     def kv_pool(self, layer: int) -> tuple[int, int]:
         k, v = C.c_void_p(), C.c_void_p()

@@ -151,6 +151,7 @@ typedef struct {
     uint32_t hidden, num_heads, num_kv_heads, head_dim, num_layers, intermediate, vocab;
     float eps, rope_theta;
     uint32_t weight_format;
+    uint32_t kv_dtype; /* KANSO_KV_* of the pools passed to the forward */
 } oracle_model_config;
 
 /* Matrices in the config's weight_format and f32 norm weights; per-layer
@@ -185,11 +186,14 @@ int oracle_forward_batch(const oracle_model_config* cfg, const oracle_model_weig
 
 /* The shared body of forward_batch / forward_batch_all_rows (src/model.rs:1382-1410,
  * RowSelection): all_rows = 0 gives logits [S][vocab] of each sequence's last row,
- * all_rows = 1 logits [T][vocab] of every new token (the speculative verifier's rows). */
+ * all_rows = 1 logits [T][vocab] of every new token (the speculative verifier's rows).
+ * The pools are of cfg->kv_dtype (k_scales / v_scales per layer for the 1-byte
+ * kinds, NULL for F32): new rows go through oracle_kv_append of that kind. */
 int oracle_forward_batch_rows(const oracle_model_config* cfg, const oracle_model_weights* w,
                               const uint32_t* tokens, const int32_t* positions,
-                              const int64_t* slot_mapping, uint32_t T, float* const* k_pools,
-                              float* const* v_pools, uint32_t num_blocks, uint32_t block_size,
+                              const int64_t* slot_mapping, uint32_t T, void* const* k_pools,
+                              void* const* v_pools, void* const* k_scales, void* const* v_scales,
+                              uint32_t num_blocks, uint32_t block_size,
                               const uint32_t* block_tables, uint32_t max_blocks,
                               const int32_t* cu_seqlens, const uint32_t* context_lens, uint32_t S,
                               int all_rows, float* logits, int nthreads);

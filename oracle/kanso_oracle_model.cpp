@@ -19,8 +19,9 @@ extern "C" {
 
 int oracle_forward_batch_rows(const oracle_model_config* cfg, const oracle_model_weights* w,
                               const uint32_t* tokens, const int32_t* positions,
-                              const int64_t* slot_mapping, uint32_t T, float* const* k_pools,
-                              float* const* v_pools, uint32_t num_blocks, uint32_t block_size,
+                              const int64_t* slot_mapping, uint32_t T, void* const* k_pools,
+                              void* const* v_pools, void* const* k_scales, void* const* v_scales,
+                              uint32_t num_blocks, uint32_t block_size,
                               const uint32_t* block_tables, uint32_t max_blocks,
                               const int32_t* cu_seqlens, const uint32_t* context_lens, uint32_t S,
                               int all_rows, float* logits, int nthreads) {
@@ -82,7 +83,8 @@ int oracle_forward_batch_rows(const oracle_model_config* cfg, const oracle_model
     // attention_scale: 1 / sqrt(head_dim) (src/model.rs:757-762), applied in f32.
     ap.scale = static_cast<float>(1.0 / std::sqrt(static_cast<double>(D)));
     ap.total_q = T;
-    ap.kv_dtype = KANSO_KV_F32;
+    ap.kv_dtype = cfg->kv_dtype;
+    if (cfg->kv_dtype > KANSO_KV_FP8 || (cfg->kv_dtype != KANSO_KV_F32 && (!k_scales || !v_scales))) return -1;
     ap.num_blocks = num_blocks;
     ap.max_q_len = 0;
     ap.pool_layout = KANSO_POOL_TOKEN_MAJOR;
@@ -95,11 +97,13 @@ int oracle_forward_batch_rows(const oracle_model_config* cfg, const oracle_model
         oracle_rope_apply(q.data(), T, H, D, positions, cos_t.data(), sin_t.data());
         oracle_rope_apply(k.data(), T, HKV, D, positions, cos_t.data(), sin_t.data());
         // write_kv_slots (src/model.rs:1673; storage.rs:219-254)
-        if (oracle_kv_append(KANSO_KV_F32, k.data(), v.data(), slot_mapping, T, num_blocks, block_size,
-                             HKV, D, k_pools[l], v_pools[l], nullptr, nullptr) != 0)
+        void* ks = cfg->kv_dtype != KANSO_KV_F32 ? k_scales[l] : nullptr;
+        void* vs = cfg->kv_dtype != KANSO_KV_F32 ? v_scales[l] : nullptr;
+        if (oracle_kv_append(cfg->kv_dtype, k.data(), v.data(), slot_mapping, T, num_blocks, block_size, HKV, D,
+                             k_pools[l], v_pools[l], ks, vs) != 0)
             return -1;
-        if (oracle_ragged_attention(q.data(), k_pools[l], v_pools[l], nullptr, nullptr, block_tables,
-                                    cu_seqlens, context_lens, &ap, attn.data(), nthreads) != 0)
+        if (oracle_ragged_attention(q.data(), k_pools[l], v_pools[l], ks, vs, block_tables, cu_seqlens,
+                                    context_lens, &ap, attn.data(), nthreads) != 0)
             return -1;
         // hidden = hidden + attn_output(attn) (src/model.rs:1716-1717)
         linear(w->wo[l], attn.data(), proj.data(), Hd, H * D);
@@ -145,7 +149,11 @@ int oracle_forward_batch(const oracle_model_config* cfg, const oracle_model_weig
                          const uint32_t* block_tables, uint32_t max_blocks,
                          const int32_t* cu_seqlens, const uint32_t* context_lens, uint32_t S,
                          float* logits, int nthreads) {
-    return oracle_forward_batch_rows(cfg, w, tokens, positions, slot_mapping, T, k_pools, v_pools,
+    oracle_model_config f32 = *cfg;
+    f32.kv_dtype = KANSO_KV_F32;
+    return oracle_forward_batch_rows(&f32, w, tokens, positions, slot_mapping, T,
+                                     reinterpret_cast<void* const*>(k_pools),
+                                     reinterpret_cast<void* const*>(v_pools), nullptr, nullptr,
                                      num_blocks, block_size, block_tables, max_blocks, cu_seqlens,
                                      context_lens, S, 0, logits, nthreads);
 }

@@ -35,20 +35,35 @@ def random_weights(cfg: dict, seed: int, std: float = 0.02) -> dict:
 
 
 class OracleModel:
-    def __init__(self, cfg: dict, weights: dict, num_blocks: int, block_size: int, nthreads=8):
-        self.cfg, self.weights = cfg, weights
+    """kv_dtype: the pool kind (oracle.KV_*): F32, or a 1-byte pool whose rows are
+    quantized by oracle_kv_append (Engine::new_with_budget_and_kv, src/engine.rs:62-100)."""
+
+    def __init__(self, cfg: dict, weights: dict, num_blocks: int, block_size: int, nthreads=8,
+                 kv_dtype: int = oracle.KV_F32):
+        self.cfg, self.weights = dict(cfg, kv_dtype=kv_dtype), weights
+        self.kv_dtype = kv_dtype
         self.num_blocks, self.block_size = num_blocks, block_size
-        n = num_blocks * block_size * cfg["num_kv_heads"] * cfg["head_dim"]
-        self.k = [np.zeros(n, np.float32) for _ in range(cfg["num_layers"])]
-        self.v = [np.zeros(n, np.float32) for _ in range(cfg["num_layers"])]
+        pools = [oracle.kv_pool_arrays(kv_dtype, num_blocks, block_size, cfg["num_kv_heads"],
+                                       cfg["head_dim"]) for _ in range(cfg["num_layers"])]
+        self.k = [p[0] for p in pools]
+        self.v = [p[1] for p in pools]
+        self.ks = [p[2] for p in pools]
+        self.vs = [p[3] for p in pools]
         self.nthreads = nthreads
         self.last_logits = None
 
     def reset_block(self, block: int) -> None:
         """allocate_zeroed's erase (src/kv_cache/mod.rs:25-35) across every layer."""
-        w = self.block_size * self.cfg["num_kv_heads"] * self.cfg["head_dim"]
+        rows = self.block_size * self.cfg["num_kv_heads"]
+        w = rows * self.cfg["head_dim"]
         for a in self.k + self.v:
-            a[block * w:(block + 1) * w] = 0.0
+            a[block * w:(block + 1) * w] = 0
+        if self.kv_dtype != oracle.KV_F32:
+            # scales of an empty row: 1.0 (INT8 / FP8, quantized_storage.rs:35-40), 0 (Q8_0)
+            per = rows if self.kv_dtype in (oracle.KV_INT8, oracle.KV_FP8) else w // 32
+            empty = 1.0 if self.kv_dtype in (oracle.KV_INT8, oracle.KV_FP8) else 0
+            for a in self.ks + self.vs:
+                a[block * per:(block + 1) * per] = empty
 
     def logits(self, plan, all_rows: bool = False) -> np.ndarray:
         """[S, vocab] of each sequence's last row, or with all_rows [T, vocab] of every
@@ -64,7 +79,8 @@ class OracleModel:
         cu = np.concatenate([[0], np.cumsum(plan.query_lens)]).astype(np.int32)
         return oracle.forward_batch(self.cfg, self.weights, self.k, self.v, self.num_blocks, bs,
                                     plan.tokens, plan.positions, plan.slot_mapping, tables,
-                                    max_blocks, cu, ctx, nthreads=self.nthreads, all_rows=all_rows)
+                                    max_blocks, cu, ctx, nthreads=self.nthreads, all_rows=all_rows,
+                                    k_scales=self.ks, v_scales=self.vs)
 
     def forward(self, plan) -> list:
         """engine_ref forward: greedy_token (src/sampler.rs:7-17) of each sequence."""

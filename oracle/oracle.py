@@ -327,7 +327,8 @@ def available() -> bool:
 class ModelConfigC(C.Structure):
     _fields_ = [(n, C.c_uint32) for n in ("hidden", "num_heads", "num_kv_heads", "head_dim",
                                           "num_layers", "intermediate", "vocab")] + [
-        ("eps", C.c_float), ("rope_theta", C.c_float), ("weight_format", C.c_uint32)]
+        ("eps", C.c_float), ("rope_theta", C.c_float), ("weight_format", C.c_uint32),
+        ("kv_dtype", C.c_uint32)]
 
 
 class ModelWeightsC(C.Structure):
@@ -338,14 +339,15 @@ class ModelWeightsC(C.Structure):
 
 def forward_batch(cfg: dict, weights: dict, k_pools, v_pools, num_blocks, block_size, tokens,
                   positions, slot_mapping, block_tables, max_blocks, cu_seqlens, context_lens,
-                  nthreads=8, all_rows=False) -> np.ndarray:
+                  nthreads=8, all_rows=False, k_scales=None, v_scales=None) -> np.ndarray:
     """oracle_forward_batch_rows: logits [S, vocab] of each sequence's last row, or with
     all_rows [T, vocab] of every new token (forward_batch_all_rows). k_pools / v_pools
     are per-layer float32 arrays updated in place (write_kv_slots)."""
     L = cfg["num_layers"]
     c = ModelConfigC(cfg["hidden"], cfg["num_heads"], cfg["num_kv_heads"], cfg["head_dim"], L,
                      cfg["intermediate"], cfg["vocab"], cfg.get("eps", 1e-5),
-                     cfg.get("rope_theta", 10000.0), cfg.get("weight_format", 0))
+                     cfg.get("rope_theta", 10000.0), cfg.get("weight_format", 0),
+                     cfg.get("kv_dtype", KV_F32))
     keep = []
 
     def arr(name):
@@ -360,6 +362,9 @@ def forward_batch(cfg: dict, weights: dict, k_pools, v_pools, num_blocks, block_
                                          "attn_norm", "ffn_norm")])
     kp = (C.c_void_p * L)(*[_p(k).value for k in k_pools])
     vp = (C.c_void_p * L)(*[_p(v).value for v in v_pools])
+    quant = cfg.get("kv_dtype", KV_F32) != KV_F32
+    ksp = (C.c_void_p * L)(*[_p(k).value for k in k_scales]) if quant else None
+    vsp = (C.c_void_p * L)(*[_p(v).value for v in v_scales]) if quant else None
     tokens = _u32(tokens)
     positions = np.ascontiguousarray(positions, dtype=np.int32)
     slots = np.ascontiguousarray(slot_mapping, dtype=np.int64)
@@ -372,6 +377,8 @@ def forward_batch(cfg: dict, weights: dict, k_pools, v_pools, num_blocks, block_
     fn.restype = C.c_int
     rc = fn(C.byref(c), C.byref(w), _p(tokens), _p(positions), _p(slots), C.c_uint32(tokens.size),
             C.cast(kp, C.POINTER(C.c_void_p)), C.cast(vp, C.POINTER(C.c_void_p)),
+            C.cast(ksp, C.POINTER(C.c_void_p)) if quant else None,
+            C.cast(vsp, C.POINTER(C.c_void_p)) if quant else None,
             C.c_uint32(num_blocks), C.c_uint32(block_size), _p(tables), C.c_uint32(max_blocks),
             _p(cu), _p(ctx), C.c_uint32(S), C.c_int(1 if all_rows else 0), _p(logits),
             C.c_int(nthreads))

@@ -23,13 +23,18 @@ SMOL4 = dict(hidden=960, num_heads=15, num_kv_heads=5, head_dim=64, num_layers=4
              intermediate=2560, vocab=49152)
 
 
-def gpu_model(ctx, cfg, weights, num_blocks, block_size, max_tokens=512, max_seqs=64):
+def gpu_model(ctx, cfg, weights, num_blocks, block_size, max_tokens=512, max_seqs=64,
+              kv_dtype=oracle.KV_F32):
     mc = ModelConfig(cfg["hidden"], cfg["num_heads"], cfg["num_kv_heads"], cfg["num_layers"],
                      cfg["intermediate"], cfg["vocab"], max_position=4096)
     m = Model(ctx, mc)
     m.load_weights(weights)
-    m.alloc_kv(num_blocks, block_size, max_tokens, max_seqs)
+    m.alloc_kv(num_blocks, block_size, max_tokens, max_seqs, kv_dtype=kv_dtype)
     return m
+
+
+KV_KINDS = [oracle.KV_F32, oracle.KV_INT8, oracle.KV_FP8, oracle.KV_Q8_0]
+KV_IDS = ["f32", "int8", "fp8", "q8_0"]
 
 
 def compact(plan, bs):
@@ -59,13 +64,17 @@ def mixed_plans(rng, bs, vocab, nblocks):
     return plan_of(p1, bs), plan_of(p2, bs)
 
 
+@pytest.mark.parametrize("kv", KV_KINDS, ids=KV_IDS)
 @pytest.mark.parametrize("cfg", [SMALL, SMOL4], ids=["small", "smollm2_width_4_layers"])
-def test_forward_logits_match_oracle(ctx, cfg):
+def test_forward_logits_match_oracle(ctx, cfg, kv):
+    """Mixed steps through kanso_model_forward against the oracle forward, with an F32
+    pool or a 1-byte pool (Engine::new_with_budget_and_kv, src/engine.rs:62-100: the
+    new rows go through the fused append + quantize, the attention reads the pool)."""
     bs, nblocks = 16, 40
     rng = np.random.default_rng(11)
     w = random_weights(cfg, seed=5)
-    gm = gpu_model(ctx, cfg, w, nblocks, bs)
-    om = OracleModel(cfg, w, nblocks, bs)
+    gm = gpu_model(ctx, cfg, w, nblocks, bs, kv_dtype=kv)
+    om = OracleModel(cfg, w, nblocks, bs, kv_dtype=kv)
     for step, plan in enumerate(mixed_plans(rng, bs, cfg["vocab"], nblocks)):
         rows, toks, tabs = compact(plan, bs)
         S = rows.shape[0]
@@ -74,9 +83,21 @@ def test_forward_logits_match_oracle(ctx, cfg):
         ctx.check_device_status()
         want = om.logits(plan)
         got = host(logits).reshape(S, cfg["vocab"])
-        assert_close(got, want, what=f"logits step {step}")
         for s in range(S):
             assert got_tok[s] == oracle.greedy(got[s])
+        if kv != oracle.KV_F32:
+            # The pool bytes are bit-exact for identical K / V rows, but the rows come out
+            # of the matrix-core products ~2^-17 away from the oracle's, and a value at an
+            # int8 / e4m3 rounding boundary then lands on the neighbouring code: one
+            # quantization step for that element. So: every logit within 1e-2, and at
+            # least 99% within the F32 tolerance (2e-3 abs / 1e-3 rel) for the 8-bit codes;
+            # 85% for e4m3, whose 3-bit mantissa makes one code step ~6% of the value.
+            assert_close(got, want, atol=1e-2, rtol=1e-2, what=f"logits step {step}")
+            strict = np.abs(got - want) <= 2e-3 + 1e-3 * np.abs(want)
+            floor = 0.85 if kv == oracle.KV_FP8 else 0.99
+            assert strict.mean() >= floor, f"step {step}: {strict.mean():.4f} within 2e-3/1e-3"
+            continue
+        assert_close(got, want, what=f"logits step {step}")
         # the K / V rows the step wrote match the oracle's pools
         slots = np.asarray(plan.slot_mapping)
         width = cfg["num_kv_heads"] * cfg["head_dim"]
@@ -149,10 +170,11 @@ def test_init_random_statistics(ctx):
     assert 0.45 < lg.std() < 0.8
 
 
-def engine_pair(ctx, cfg, w, max_running, total_blocks, bs, budget):
-    gm = gpu_model(ctx, cfg, w, total_blocks, bs, max_tokens=budget, max_seqs=max_running + 1)
+def engine_pair(ctx, cfg, w, max_running, total_blocks, bs, budget, kv_dtype=oracle.KV_F32):
+    gm = gpu_model(ctx, cfg, w, total_blocks, bs, max_tokens=budget, max_seqs=max_running + 1,
+                   kv_dtype=kv_dtype)
     eng = Engine(gm, max_running, total_blocks, bs, budget)
-    om = OracleModel(cfg, w, total_blocks, bs)
+    om = OracleModel(cfg, w, total_blocks, bs, kv_dtype=kv_dtype)
     ref = R.Engine(om.forward, max_running, total_blocks, bs, budget, reset_block=om.reset_block)
     return eng, ref
 
@@ -180,10 +202,12 @@ def run_both(eng, ref, requests, max_steps=2000):
     return gen_a, gen_b
 
 
-@pytest.mark.parametrize("cfg,budget,total_blocks", [(SMALL, 32, 64), (SMALL, 512, 14),
-                                                     (SMOL4, 64, 64)],
-                         ids=["small_chunked", "small_tight_pool", "smollm2_width_4_layers"])
-def test_engine_checksum_matches_oracle(ctx, cfg, budget, total_blocks):
+@pytest.mark.parametrize("cfg,budget,total_blocks,kv", [
+    (SMALL, 32, 64, oracle.KV_F32), (SMALL, 512, 14, oracle.KV_F32), (SMOL4, 64, 64, oracle.KV_F32),
+    (SMALL, 32, 64, oracle.KV_INT8), (SMALL, 512, 14, oracle.KV_Q8_0), (SMOL4, 64, 64, oracle.KV_FP8)],
+    ids=["small_chunked", "small_tight_pool", "smollm2_width_4_layers", "small_chunked_int8",
+         "small_tight_pool_q8_0", "smollm2_width_4_layers_fp8"])
+def test_engine_checksum_matches_oracle(ctx, cfg, budget, total_blocks, kv):
     rng = np.random.default_rng(budget + total_blocks)
     w = random_weights(cfg, seed=9)
     bs = 16
@@ -194,7 +218,7 @@ def test_engine_checksum_matches_oracle(ctx, cfg, budget, total_blocks):
         prompt = ([(i % 3 * 10 + p) % 30 for p in range(plen)] if i % 2 == 0
                   else rng.integers(0, cfg["vocab"], plen).tolist())
         reqs.append((prompt, int(rng.integers(4, 20)), int(rng.integers(0, 6))))
-    eng, ref = engine_pair(ctx, cfg, w, 4, total_blocks, bs, budget)
+    eng, ref = engine_pair(ctx, cfg, w, 4, total_blocks, bs, budget, kv_dtype=kv)
     gen_a, gen_b = run_both(eng, ref, reqs)
     assert fnv1a_64(gen_a) == R.fnv1a_64(gen_b) == oracle.fnv1a_64(gen_b)
     assert len(gen_a) == sum(g for _, g, _ in reqs)

@@ -120,6 +120,31 @@ def test_golden_logits_fixture():
         assert top(got) == top(exp), key
 
 
+@pytest.mark.parametrize("kv", ["int8", "fp8"])
+def test_quantized_kv_logits_track_f32_on_the_mock(kv):
+    """tests/test_quantized_kv_engine.rs:147-207 on the reproduced mock model: after a
+    prefill of `ctx` tokens (i % 50) and one decode step (token 7), the logits with an
+    INT8 / FP8 pool stay within 20% of the F32 logit range (MAX_REL_DRIFT, :28) and
+    pick the same greedy token, at contexts 512 and 2048 (:30)."""
+    import mock_rng
+    kind = oracle.KV_INT8 if kv == "int8" else oracle.KV_FP8
+    cfg, w = mock_rng.mock_tiny_weights(16, 4, 2, 2, 50)
+    bs = 16
+    for ctx in (512, 2048):
+        blocks = -(-(ctx + 1) // bs)
+        table = list(range(blocks))
+        prompt = [i % 50 for i in range(ctx)]
+        out = {}
+        for name, kd in (("f32", oracle.KV_F32), (kv, kind)):
+            m = OracleModel(cfg, w, blocks, bs, kv_dtype=kd)
+            m.logits(plan_of([(prompt, 0, table)], bs))
+            out[name] = m.logits(plan_of([([7], ctx, table)], bs))[0]
+        ref, got = out["f32"], out[kv]
+        rel = np.abs(ref - got).max() / (ref.max() - ref.min())
+        assert rel <= 0.20, (ctx, rel)
+        assert int(np.argmax(ref)) == int(np.argmax(got)), ctx
+
+
 def _f64_forward(cfg, w, tokens):
     """One sequence from position 0, every op in float64 numpy (no paging)."""
     h, H, KV, D = cfg["hidden"], cfg["num_heads"], cfg["num_kv_heads"], cfg["head_dim"]
