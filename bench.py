@@ -251,11 +251,12 @@ def config5_workload(seed=0x5EED0005, num_requests=64, rate=40.0, step_secs=0.00
     return schedule_to_trace(sched, plen, glen, step_secs)
 
 
-def engine_bench(ctx, K, torch, num_requests=64):
+def engine_bench(ctx, K, torch, num_requests=64, kv_dtype=0):
     """Config 5: SmolLM2-360M-architecture random-init model (32 layers, Q8_0 weights
     N(0, 0.02^2), tied embeddings, F32 KV) under the C++ continuous-batching engine:
     512-token budget, max_running 64, block size 16, greedy. Value = generated
-    tokens / wall seconds of the whole run (execute_engine_run, src/bench.rs:447-537)."""
+    tokens / wall seconds of the whole run (execute_engine_run, src/bench.rs:447-537).
+    kv_dtype != 0: the same run on a 1-byte pool (Engine::new_with_budget_and_kv)."""
     from kanso_infer_amd.engine import Engine, Model, ModelConfig, run_benchmark_workload
     cfg = ModelConfig.smollm2_360m(max_position=4096)
     t0 = time.perf_counter()
@@ -265,7 +266,7 @@ def engine_bench(ctx, K, torch, num_requests=64):
     max_tokens = max(r.prompt_len + r.gen_len for r in reqs)
     blocks_per_seq = -(-max_tokens // 16) + 1  # create_engine_for_model_profile, src/bench.rs:598-614
     total_blocks = max(blocks_per_seq * len(reqs), 128)
-    model.alloc_kv(total_blocks, 16, 512, 65)
+    model.alloc_kv(total_blocks, 16, 512, 65, kv_dtype=kv_dtype)
     log(f"config5: model ready in {time.perf_counter() - t0:.1f} s, {total_blocks} KV blocks")
     # warm-up on a throwaway engine (same model and pool), so first-call costs stay out
     warm = Engine(model, 64, total_blocks, 16, 512)
@@ -274,6 +275,10 @@ def engine_bench(ctx, K, torch, num_requests=64):
     warm.close()
     eng = Engine(model, 64, total_blocks, 16, 512)
     kv_tok = cfg.kv_cache_bytes_per_token_f32()
+    if kv_dtype:  # 1-byte elements plus the row scales (f32 per row; f16 per 32 for Q8_0)
+        d = cfg.head_dim
+        row = d + 4 if kv_dtype in (K.KANSO_KV_INT8, K.KANSO_KV_FP8) else d + 2 * d // 32
+        kv_tok = kv_tok * row // (4 * d)
     wbytes = cfg.weight_bytes_q8_0()
     acc = dict(kv_bytes=0, steps_with_work=0, tokens=0, max_batch=0, step_times=[])
 
@@ -403,7 +408,7 @@ def config5_cpu_baseline(threads=None):
                        f"32 layers, {el:.1f} s on {threads} threads (setup {setup:.1f} s)")
 
 
-def config5_checksum_parity(ctx, K, torch):
+def config5_checksum_parity(ctx, K, torch, kv_dtype=0):
     """Greedy token streams of the GPU engine and of the oracle engine (scheduler
     restatement + CPU forward) on the same random-init weights: SmolLM2 widths, 4 of
     the 32 layers, 6 requests with bench.rs-pattern and random prompts, chunked
@@ -419,9 +424,10 @@ def config5_checksum_parity(ctx, K, torch):
     bs, budget, total_blocks, max_running = 16, 64, 64, 4
     gm = Model(ctx, ModelConfig(960, 15, 5, 4, 2560, 49152, max_position=4096))
     gm.load_weights(w)
-    gm.alloc_kv(total_blocks, bs, budget, max_running + 1)
+    gm.alloc_kv(total_blocks, bs, budget, max_running + 1, kv_dtype=kv_dtype)
     eng = Engine(gm, max_running, total_blocks, bs, budget)
-    om = OracleModel(cfg, w, total_blocks, bs, nthreads=min(os.cpu_count() or 1, 16))
+    om = OracleModel(cfg, w, total_blocks, bs, nthreads=min(os.cpu_count() or 1, 16),
+                     kv_dtype=kv_dtype)
     ref = engine_ref.Engine(om.forward, max_running, total_blocks, bs, budget,
                             reset_block=om.reset_block)
     rng = np.random.default_rng(7)
@@ -778,6 +784,11 @@ def main():
         log(f"config5: {extras['config5_engine']}")
         extras["config5_engine"]["checksum_parity"] = config5_checksum_parity(ctx, K, torch)
         log(f"config5 parity: {extras['config5_engine']['checksum_parity']}")
+        # the same run with an INT8 pool (the reference's kv_mode = Int8)
+        r8 = engine_bench(ctx, K, torch, kv_dtype=K.KANSO_KV_INT8)
+        r8["checksum_parity"] = config5_checksum_parity(ctx, K, torch, kv_dtype=K.KANSO_KV_INT8)
+        extras["config5_engine_int8_kv"] = {k: v for k, v in r8.items() if k != "workload"}
+        log(f"config5 int8 kv: {extras['config5_engine_int8_kv']}")
         if not args.no_cpu:
             extras["config5_engine"]["cpu_baseline"] = config5_cpu_baseline()
             log(f"config5 cpu: {extras['config5_engine']['cpu_baseline']}")
