@@ -62,6 +62,7 @@ struct AttnArgs {
     const uint32_t* ctx_lens;
     float* part_out;     // [T][H][max_parts][D]
     float2* part_stats;  // [T][H][max_parts] (m in log2 units, l)
+    uint32_t* row_np;    // [T] partitions of each query row (0: no key), for the merge
     float* out;          // [T][H][D]
     uint32_t* status;
     uint32_t num_seqs, num_heads, num_kv_heads, group, block_size, bs_shift;
@@ -1237,6 +1238,7 @@ __device__ void zero_empty_rows(const AttnArgs& a, const SeqTable& st, uint32_t 
         const int32_t ql = st.cu[s + 1] - st.cu[s];
         for (int32_t i = 0; i < ql; ++i)
             if (row_limit(st.ctx[s], ql, i, a.capacity) == 0) {
+                a.row_np[st.cu[s] + i] = 0;
                 float* row = a.out + static_cast<size_t>(st.cu[s] + i) * a.num_heads * D;
                 for (uint32_t e = 0; e < a.num_heads * D; ++e) row[e] = 0.f;
             }
@@ -1280,6 +1282,9 @@ __global__ __launch_bounds__(kThreads, 2) void attn_main(AttnArgs a) {
                         if (local < np) break;
                         local -= np;
                     }
+                    if (local == 0 && kvh == 0 && static_cast<int32_t>(threadIdx.x) < min(kChunkBlockRows, ql - i0))
+                        a.row_np[st.cu[s] + i0 + threadIdx.x] =
+                            ceil_div(row_limit(st.ctx[s], ql, i0 + threadIdx.x, a.capacity), a.chunk_part);
                     chunk_block<GC, KVT>(a, st, rs, stage, static_cast<uint32_t>(st.cu[s] + i0), local,
                                          min(kChunkBlockRows, ql - i0), s, kvh);
                     __syncthreads();  // the next item's prologue reuses the stages
@@ -1309,6 +1314,8 @@ __global__ __launch_bounds__(kThreads, 2) void attn_main(AttnArgs a) {
             }
         }
         const uint32_t row = static_cast<uint32_t>(st.cu[s] + i);
+        if (local == 0 && kvh == 0 && lane == 0)
+            a.row_np[row] = ceil_div(row_limit(st.ctx[s], ql, i, a.capacity), a.part_size);
         if constexpr (KVT == KANSO_KV_FP8 && BUF && D == 64 && GMAX <= 4)
             decode_item_mq<GMAX, KVT, 2>(a, st, rs, row, local, a.part_size, s, kvh, lane);
         else if constexpr (KVT != KANSO_KV_F32 && BUF && D >= kQE)
@@ -1320,31 +1327,18 @@ __global__ __launch_bounds__(kThreads, 2) void attn_main(AttnArgs a) {
 
 // One group of LPG lanes per (row, query head) in a grid-stride loop: rows split
 // over several partitions are merged (a kernel boundary orders them after every
-// partial); single-partition rows were written by stage 1.
+// partial); single-partition rows were written by stage 1. Each row's partition
+// count comes from the main kernel (row_np), so no sequence table is built here:
+// the first loads are the row's statistics.
 template <int D, int LPG>
 __global__ __launch_bounds__(kThreads) void attn_reduce(AttnArgs a) {
-    __shared__ SeqTable st;
-    const uint32_t tid = threadIdx.x;
-    for (uint32_t s = tid; s <= a.num_seqs; s += kThreads) {
-        st.cu[s] = a.cu[s];
-        if (s < a.num_seqs) st.ctx[s] = static_cast<int32_t>(a.ctx_lens[s]);
-    }
-    __syncthreads();
     const int lane = threadIdx.x & (kWave - 1);
     constexpr uint32_t kGroups = kThreads / LPG;
     const uint32_t n_groups = gridDim.x * kGroups;
     const uint32_t n_work = a.total_q * a.num_heads;
     for (uint32_t w = blockIdx.x * kGroups + threadIdx.x / LPG; w < n_work; w += n_groups) {
         const uint32_t row = w / a.num_heads, h = w % a.num_heads;
-        uint32_t lo = 0, hi = a.num_seqs;  // last s with cu[s] <= row
-        while (hi - lo > 1) {
-            const uint32_t mid = (lo + hi) >> 1;
-            if (static_cast<uint32_t>(st.cu[mid]) <= row) lo = mid;
-            else hi = mid;
-        }
-        const int32_t ql = st.cu[lo + 1] - st.cu[lo];
-        const uint32_t lim = row_limit(st.ctx[lo], ql, static_cast<int32_t>(row) - st.cu[lo], a.capacity);
-        const uint32_t np = ceil_div(lim, part_of(a, ql, a.part_size));
+        const uint32_t np = a.row_np[row];  // written by the main kernel for every row
         if (np > 1) merge_partials<D, LPG>(a, static_cast<size_t>(row) * a.num_heads + h, np, lane);
     }
 }
@@ -1567,7 +1561,8 @@ int run_ragged(kanso_ctx* ctx, const kanso_ragged_attention_params* p, const flo
     // Scratch: [stats T*H*max_parts float2][partials T*H*max_parts*D f32].
     const size_t off_stats = 0;
     const size_t off_part = align_up(static_cast<size_t>(T) * H * max_parts * sizeof(float2), 256);
-    const size_t total = off_part + partial_elems * sizeof(float);
+    const size_t off_np = align_up(off_part + partial_elems * sizeof(float), 256);
+    const size_t total = off_np + static_cast<size_t>(T) * sizeof(uint32_t);
     int rc = ensure_scratch(ctx, total);
     if (rc) return rc;
     char* base = static_cast<char*>(ctx->scratch);
@@ -1583,6 +1578,7 @@ int run_ragged(kanso_ctx* ctx, const kanso_ragged_attention_params* p, const flo
     a.ctx_lens = ctx_lens;
     a.part_out = reinterpret_cast<float*>(base + off_part);
     a.part_stats = reinterpret_cast<float2*>(base + off_stats);
+    a.row_np = reinterpret_cast<uint32_t*>(base + off_np);
     a.out = out;
     a.status = ctx->status;
     a.num_seqs = S;
