@@ -31,6 +31,8 @@
 //            coalesced 512 B load.
 #pragma once
 
+#include <atomic>
+
 #include "common.hpp"
 
 namespace kanso {
@@ -618,15 +620,15 @@ struct SingleGroup<EpiStore<ADD, 2>> {
 // (e.g. gate/up at 80 tokens 10.4 us against 17.4 with NU = 1, down 10.1 against
 // 16.5).
 inline uint32_t device_cus() {
-    static int cached[64] = {};
+    static std::atomic<int> cached[64] = {};  // per device; 0 = not queried yet
     int dev = 0;
     if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
-    if (cached[dev] == 0) {
-        int n = 0;
+    int n = cached[dev].load(std::memory_order_relaxed);
+    if (n == 0) {
         if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0) n = 256;
-        cached[dev] = n;
+        cached[dev].store(n, std::memory_order_relaxed);
     }
-    return static_cast<uint32_t>(cached[dev]);
+    return static_cast<uint32_t>(n);
 }
 
 inline uint32_t pick_nu(uint32_t units, uint32_t tiles) {
