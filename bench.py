@@ -348,7 +348,10 @@ def verify_bench(ctx, K, torch, num_seqs=16, context=1000, rows=5, reps=20):
     ver = step([(s, context, rows) for s in range(num_seqs)])
 
     def timed(fn, args):
-        for _ in range(3):
+        # at least 0.5 s of the same call first: the first process on a fresh box ran
+        # its first seconds at about half speed
+        t_end = time.perf_counter() + 0.5
+        while time.perf_counter() < t_end:
             fn(*args)
         t0 = time.perf_counter()
         for _ in range(reps):

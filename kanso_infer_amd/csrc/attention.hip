@@ -1720,8 +1720,11 @@ uint32_t kanso_ragged_chunk_partition_size(const kanso_ctx* ctx, const kanso_rag
     }
     if (T == 0 || cap == 0 || !use_mfma_path(p, max_q)) return 0;
     const uint32_t p_max = std::max(32u, std::min(512u, 62u * p->block_size / 32u * 32u));
-    const uint64_t resident = std::min<uint64_t>(main_grid(ctx, T, 1, HKV, true), 2ull * ctx->num_cus);
     for (uint32_t cp = std::min(64u, p_max); cp <= p_max; cp += 32) {
+        // the launch's grid for this partition (its partial count sizes it), at most
+        // two workgroups per CU resident
+        const uint64_t resident =
+            std::min<uint64_t>(main_grid(ctx, T, (cap + cp - 1) / cp, HKV, true), 2ull * ctx->num_cus);
         uint64_t n_chunk = 0;
         for (uint32_t s = 0; s < S; ++s) {
             const uint32_t ql = q_lens[s], c = context_lens[s];
