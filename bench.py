@@ -633,8 +633,9 @@ def main():
     POOL_LAYOUT = 1 if args.pool_layout == "head" else 0
     PARTITION = args.partition
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
-        print("bench.py measures one GPU: this path has no multi-GPU component in this build "
-              "(see DESIGN.md for how it would shard); run with --gpus 1", file=sys.stderr)
+        print("bench.py measures one GPU: this build has no multi-GPU component (the path "
+              "would shard by sequences, one engine and KV pool per GPU); run with --gpus 1",
+              file=sys.stderr)
         sys.exit(2)
 
     import torch
