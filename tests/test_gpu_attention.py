@@ -149,6 +149,31 @@ def test_explicit_partition_size(ctx, partition, kv_dtype):
     assert_close(got, want, what=f"{b.label} P {partition} kv {kv_dtype}")
 
 
+@pytest.mark.parametrize("chunks", [0, 4])
+def test_max_sequences_per_call(ctx, chunks):
+    """2048 sequences in one call (the LDS-resident per-call limit), all-decode and
+    mixed with matrix-core chunks, against the oracle; 2049 is rejected."""
+    rng = np.random.default_rng(90 + chunks)
+    S = 2048
+    q_lens = np.ones(S, np.int64)
+    q_lens[:chunks] = rng.integers(3, 20, chunks)
+    ctx_lens = rng.integers(1, 40, S).astype(np.int64) + np.where(q_lens > 1, q_lens, 0)
+    nb = int(((ctx_lens + 15) // 16).sum()) + 8
+    tables = workloads._scatter_tables(rng, ctx_lens, 16, nb)
+    b = workloads.AttnBatch(q_lens, ctx_lens, tables, nb, label=f"S2048 chunks {chunks}",
+                            **workloads.SMOLLM2)
+    kp, vp, ks, vs = fill_pool(b, oracle.KV_F32, 91)
+    q = rng.standard_normal(b.total_q * b.num_heads * b.head_dim).astype(np.float32)
+    got = run_ragged_gpu(ctx, b, q, kp, vp)
+    want = run_ragged_oracle(b, q, kp, vp)
+    assert_close(got, want, what=b.label)
+    over = workloads.AttnBatch(np.ones(S + 1, np.int64), np.ones(S + 1, np.int64),
+                               np.zeros((S + 1, 1), np.uint32), 1, **workloads.SMOLLM2)
+    with pytest.raises(K.EngineError):
+        run_ragged_gpu(ctx, over, np.zeros(over.total_q * 15 * 64, np.float32),
+                       np.zeros(16 * 5 * 64, np.float32), np.zeros(16 * 5 * 64, np.float32))
+
+
 def test_rejects_bad_partition_size(ctx):
     b = workloads.small_mixed(12)
     kp, vp, ks, vs = fill_pool(b, oracle.KV_F32, 12)
