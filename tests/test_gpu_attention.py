@@ -174,6 +174,20 @@ def test_max_sequences_per_call(ctx, chunks):
                        np.zeros(16 * 5 * 64, np.float32), np.zeros(16 * 5 * 64, np.float32))
 
 
+@pytest.mark.parametrize("bs", [1, 4, 32])
+def test_block_size_extremes_with_longest_partition(ctx, bs):
+    """Block sizes 1, 4 and 32 with the longest legal partitions (62 table entries,
+    at most 992 keys) for decode and chunk rows, against the oracle."""
+    b = workloads.small_mixed(20 + bs, block_size=bs, max_ctx=1500, chunk_max=70)
+    kp, vp, ks, vs = fill_pool(b, oracle.KV_F32, 20 + bs)
+    q = np.random.default_rng(63).standard_normal(
+        b.total_q * b.num_heads * b.head_dim).astype(np.float32)
+    longest = max(32, min(992, 62 * bs // 32 * 32))
+    got = run_ragged_gpu(ctx, b, q, kp, vp, partition_size=longest, chunk_partition_size=longest)
+    want = run_ragged_oracle(b, q, kp, vp)
+    assert_close(got, want, what=f"{b.label} bs {bs} P {longest}")
+
+
 def test_rejects_bad_partition_size(ctx):
     b = workloads.small_mixed(12)
     kp, vp, ks, vs = fill_pool(b, oracle.KV_F32, 12)

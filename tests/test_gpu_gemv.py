@@ -53,6 +53,22 @@ def test_q4_k(ctx, name, rows, cols, batch):
     assert_close(got, want, what=f"q4_k {name} b{batch}")
 
 
+@pytest.mark.parametrize("batch", [1, 40, 300])
+@pytest.mark.parametrize("rows,cols", [(16, 64), (80, 96), (1008, 960), (4112, 2560)])
+def test_q8_0_ragged_row_counts(ctx, rows, cols, batch):
+    """Row counts with an odd number of 16-row groups and of row pairs, so the last
+    workgroup holds fewer groups / units than the others (NU > 1 clamps its extra
+    units), at 16-token and 32-token tiles; GGUF-layout and packed entry points."""
+    got, want = run(ctx, "q8_0", rows, cols, batch, seed=5)
+    assert_close(got, want, what=f"q8_0 {rows}x{cols} b{batch}")
+    w, wd = weights("q8_0", rows, cols)
+    packed = K.pack_q8_0_matrix(ctx, wd, rows, cols)
+    x = np.random.default_rng(5 + batch).standard_normal((batch, cols)).astype(np.float32)
+    y = torch.empty(batch * rows, dtype=torch.float32, device="cuda:0")
+    K.gemm_q8_0(ctx, packed, dev(x), y, rows, cols)
+    assert_close(host(y), want, what=f"packed q8_0 {rows}x{cols} b{batch}")
+
+
 def test_reference_closed_form(ctx):
     # probes.rs:64-71 with an f16 scale: d = 0.01 (as f16), qs = 1, x = 1
     rows, cols = 64, 1024
