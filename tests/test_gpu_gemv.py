@@ -69,6 +69,14 @@ def test_q8_0_ragged_row_counts(ctx, rows, cols, batch):
     assert_close(host(y), want, what=f"packed q8_0 {rows}x{cols} b{batch}")
 
 
+@pytest.mark.parametrize("batch", [1, 40, 300])
+@pytest.mark.parametrize("rows,cols", [(80, 256), (1008, 2560)])
+def test_q4_k_ragged_row_counts(ctx, rows, cols, batch):
+    """Q4_K at odd group / pair counts (partial last workgroup)."""
+    got, want = run(ctx, "q4_k", rows, cols, batch, seed=6)
+    assert_close(got, want, what=f"q4_k {rows}x{cols} b{batch}")
+
+
 def test_reference_closed_form(ctx):
     # probes.rs:64-71 with an f16 scale: d = 0.01 (as f16), qs = 1, x = 1
     rows, cols = 64, 1024
