@@ -42,6 +42,7 @@
 #include <cstdlib>
 
 #include "common.hpp"
+#include "model.hpp"
 
 namespace kanso {
 namespace {
@@ -72,7 +73,17 @@ struct AttnArgs {
     uint32_t head_major;  // pool rows [block][kv head][offset] instead of [block][offset][kv head]
     uint32_t pool_bytes, scale_bytes;  // per pool tensor, for buffer resources (< 4 GiB)
     float scale_log2;
+    uint32_t out_nbk;  // 0: out is row-major [T][H][D]; else the tiled activation order, K / 32
 };
+
+// Output of query row `head / H`, head `head % H`, dims d .. (up to 4 consecutive
+// floats starting at a multiple of 4: contiguous in both orders).
+__device__ __forceinline__ float* out_at(const AttnArgs& a, size_t head, uint32_t D, uint32_t d) {
+    if (!a.out_nbk) return a.out + head * D + d;
+    const uint32_t row = static_cast<uint32_t>(head / a.num_heads);
+    const uint32_t col = static_cast<uint32_t>(head % a.num_heads) * D + d;
+    return a.out + act_tile_off(row, col, a.out_nbk);
+}
 
 // Key limit of row i of a sequence: keys 0..=ctx-q_len+i, clamped to what the table
 // can address (the Metal kernel clamps the same way, paged_attention_v2.metal:86-89).
@@ -366,7 +377,7 @@ __device__ __forceinline__ void merge_partials(const AttnArgs& a, size_t head, u
     if (r == 0)
 #pragma unroll
         for (int k = 0; k < N4; ++k)
-            *reinterpret_cast<float4*>(a.out + head * D + d0 + 4 * k) =
+            *reinterpret_cast<float4*>(out_at(a, head, D, d0 + 4 * k)) =
                 make_float4(o[k].x * inv, o[k].y * inv, o[k].z * inv, o[k].w * inv);
 }
 
@@ -548,7 +559,7 @@ __device__ void decode_item(const AttnArgs& a, const SeqTable& st, const PoolRsr
         if (single) {
             const float inv = l[g] > 0.f ? 1.0f / l[g] : 0.f;
             if (ts == 0)
-                *reinterpret_cast<float4*>(a.out + head * D + dl * 4) =
+                *reinterpret_cast<float4*>(out_at(a, head, D, dl * 4)) =
                     make_float4(acc[g].x * inv, acc[g].y * inv, acc[g].z * inv, acc[g].w * inv);
             continue;
         }
@@ -746,9 +757,11 @@ __device__ void decode_item_q(const AttnArgs& a, const SeqTable& st, const PoolR
         if (single) {
             const float inv = l[g] > 0.f ? 1.0f / l[g] : 0.f;
             if (ts == 0) {
-                float4* d4 = reinterpret_cast<float4*>(a.out + head * D + dl * kQE);
-                d4[0] = make_float4(acc[g][0] * inv, acc[g][1] * inv, acc[g][2] * inv, acc[g][3] * inv);
-                d4[1] = make_float4(acc[g][4] * inv, acc[g][5] * inv, acc[g][6] * inv, acc[g][7] * inv);
+                static_assert(kQE == 8, "two float4 per lane");
+                *reinterpret_cast<float4*>(out_at(a, head, D, dl * kQE)) =
+                    make_float4(acc[g][0] * inv, acc[g][1] * inv, acc[g][2] * inv, acc[g][3] * inv);
+                *reinterpret_cast<float4*>(out_at(a, head, D, dl * kQE + 4)) =
+                    make_float4(acc[g][4] * inv, acc[g][5] * inv, acc[g][6] * inv, acc[g][7] * inv);
             }
             continue;
         }
@@ -984,9 +997,10 @@ __device__ void decode_item_mq(const AttnArgs& a, const SeqTable& st, const Pool
             if (c == 0)
 #pragma unroll
                 for (int h = 0; h < 2; ++h) {
-                    float4* d4 = reinterpret_cast<float4*>(a.out + head * 64 + 32 * h + 8 * j);
-                    d4[0] = make_float4(acc[g][h][0] * inv, acc[g][h][1] * inv, acc[g][h][2] * inv, acc[g][h][3] * inv);
-                    d4[1] = make_float4(acc[g][h][4] * inv, acc[g][h][5] * inv, acc[g][h][6] * inv, acc[g][h][7] * inv);
+                    *reinterpret_cast<float4*>(out_at(a, head, 64, 32 * h + 8 * j)) =
+                        make_float4(acc[g][h][0] * inv, acc[g][h][1] * inv, acc[g][h][2] * inv, acc[g][h][3] * inv);
+                    *reinterpret_cast<float4*>(out_at(a, head, 64, 32 * h + 8 * j + 4)) =
+                        make_float4(acc[g][h][4] * inv, acc[g][h][5] * inv, acc[g][h][6] * inv, acc[g][h][7] * inv);
                 }
             continue;
         }
@@ -1217,10 +1231,10 @@ __device__ void chunk_block(const AttnArgs& a, const SeqTable& st, const PoolRsr
         const size_t head = static_cast<size_t>(qrow) * a.num_heads + kvh * G + g;
         if (writer) {
             const float inv = single ? (l[g] > 0.f ? 1.0f / l[g] : 0.f) : 1.0f;
-            float* dst = single ? a.out + head * D : a.part_out + (head * a.max_parts + part) * D;
+            float* dst = a.part_out + (head * a.max_parts + part) * D;
 #pragma unroll
             for (int r = 0; r < 4; ++r)
-                *reinterpret_cast<float4*>(dst + 16 * qq + 4 * r) =
+                *reinterpret_cast<float4*>(single ? out_at(a, head, D, 16 * qq + 4 * r) : dst + 16 * qq + 4 * r) =
                     make_float4(o[g][0][r] * inv, o[g][1][r] * inv, o[g][2][r] * inv, o[g][3][r] * inv);
             if (!single && qq == 0) a.part_stats[head * a.max_parts + part] = make_float2(m[g], l[g]);
         }
@@ -1239,8 +1253,9 @@ __device__ void zero_empty_rows(const AttnArgs& a, const SeqTable& st, uint32_t 
         for (int32_t i = 0; i < ql; ++i)
             if (row_limit(st.ctx[s], ql, i, a.capacity) == 0) {
                 a.row_np[st.cu[s] + i] = 0;
-                float* row = a.out + static_cast<size_t>(st.cu[s] + i) * a.num_heads * D;
-                for (uint32_t e = 0; e < a.num_heads * D; ++e) row[e] = 0.f;
+                const size_t head0 = static_cast<size_t>(st.cu[s] + i) * a.num_heads;
+                for (uint32_t e = 0; e < a.num_heads * D; e += 4)
+                    *reinterpret_cast<float4*>(out_at(a, head0 + e / D, D, e % D)) = make_float4(0.f, 0.f, 0.f, 0.f);
             }
     }
 }
@@ -1485,7 +1500,7 @@ uint32_t host_row_limit(uint32_t ctx_len, uint32_t q_len, uint32_t i, uint32_t c
 int run_ragged(kanso_ctx* ctx, const kanso_ragged_attention_params* p, const float* q,
                const void* kp, const void* vp, const void* ks, const void* vs,
                const uint32_t* tables, const int32_t* cu, const uint32_t* ctx_lens, float* out,
-               hipStream_t stream, const char* who) {
+               hipStream_t stream, const char* who, bool out_tiled = false) {
     const uint32_t S = p->num_seqs, H = p->num_heads, HKV = p->num_kv_heads, D = p->head_dim;
     if (!q || !kp || !vp || !tables || !cu || !ctx_lens || !out) {
         set_error("%s: null buffer", who);
@@ -1580,6 +1595,7 @@ int run_ragged(kanso_ctx* ctx, const kanso_ragged_attention_params* p, const flo
     a.part_stats = reinterpret_cast<float2*>(base + off_stats);
     a.row_np = reinterpret_cast<uint32_t*>(base + off_np);
     a.out = out;
+    a.out_nbk = out_tiled ? H * D / 32 : 0u;
     a.status = ctx->status;
     a.num_seqs = S;
     a.num_heads = H;
@@ -1637,6 +1653,20 @@ int run_ragged(kanso_ctx* ctx, const kanso_ragged_attention_params* p, const flo
 }
 
 }  // namespace
+
+int op_ragged_attention(kanso_ctx* ctx, const kanso_ragged_attention_params* p, const float* q, const void* k_pool,
+                        const void* v_pool, const void* k_scales, const void* v_scales, const uint32_t* block_tables,
+                        const int32_t* cu_seqlens, const uint32_t* context_lens, float* out, hipStream_t s,
+                        bool out_tiled) {
+    if (out_tiled && (p->num_heads * p->head_dim) % 32 != 0) {
+        set_error("ragged attention: tiled output needs heads x head_dim (%u) to be a multiple of 32",
+                  p->num_heads * p->head_dim);
+        return KANSO_E_INVALID_SHAPE;
+    }
+    return run_ragged(ctx, p, q, k_pool, v_pool, k_scales, v_scales, block_tables, cu_seqlens, context_lens, out, s,
+                      "ragged attention", out_tiled);
+}
+
 }  // namespace kanso
 
 using namespace kanso;

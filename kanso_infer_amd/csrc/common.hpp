@@ -130,6 +130,20 @@ __device__ __forceinline__ float group_max(float v) {
     return v;
 }
 
+// Tiled activation order: the decoder's activation matrices [tokens][K] (K a
+// multiple of 32) laid out in the order the bf16 matrix cores take their A operand
+// (lane l = 16 kq + mm holds token mm, columns 32 b + 8 kq .. + 7). Token m, column
+// k lives in 16-token tile m / 16, 32-column block k / 32, half (k % 8) / 4, at lane
+// 16 ((k % 32) / 8) + m % 16, element k % 4:
+//   ((tile * nbk + block) * 2 + half) * 256 + lane * 4 + k % 4   (nbk = K / 32).
+// So one wave reads a (tile, block, half) slice as one contiguous 1 KB load, where
+// the row-major order makes each load touch 16 rows; four consecutive columns
+// (k % 4 == 0) stay contiguous, so float4 stores of a row keep working.
+__host__ __device__ __forceinline__ size_t act_tile_off(uint32_t m, uint32_t k, uint32_t nbk) {
+    return ((static_cast<size_t>(m >> 4) * nbk + (k >> 5)) * 2 + ((k >> 2) & 1)) * 256 +
+           (((k >> 3) & 3) * 16 + (m & 15)) * 4 + (k & 3);
+}
+
 // 2^x on the transcendental unit (v_exp_f32); results below the f32 normal range
 // flush to 0, which only ever affects probabilities that are already negligible.
 __device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }

@@ -84,14 +84,30 @@ __global__ void iota_i64_kernel(int64_t* out, uint64_t n) {
         out[i] = static_cast<int64_t>(i);
 }
 
+// Allocates a device buffer owned by the model. A buffer that *p already holds is
+// replaced: freed and dropped from the model's list (callers that grow a buffer
+// synchronise the device first, so no queued kernel still reads it).
 template <class T>
 int dev_alloc(kanso_model* m, T** p, size_t bytes) {
     void* q = nullptr;
     KANSO_HIP_TRY(hipMalloc(&q, std::max<size_t>(bytes, 256)));
+    if (*p) {
+        void* old = static_cast<void*>(*p);
+        for (size_t i = 0; i < m->allocations.size(); ++i)
+            if (m->allocations[i] == old) {
+                m->allocations[i] = m->allocations.back();
+                m->allocations.pop_back();
+                (void)hipFree(old);
+                break;
+            }
+    }
     m->allocations.push_back(q);
     *p = static_cast<T*>(q);
     return KANSO_OK;
 }
+
+// Activation rows are padded to whole 16-token tiles (the tiled activation order).
+size_t tile_rows(uint32_t t) { return (static_cast<size_t>(t) + 15) / 16 * 16; }
 
 int model_check(kanso_model* m, const char* who) {
     if (!m) {
@@ -189,11 +205,17 @@ int ensure_step_buffers(kanso_model* m, uint32_t T, uint32_t S, uint32_t tables,
     const kanso_model_config& c = m->cfg;
     int rc;
     if (T > m->cap_tokens || S > m->cap_seqs) {
-        const uint32_t t = std::max(T, m->cap_tokens), sq = std::max(S, m->cap_seqs);
-        if ((rc = dev_alloc(m, &m->hidden, static_cast<size_t>(t) * c.hidden * 4))) return rc;
+        // grow with headroom, so a caller whose batch creeps up step by step does
+        // not reallocate on every step; the old buffers may still be in use by
+        // queued work, so wait for it before they are replaced
+        KANSO_HIP_TRY(hipDeviceSynchronize());
+        const uint32_t t = T > m->cap_tokens ? std::max(T, m->cap_tokens + m->cap_tokens / 2) : m->cap_tokens;
+        const uint32_t sq = S > m->cap_seqs ? std::max(S, m->cap_seqs + m->cap_seqs / 2) : m->cap_seqs;
+        const size_t tr = tile_rows(t);
+        if ((rc = dev_alloc(m, &m->hidden, tr * c.hidden * 4))) return rc;
         if ((rc = dev_alloc(m, &m->q, static_cast<size_t>(t) * c.num_heads * 64 * 4))) return rc;
-        if ((rc = dev_alloc(m, &m->attn, static_cast<size_t>(t) * c.num_heads * 64 * 4))) return rc;
-        if ((rc = dev_alloc(m, &m->act, static_cast<size_t>(t) * c.intermediate * 4))) return rc;
+        if ((rc = dev_alloc(m, &m->attn, tr * c.num_heads * 64 * 4))) return rc;
+        if ((rc = dev_alloc(m, &m->act, tr * c.intermediate * 4))) return rc;
         if ((rc = dev_alloc(m, &m->cu, (sq + 1) * 4ull))) return rc;
         if ((rc = dev_alloc(m, &m->seq_of_query, t * 4ull))) return rc;
         if ((rc = dev_alloc(m, &m->positions, t * 4ull))) return rc;
@@ -220,13 +242,16 @@ int ensure_step_buffers(kanso_model* m, uint32_t T, uint32_t S, uint32_t tables,
         }
     }
     if (tables > m->cap_tables) {
-        if ((rc = dev_alloc(m, &m->tables, static_cast<size_t>(tables) * 4))) return rc;
-        m->cap_tables = tables;
+        KANSO_HIP_TRY(hipDeviceSynchronize());
+        const uint32_t want = std::max(tables, m->cap_tables + m->cap_tables / 2);
+        if ((rc = dev_alloc(m, &m->tables, static_cast<size_t>(want) * 4))) return rc;
+        m->cap_tables = want;
     }
     const size_t need = align_up(static_cast<size_t>(S) * sizeof(kanso_seq_plan), 256) +
                         align_up(static_cast<size_t>(arena) * 4, 256) + align_up(static_cast<size_t>(S) * 4, 256);
     if (need > m->stage_bytes) {
         const size_t want = align_up(need + need / 2, 1 << 16);
+        KANSO_HIP_TRY(hipDeviceSynchronize());
         if ((rc = dev_alloc(m, &m->d_stage, want))) return rc;
         void* h = nullptr;
         KANSO_HIP_TRY(hipHostMalloc(&h, want));
@@ -249,8 +274,10 @@ int model_reset_blocks(kanso_model* m, const uint32_t* blocks, uint32_t n, hipSt
     const uint32_t L = m->cfg.num_layers;
     const uint32_t need = m->kv_dtype == KANSO_KV_F32 ? n : n * L;
     if (need > m->cap_reset) {
-        if ((rc = dev_alloc(m, &m->d_reset, need * 4ull))) return rc;
-        m->cap_reset = need;
+        KANSO_HIP_TRY(hipDeviceSynchronize());
+        const uint32_t want = std::max(need, m->cap_reset + m->cap_reset / 2);
+        if ((rc = dev_alloc(m, &m->d_reset, want * 4ull))) return rc;
+        m->cap_reset = want;
     }
     if (m->kv_dtype != KANSO_KV_F32) {
         // Every layer's pool is the next num_blocks blocks of one pool of L x num_blocks
@@ -347,7 +374,9 @@ int model_forward(kanso_model* m, const HostStep& step, float* logits, uint32_t*
     if ((rc = kanso_pack_step(m->ctx, d_plan, S, d_tok_arena, d_tab_arena, m->block_size, max_blocks, T, &packed,
                               reinterpret_cast<kanso_stream_t>(s))))
         return rc;
-    if ((rc = op_embed(m->ctx, m->embed, c.vocab, c.hidden, m->tokens, T, m->hidden, s))) return rc;
+    // hidden, attn and act are in the tiled activation order (act_tile_off): the
+    // products read them as contiguous 1 KB slices
+    if ((rc = op_embed(m->ctx, m->embed, c.vocab, c.hidden, m->tokens, T, m->hidden, s, true))) return rc;
 
     kanso_qkv_params qp{T, c.hidden, c.num_heads, c.num_kv_heads, 64, c.max_position, c.eps, m->num_blocks,
                         m->block_size};
@@ -392,28 +421,28 @@ int model_forward(kanso_model* m, const HostStep& step, float* logits, uint32_t*
         if (!quant) {
             if ((rc = op_qkv_rope_append(m->ctx, &qp, L.qkv, m->hidden, L.attn_norm, m->positions, m->slots,
                                          m->cos_t, m->sin_t, m->q, reinterpret_cast<float*>(kp),
-                                         reinterpret_cast<float*>(vp), s)))
+                                         reinterpret_cast<float*>(vp), s, true)))
                 return rc;
         } else {
             if ((rc = op_qkv_rope_append(m->ctx, &qs, L.qkv, m->hidden, L.attn_norm, m->positions, m->iota,
-                                         m->cos_t, m->sin_t, m->q, m->k_stage, m->v_stage, s)))
+                                         m->cos_t, m->sin_t, m->q, m->k_stage, m->v_stage, s, true)))
                 return rc;
             if ((rc = kanso_kv_append(m->ctx, m->kv_dtype, m->k_stage, m->v_stage, m->slots, T, m->num_blocks,
                                       m->block_size, c.num_kv_heads, c.head_dim, kp, vp, ks, vs,
                                       reinterpret_cast<kanso_stream_t>(s))))
                 return rc;
         }
-        if ((rc = kanso_ragged_paged_attention(m->ctx, &ap, m->q, kp, vp, ks, vs, m->tables, m->cu, m->ctx_lens,
-                                               m->attn, reinterpret_cast<kanso_stream_t>(s))))
+        if ((rc = op_ragged_attention(m->ctx, &ap, m->q, kp, vp, ks, vs, m->tables, m->cu, m->ctx_lens, m->attn, s,
+                                      true)))
             return rc;
-        if ((rc = op_gemm_residual(L.o, m->attn, m->hidden, c.hidden, qd, T, s))) return rc;
+        if ((rc = op_gemm_residual(L.o, m->attn, m->hidden, c.hidden, qd, T, s, true))) return rc;
         if ((rc = op_gate_up_swiglu(L.gate_up, m->hidden, L.ffn_norm, c.eps, T, c.hidden, c.intermediate, m->act,
-                                    s)))
+                                    s, true)))
             return rc;
-        if ((rc = op_gemm_residual(L.down, m->act, m->hidden, c.hidden, c.intermediate, T, s))) return rc;
+        if ((rc = op_gemm_residual(L.down, m->act, m->hidden, c.hidden, c.intermediate, T, s, true))) return rc;
     }
     if ((rc = op_lm_head_argmax(m->ctx, m->lm_head, m->hidden, d_last, m->final_norm, c.eps, R, c.hidden, c.vocab,
-                                logits, m->next, s)))
+                                logits, m->next, s, true)))
         return rc;
     KANSO_HIP_TRY(hipMemcpyAsync(m->h_next, m->next, R * 4ull, hipMemcpyDeviceToHost, s));
     KANSO_HIP_TRY(hipStreamSynchronize(s));

@@ -10,17 +10,23 @@ namespace kanso {
 
 // Fused decoder ops (decoder.hip).
 int op_embed(kanso_ctx* ctx, const void* table, uint32_t vocab, uint32_t hidden, const uint32_t* tokens,
-             uint32_t T, float* out, hipStream_t s);
+             uint32_t T, float* out, hipStream_t s, bool tiled);
 int op_qkv_rope_append(kanso_ctx* ctx, const kanso_qkv_params* p, const void* w, const float* x,
                        const float* norm_w, const int32_t* positions, const int64_t* slots, const float* cos_t,
-                       const float* sin_t, float* q, float* k_pool, float* v_pool, hipStream_t s);
+                       const float* sin_t, float* q, float* k_pool, float* v_pool, hipStream_t s, bool tiled);
 int op_gemm_residual(const void* w, const float* x, float* y, uint32_t out, uint32_t in, uint32_t T,
-                     hipStream_t s);
+                     hipStream_t s, bool tiled);
 int op_gate_up_swiglu(const void* w, const float* x, const float* norm_w, float eps, uint32_t T,
-                      uint32_t hidden, uint32_t inter, float* h, hipStream_t s);
+                      uint32_t hidden, uint32_t inter, float* h, hipStream_t s, bool tiled);
 int op_lm_head_argmax(kanso_ctx* ctx, const void* w, const float* x, const int32_t* rows, const float* norm_w,
                       float eps, uint32_t S, uint32_t hidden, uint32_t vocab, float* logits, uint32_t* tokens,
-                      hipStream_t s);
+                      hipStream_t s, bool tiled);
+// The ragged attention with its output in the tiled activation order (the O
+// projection's input) when out_tiled is set (attention.hip).
+int op_ragged_attention(kanso_ctx* ctx, const kanso_ragged_attention_params* p, const float* q, const void* k_pool,
+                        const void* v_pool, const void* k_scales, const void* v_scales, const uint32_t* block_tables,
+                        const int32_t* cu_seqlens, const uint32_t* context_lens, float* out, hipStream_t s,
+                        bool out_tiled);
 
 // One step as the scheduler hands it over: the compact plan plus the token and
 // block-table arenas kanso_pack_step reads (host memory).

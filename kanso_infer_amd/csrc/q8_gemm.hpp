@@ -44,14 +44,17 @@ constexpr uint32_t kPackedTileBytes = 544;  // 16 rows x (32 qs + 2 d)
 
 __device__ __forceinline__ float f16_bits_to_f32(uint16_t h) { return __half2float(__ushort_as_half(h)); }
 
-// 8 int8 (little-endian in q) -> 8 bf16 (exact: |q| <= 128 needs 8 bits).
+// 8 int8 (little-endian in q) -> 8 bf16 (exact: |q| <= 128 needs 8 bits). Each
+// byte converts to f32 (sign-extended byte select); one byte permute then takes
+// the upper halves of two floats, which are their bf16 values (exact, no rounding).
 __device__ __forceinline__ bf16x8 i8x8_to_bf16(uint64_t q) {
     uint32_t w[4];
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
         const float f0 = static_cast<float>(static_cast<int8_t>((q >> (16 * i)) & 0xff));
         const float f1 = static_cast<float>(static_cast<int8_t>((q >> (16 * i + 8)) & 0xff));
-        w[i] = (__builtin_bit_cast(uint32_t, f0) >> 16) | (__builtin_bit_cast(uint32_t, f1) & 0xffff0000u);
+        // bytes 2,3 of f0 -> 0,1 and bytes 2,3 of f1 -> 2,3
+        w[i] = __builtin_amdgcn_perm(__builtin_bit_cast(uint32_t, f1), __builtin_bit_cast(uint32_t, f0), 0x07060302u);
     }
     return __builtin_bit_cast(bf16x8, w);
 }
@@ -79,15 +82,40 @@ __device__ __forceinline__ Bf16Pair split_bf16(const float (&x)[8]) {
 
 // ---------------------------------------------------------------- weight loaders
 
+// A loader splits into load() (raw bytes only: every load of a round is issued
+// before any of them is used) and decode() (after the round's loads are in
+// flight). Converting the f16 scale inside load() made the compiler wait for each
+// block's loads before issuing the next block's, one memory round trip per block.
+struct RawQ8 {
+    uint64_t q;
+    uint32_t d;  // f16 bits
+};
+
+// at(g, lane) resolves a lane's row of 16-row group g once per kernel; load()
+// then adds a 32-bit block offset (the 64-bit address arithmetic per block cost
+// more instructions than the conversion of the block's weights).
 struct WPacked {
     const uint8_t* w;
     uint32_t nb;  // in / 32
     static constexpr bool kHasMin = false;
-    __device__ __forceinline__ void load(uint32_t g, uint32_t b, int lane, uint64_t& q, float& d, float& m) const {
+    using Raw = RawQ8;
+    struct Ptr {
+        const uint8_t* q;  // lane's 8 bytes of block 0
+        const uint8_t* d;  // lane's row scale of block 0
+    };
+    __device__ __forceinline__ Ptr at(uint32_t g, int lane) const {
+        const uint8_t* t = w + static_cast<size_t>(g) * nb * kPackedTileBytes;
+        return {t + 8 * lane, t + 512 + 2 * (lane & 15)};
+    }
+    __device__ __forceinline__ void load(const Ptr& p, uint32_t b, Raw& r) const {
+        const uint32_t off = b * kPackedTileBytes;
+        r.q = *reinterpret_cast<const uint64_t*>(p.q + off);
+        r.d = *reinterpret_cast<const uint16_t*>(p.d + off);
+    }
+    __device__ __forceinline__ void decode(const Raw& r, uint32_t, uint64_t& q, float& d, float& m) const {
+        q = r.q;
+        d = f16_bits_to_f32(static_cast<uint16_t>(r.d));
         m = 0.f;
-        const uint8_t* p = w + (static_cast<size_t>(g) * nb + b) * kPackedTileBytes;
-        q = *reinterpret_cast<const uint64_t*>(p + 8 * lane);
-        d = f16_bits_to_f32(*reinterpret_cast<const uint16_t*>(p + 512 + 2 * (lane & 15)));
     }
 };
 
@@ -96,19 +124,29 @@ struct WGguf {
     uint32_t nb;
     uint32_t rows;
     static constexpr bool kHasMin = false;
-    __device__ __forceinline__ void load(uint32_t g, uint32_t b, int lane, uint64_t& q, float& d, float& m) const {
-        m = 0.f;
-        const uint32_t row = g * 16 + (lane & 15);
-        if (row >= rows) {
-            q = 0;
-            d = 0.f;
-            return;
-        }
+    using Raw = RawQ8;
+    struct Ptr {
+        const uint8_t* blk;  // the lane's row, block 0
+        uint32_t kq;         // byte offset of the lane's 8 quants in a block
+    };
+    __device__ __forceinline__ Ptr at(uint32_t g, int lane) const {
+        // rows past the matrix read row 0 and are zeroed in decode()
+        uint32_t row = g * 16 + (lane & 15);
+        row = row < rows ? row : 0;
+        return {w + static_cast<size_t>(row) * nb * 34, 2u + 8u * static_cast<uint32_t>(lane >> 4)};
+    }
+    __device__ __forceinline__ void load(const Ptr& p, uint32_t b, Raw& r) const {
         // Blocks are 34 B, so qs is only 2-byte aligned; gfx950 serves an unaligned
         // 8-byte global load as one instruction (global_load_dwordx2).
-        const uint8_t* p = w + (static_cast<size_t>(row) * nb + b) * 34;
-        d = f16_bits_to_f32(*reinterpret_cast<const uint16_t*>(p));
-        __builtin_memcpy(&q, __builtin_assume_aligned(p + 2 + 8 * (lane >> 4), 2), 8);
+        const uint8_t* blk = p.blk + b * 34;
+        r.d = *reinterpret_cast<const uint16_t*>(blk);
+        __builtin_memcpy(&r.q, __builtin_assume_aligned(blk + p.kq, 2), 8);
+    }
+    __device__ __forceinline__ void decode(const Raw& r, uint32_t row, uint64_t& q, float& d, float& m) const {
+        const bool ok = row < rows;
+        q = ok ? r.q : 0;
+        d = ok ? f16_bits_to_f32(static_cast<uint16_t>(r.d)) : 0.f;
+        m = 0.f;
     }
 };
 
@@ -122,23 +160,33 @@ struct WQ4K {
     const uint8_t* w;
     uint32_t nsb;  // in / 256
     uint32_t rows;
-    __device__ __forceinline__ void load(uint32_t g, uint32_t b, int lane, uint64_t& q, float& d, float& m) const {
-        const uint32_t row = g * 16 + (lane & 15);
-        if (row >= rows) {
-            q = 0;
-            d = 0.f;
-            m = 0.f;
-            return;
-        }
-        const uint8_t* blk = w + (static_cast<size_t>(row) * nsb + b / 8) * 144;
-        const uint32_t sub = b % 8, j = sub / 2;
-        const uint32_t dd = *reinterpret_cast<const uint32_t*>(blk);
-        const uint32_t s0 = *reinterpret_cast<const uint32_t*>(blk + 4);
-        const uint32_t s1 = *reinterpret_cast<const uint32_t*>(blk + 8);
-        const uint32_t s2 = *reinterpret_cast<const uint32_t*>(blk + 12);
-        const uint64_t raw = *reinterpret_cast<const uint64_t*>(blk + 16 + 32 * j + 8 * (lane >> 4));
+    struct Raw {
+        uint64_t q;
+        uint32_t dd, s0, s1, s2;
+        uint32_t sub;
+    };
+    struct Ptr {
+        const uint8_t* row;  // the lane's row
+        uint32_t kq;         // byte offset of the lane's 8 bytes in a 32-byte qs slice
+    };
+    __device__ __forceinline__ Ptr at(uint32_t g, int lane) const {
+        uint32_t row = g * 16 + (lane & 15);
+        row = row < rows ? row : 0;
+        return {w + static_cast<size_t>(row) * nsb * 144, 8u * static_cast<uint32_t>(lane >> 4)};
+    }
+    __device__ __forceinline__ void load(const Ptr& p, uint32_t b, Raw& r) const {
+        const uint8_t* blk = p.row + (b / 8) * 144;
+        r.sub = b % 8;
+        r.dd = *reinterpret_cast<const uint32_t*>(blk);
+        r.s0 = *reinterpret_cast<const uint32_t*>(blk + 4);
+        r.s1 = *reinterpret_cast<const uint32_t*>(blk + 8);
+        r.s2 = *reinterpret_cast<const uint32_t*>(blk + 12);
+        r.q = *reinterpret_cast<const uint64_t*>(blk + 16 + 32 * (r.sub / 2) + p.kq);
+    }
+    __device__ __forceinline__ void decode(const Raw& r, uint32_t row, uint64_t& q, float& d, float& m) const {
+        const uint32_t sub = r.sub;
         const auto byte = [&](uint32_t i) -> uint32_t {
-            const uint32_t word = i < 4 ? s0 : (i < 8 ? s1 : s2);
+            const uint32_t word = i < 4 ? r.s0 : (i < 8 ? r.s1 : r.s2);
             return (word >> (8 * (i % 4))) & 0xff;
         };
         uint32_t sc, mn;
@@ -149,16 +197,18 @@ struct WQ4K {
             sc = (byte(sub + 4) & 0xF) | ((byte(sub - 4) >> 6) << 4);
             mn = (byte(sub + 4) >> 4) | ((byte(sub) >> 6) << 4);
         }
-        d = f16_bits_to_f32(static_cast<uint16_t>(dd & 0xffff)) * static_cast<float>(sc);
-        m = f16_bits_to_f32(static_cast<uint16_t>(dd >> 16)) * static_cast<float>(mn);
-        q = (sub & 1) ? ((raw >> 4) & 0x0f0f0f0f0f0f0f0full) : (raw & 0x0f0f0f0f0f0f0f0full);
+        const bool ok = row < rows;
+        d = ok ? f16_bits_to_f32(static_cast<uint16_t>(r.dd & 0xffff)) * static_cast<float>(sc) : 0.f;
+        m = ok ? f16_bits_to_f32(static_cast<uint16_t>(r.dd >> 16)) * static_cast<float>(mn) : 0.f;
+        q = ok ? ((sub & 1) ? ((r.q >> 4) & 0x0f0f0f0f0f0f0f0full) : (r.q & 0x0f0f0f0f0f0f0f0full)) : 0;
     }
 };
 
 // ---------------------------------------------------------------- activations
 
-// x rows: token m reads row (rows ? rows[m] : m) of a [*, ldx] f32 matrix. With
-// norm_w set, the row is RMS-normalised first: x / sqrt(mean(x^2) + eps) * w
+// x rows: token m reads row (rows ? rows[m] : m) of a [*, ldx] f32 matrix, or, with
+// tiled set, of the tiled activation order (act_tile_off, K = in). With norm_w set,
+// the row is RMS-normalised first: x / sqrt(mean(x^2) + eps) * w
 // (Model::rmsnorm, src/model.rs:653-659).
 struct XIn {
     const float* x;
@@ -168,9 +218,16 @@ struct XIn {
     uint32_t ldx;
     uint32_t T;
     uint32_t in;
-    __device__ __forceinline__ const float* row(uint32_t m) const {
-        return x + static_cast<size_t>(rows ? static_cast<uint32_t>(rows[m]) : m) * ldx;
+    uint32_t tiled = 0;
+    // lane's pointer to columns 8 kq .. of token m, block 0; block b adds b *
+    // bstride(), the second half of the 8 columns hoff()
+    __device__ __forceinline__ const float* lane_ptr(uint32_t m, int kq) const {
+        const uint32_t r = rows ? static_cast<uint32_t>(rows[m]) : m;
+        if (tiled) return x + act_tile_off(r, 8u * kq, in / 32);
+        return x + static_cast<size_t>(r) * ldx + 8 * kq;
     }
+    __device__ __forceinline__ uint32_t bstride() const { return tiled ? 512u : 32u; }
+    __device__ __forceinline__ uint32_t hoff() const { return tiled ? 256u : 4u; }
 };
 
 // ---------------------------------------------------------------- the kernel
@@ -210,7 +267,8 @@ __global__ __launch_bounds__(KS * kWave) void q8_gemm_kernel(WL wl, XIn xa, Epi 
     static_assert(NG * MT <= 8 && NC <= KS, "partial sums must fit 64 KB of LDS");
     __shared__ floatx4 s_part[KS][NG][MT][kWave];
     __shared__ float s_ss[KS][MT][16];
-    const int lane = threadIdx.x & (kWave - 1), wv = threadIdx.x / kWave;
+    // the wave index is uniform: keep it (and every block index) in scalar registers
+    const int lane = threadIdx.x & (kWave - 1), wv = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
     const int kq = lane >> 4, mm = lane & 15;
     const uint32_t u0 = blockIdx.x * NU;
     const uint32_t t0 = blockIdx.y * 16 * MT;
@@ -224,14 +282,19 @@ __global__ __launch_bounds__(KS * kWave) void q8_gemm_kernel(WL wl, XIn xa, Epi 
         g[EG * j] = ga;
         if constexpr (EG == 2) g[EG * j + 1] = gb;
     }
+    typename WL::Ptr wp[NG];
+#pragma unroll
+    for (int n = 0; n < NG; ++n) wp[n] = wl.at(g[n], lane);
+    // a lane's x row (tokens past T repeat the tile's first token: their products
+    // land in accumulator rows that are never stored) at its k-chunk
     const float* xr[MT];
-    bool mok[MT];
 #pragma unroll
     for (int i = 0; i < MT; ++i) {
         const uint32_t m = t0 + 16 * i + mm;
-        mok[i] = m < xa.T;
-        xr[i] = xa.row(mok[i] ? m : t0);
+        xr[i] = xa.lane_ptr(m < xa.T ? m : t0, kq);
     }
+    const float* nr = NORM ? xa.norm_w + 8 * kq : nullptr;
+    const uint32_t xbs = xa.bstride(), xho = xa.hoff();
     // wave c < NC stores combination c = (tile c % MT, unit c / MT); the epilogue's
     // own operands (residual rows, RoPE tables, slots) are requested now, so their
     // latency hides under the main loop
@@ -249,8 +312,7 @@ __global__ __launch_bounds__(KS * kWave) void q8_gemm_kernel(WL wl, XIn xa, Epi 
         ss[i] = 0.f;
     }
     for (uint32_t b0 = wv; b0 < nb; b0 += KS * U) {
-        uint64_t q[NG][U];
-        float d[NG][U], mn[NG][U];
+        typename WL::Raw raw[NG][U];
         float4 xv[U][MT][2], nv[U][2];
         bool live[U];
 #pragma unroll
@@ -258,16 +320,16 @@ __global__ __launch_bounds__(KS * kWave) void q8_gemm_kernel(WL wl, XIn xa, Epi 
             live[u] = b0 + u * KS < nb;
             const uint32_t b = live[u] ? b0 + u * KS : nb - 1;
 #pragma unroll
-            for (int n = 0; n < NG; ++n) wl.load(g[n], b, lane, q[n][u], d[n][u], mn[n][u]);
-            const uint32_t k = 32 * b + 8 * kq;
+            for (int n = 0; n < NG; ++n) wl.load(wp[n], b, raw[n][u]);
+            const uint32_t k = 32 * b;
 #pragma unroll
             for (int i = 0; i < MT; ++i) {
-                xv[u][i][0] = *reinterpret_cast<const float4*>(xr[i] + k);
-                xv[u][i][1] = *reinterpret_cast<const float4*>(xr[i] + k + 4);
+                xv[u][i][0] = *reinterpret_cast<const float4*>(xr[i] + b * xbs);
+                xv[u][i][1] = *reinterpret_cast<const float4*>(xr[i] + b * xbs + xho);
             }
             if constexpr (NORM) {
-                nv[u][0] = *reinterpret_cast<const float4*>(xa.norm_w + k);
-                nv[u][1] = *reinterpret_cast<const float4*>(xa.norm_w + k + 4);
+                nv[u][0] = *reinterpret_cast<const float4*>(nr + k);
+                nv[u][1] = *reinterpret_cast<const float4*>(nr + k + 4);
             } else {
                 nv[u][0] = nv[u][1] = make_float4(0.f, 0.f, 0.f, 0.f);
             }
@@ -279,11 +341,14 @@ __global__ __launch_bounds__(KS * kWave) void q8_gemm_kernel(WL wl, XIn xa, Epi 
         for (int u = 0; u < U; ++u) {
             // a repeated block contributes nothing: zero scale and min, no squares
             bf16x8 w[NG];
+            float d[NG], mn[NG];
 #pragma unroll
             for (int n = 0; n < NG; ++n) {
-                d[n][u] = live[u] ? d[n][u] : 0.f;
-                mn[n][u] = live[u] ? mn[n][u] : 0.f;
-                w[n] = i8x8_to_bf16(q[n][u]);
+                uint64_t qb;
+                wl.decode(raw[n][u], g[n] * 16 + mm, qb, d[n], mn[n]);
+                d[n] = live[u] ? d[n] : 0.f;
+                mn[n] = live[u] ? mn[n] : 0.f;
+                w[n] = i8x8_to_bf16(qb);
             }
             const float sq = live[u] ? 1.f : 0.f;
             const float nw[8] = {nv[u][0].x, nv[u][0].y, nv[u][0].z, nv[u][0].w,
@@ -292,10 +357,7 @@ __global__ __launch_bounds__(KS * kWave) void q8_gemm_kernel(WL wl, XIn xa, Epi 
             for (int i = 0; i < MT; ++i) {
                 float xs[8] = {xv[u][i][0].x, xv[u][i][0].y, xv[u][i][0].z, xv[u][i][0].w,
                                xv[u][i][1].x, xv[u][i][1].y, xv[u][i][1].z, xv[u][i][1].w};
-                if (!mok[i]) {
-#pragma unroll
-                    for (int j = 0; j < 8; ++j) xs[j] = 0.f;
-                } else if constexpr (NORM) {
+                if constexpr (NORM) {
                     float s2 = 0.f;
 #pragma unroll
                     for (int j = 0; j < 8; ++j) {
@@ -319,9 +381,9 @@ __global__ __launch_bounds__(KS * kWave) void q8_gemm_kernel(WL wl, XIn xa, Epi 
                     floatx4 t = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a.hi, w[n], z, 0, 0, 0);
                     t = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a.lo, w[n], t, 0, 0, 0);
                     if constexpr (WL::kHasMin)
-                        acc[n][i] += d[n][u] * t - mn[n][u] * sx;
+                        acc[n][i] += d[n] * t - mn[n] * sx;
                     else
-                        acc[n][i] += d[n][u] * t;
+                        acc[n][i] += d[n] * t;
                 }
             }
         }
@@ -366,12 +428,17 @@ __global__ __launch_bounds__(KS * kWave) void q8_gemm_kernel(WL wl, XIn xa, Epi 
 
 // y[m][row] (= or +=) for rows < rows. NG = 2: pair p = groups 2p, 2p+1; NG = 1:
 // workgroup p owns group p alone (twice the workgroups, half the bytes each).
+// tiled: y is in the tiled activation order with K = rows (a multiple of 32).
 template <bool ADD, int NG = 2>
 struct EpiStore {
     static constexpr int kGroups = NG;
     float* y;
     uint32_t ldy;
     uint32_t rows;
+    uint32_t tiled = 0;
+    __device__ __forceinline__ size_t at(uint32_t m, uint32_t r) const {
+        return tiled ? act_tile_off(m, r, rows / 32) : static_cast<size_t>(m) * ldy + r;
+    }
     __device__ __forceinline__ void groups(uint32_t p, uint32_t& g0, uint32_t& g1) const {
         g0 = NG * p;
         g1 = NG * p + 1;
@@ -387,9 +454,8 @@ struct EpiStore {
             for (int i = 0; i < 4; ++i) {
                 const uint32_t m = m0 + i;
                 if (m >= T) break;
-                const float* yr = y + static_cast<size_t>(m) * ldy;
-                if (r0 < rows) r.a0[i] = yr[r0];
-                if (NG == 2 && r1 < rows) r.a1[i] = yr[r1];
+                if (r0 < rows) r.a0[i] = y[at(m, r0)];
+                if (NG == 2 && r1 < rows) r.a1[i] = y[at(m, r1)];
             }
         }
         return r;
@@ -401,9 +467,8 @@ struct EpiStore {
         for (int r = 0; r < 4; ++r) {
             const uint32_t m = m0 + r;
             if (m >= T) break;
-            float* yr = y + static_cast<size_t>(m) * ldy;
-            if (r0 < rows) yr[r0] = ADD ? pr.a0[r] + v0[r] : v0[r];
-            if (NG == 2 && r1 < rows) yr[r1] = ADD ? pr.a1[r] + v1[r] : v1[r];
+            if (r0 < rows) y[at(m, r0)] = ADD ? pr.a0[r] + v0[r] : v0[r];
+            if (NG == 2 && r1 < rows) y[at(m, r1)] = ADD ? pr.a1[r] + v1[r] : v1[r];
         }
     }
 };
@@ -416,6 +481,7 @@ struct EpiSwiGLU {
     float* h;
     uint32_t ldh;
     uint32_t inter;
+    uint32_t tiled = 0;  // h in the tiled activation order (K = inter, a multiple of 32)
     __device__ __forceinline__ void groups(uint32_t p, uint32_t& g0, uint32_t& g1) const {
         g0 = 2 * p;
         g1 = 2 * p + 1;
@@ -430,7 +496,8 @@ struct EpiSwiGLU {
         for (int r = 0; r < 4; ++r) {
             const uint32_t m = m0 + r;
             if (m >= T) break;
-            h[static_cast<size_t>(m) * ldh + j] = g[r] / (1.0f + expf(-g[r])) * u[r];
+            const size_t at = tiled ? act_tile_off(m, j, inter / 32) : static_cast<size_t>(m) * ldh + j;
+            h[at] = g[r] / (1.0f + expf(-g[r])) * u[r];
         }
     }
 };
@@ -609,7 +676,7 @@ struct SingleGroup {
 template <bool ADD>
 struct SingleGroup<EpiStore<ADD, 2>> {
     static constexpr bool kOk = true;
-    static EpiStore<ADD, 1> make(const EpiStore<ADD, 2>& e) { return {e.y, e.ldy, e.rows}; }
+    static EpiStore<ADD, 1> make(const EpiStore<ADD, 2>& e) { return {e.y, e.ldy, e.rows, e.tiled}; }
 };
 
 // Units per workgroup for 16-token tiles. At these sizes a product's time follows
