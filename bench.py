@@ -238,34 +238,20 @@ def gemv_bench(ctx, torch, K, oracle_mod, quick):
     return out
 
 
-def config5_workload(seed=0x5EED0005, num_requests=64, rate=40.0, step_secs=0.005):
-    """Config 5 requests: prompt lengths log-uniform [16, 2048], generation lengths
-    uniform [32, 512], Poisson arrivals at `rate` requests/s mapped to steps of
-    `step_secs` (the reference's sweep constants, src/bench/traffic.rs:5-9, 153-160),
-    synthetic prompts (req*10 + p) % 30 (src/bench.rs:470-474). numpy PCG64 seeded."""
-    from kanso_infer_amd.engine import generate_poisson_schedule, schedule_to_trace
-    rng = np.random.default_rng(seed)
-    plen = np.rint(np.exp(rng.uniform(np.log(16), np.log(2048), num_requests))).astype(int)
-    glen = rng.integers(32, 513, num_requests)
-    sched = generate_poisson_schedule(num_requests, rate, seed + 1)
-    return schedule_to_trace(sched, plen, glen, step_secs)
-
-
 def engine_bench(ctx, K, torch, num_requests=64, kv_dtype=0):
     """Config 5: SmolLM2-360M-architecture random-init model (32 layers, Q8_0 weights
     N(0, 0.02^2), tied embeddings, F32 KV) under the C++ continuous-batching engine:
     512-token budget, max_running 64, block size 16, greedy. Value = generated
     tokens / wall seconds of the whole run (execute_engine_run, src/bench.rs:447-537).
     kv_dtype != 0: the same run on a 1-byte pool (Engine::new_with_budget_and_kv)."""
+    from kanso_infer_amd import workloads
     from kanso_infer_amd.engine import Engine, Model, ModelConfig, run_benchmark_workload
     cfg = ModelConfig.smollm2_360m(max_position=4096)
     t0 = time.perf_counter()
     model = Model(ctx, cfg)
     model.init_random(seed=0x5EED0057, std=0.02)
-    reqs = config5_workload(num_requests=num_requests)
-    max_tokens = max(r.prompt_len + r.gen_len for r in reqs)
-    blocks_per_seq = -(-max_tokens // 16) + 1  # create_engine_for_model_profile, src/bench.rs:598-614
-    total_blocks = max(blocks_per_seq * len(reqs), 128)
+    reqs = workloads.config5_workload(num_requests=num_requests)
+    total_blocks = workloads.config5_total_blocks(reqs)
     model.alloc_kv(total_blocks, 16, 512, 65, kv_dtype=kv_dtype)
     log(f"config5: model ready in {time.perf_counter() - t0:.1f} s, {total_blocks} KV blocks")
     # warm-up on a throwaway engine (same model and pool), so first-call costs stay out
@@ -305,6 +291,7 @@ def engine_bench(ctx, K, torch, num_requests=64, kv_dtype=0):
         "decode_ms_per_step": round(rep["decode_ms_per_step"], 3),
         "max_sequences_per_step": acc["max_batch"],
         "checksum_fnv1a64": f"{rep['checksum']:016x}",
+        "checksum_oracle": config5_oracle_fixture(rep["generated"]) if kv_dtype == 0 and num_requests == 64 else None,
         "prefix_hit_rate": round(rep["prefix_hit_rate"], 4),
         "bytes_read_per_step": int(step_bytes / max(acc["steps_with_work"], 1)),
         "hbm_frac": round(step_bytes / rep["total_duration_secs"] / HBM_PEAK, 4),
@@ -409,6 +396,24 @@ def config5_cpu_baseline(threads=None):
     return dict(value=round(S / el, 2), unit="tokens/s", cores=threads, kind="port",
                 sample=f"one decode step, 16 sequences, contexts U[128,1024] (mean {ctx.mean():.0f}), "
                        f"32 layers, {el:.1f} s on {threads} threads (setup {setup:.1f} s)")
+
+
+def config5_oracle_fixture(generated):
+    """The oracle engine's token stream of this very run (32 layers, the 64-request
+    trace, budget 512, the same init weights), committed by
+    tests/golden/make_config5_checksum.py, against the GPU run's tokens."""
+    path = ROOT / "tests" / "golden" / "config5_oracle.json"
+    if not path.exists():
+        return dict(available=False, reason=f"{path.name} not generated")
+    info = json.loads(path.read_text())
+    want = np.load(path.with_name("config5_oracle_tokens.npy"))
+    got = np.asarray(generated, np.uint32)
+    n = min(got.size, want.size)
+    diff = np.flatnonzero(got[:n] != want[:n])
+    return dict(oracle=info["checksum"], match=bool(got.size == want.size and diff.size == 0),
+                tokens=int(want.size), first_difference=int(diff[0]) if diff.size else None,
+                workload="the full config-5 run: 32 layers, 64 requests, budget 512 (oracle engine on the "
+                         "host restatement of kanso_model_init_random's weights)")
 
 
 def config5_checksum_parity(ctx, K, torch, kv_dtype=0):

@@ -386,11 +386,23 @@ int kanso_model_destroy(kanso_model* model);
 int kanso_model_set_weight(kanso_model* model, uint32_t kind, uint32_t layer,
                            const void* host_data, size_t bytes);
 
-/* Random-init weights generated on the device: every matrix N(0, std^2) from this
- * build's counter-based generator (splitmix64 + Box-Muller), quantized to Q8_0 by
- * the rule of kanso_quantize_q8_0; norms = 1 (create_mock_*, src/model.rs:520-651,
- * with SmolLM2's std of 0.02 in place of N(0,1)). */
+/* Random-init weights generated on the device (create_mock_*, src/model.rs:520-651,
+ * with SmolLM2's std of 0.02 in place of N(0,1)): matrix j (embedding 1, untied
+ * lm_head 2, then per layer Q, K, V, O, gate, up, down) draws element i from
+ * splitmix64(seed_j ^ (i * 0xd1342543de82ef95)), seed_j = seed * 0x100000001b3 +
+ * j * 0x9e3779b97f4a7c15 (mod 2^64): the sum s of the hash's four 16-bit fields
+ * minus 131070 (an Irwin-Hall(4) draw with mean 0) times
+ * c = (float)(std * sqrt(3) / 65536), one f32 multiply. Matrices are then quantized
+ * to Q8_0 by the rule of kanso_quantize_q8_0; norms = 1. Every value is an exact
+ * integer times one rounding, so a host restatement reproduces the weights bit
+ * for bit. */
 int kanso_model_init_random(kanso_model* model, uint64_t seed, float std);
+
+/* Reads one weight back to host memory in kanso_model_set_weight's format (GGUF
+ * Q8_0 bytes of a matrix, f32 norm vectors). No reference counterpart: the
+ * reference keeps its weights in host tensors (src/weights.rs:33-45). */
+int kanso_model_get_weight(kanso_model* model, uint32_t kind, uint32_t layer, void* host_out,
+                           size_t bytes);
 
 /* Allocates the F32 KV pool: num_blocks blocks of block_size tokens per layer, and
  * step buffers for up to max_tokens rows and max_seqs sequences per forward. */

@@ -169,6 +169,7 @@ SIGNATURES: dict[str, tuple] = {
     "kanso_model_destroy": (_I, [_P]),
     "kanso_model_set_weight": (_I, [_P, _U, _U, _P, C.c_size_t]),
     "kanso_model_init_random": (_I, [_P, C.c_uint64, C.c_float]),
+    "kanso_model_get_weight": (_I, [_P, _U, _U, _P, C.c_size_t]),
     "kanso_model_alloc_kv": (_I, [_P, _U, _U, _U, _U]),
     "kanso_model_alloc_kv_quant": (_I, [_P, _U, _U, _U, _U, _U]),
     "kanso_model_kv_pool": (_I, [_P, _U, C.POINTER(_P), C.POINTER(_P)]),

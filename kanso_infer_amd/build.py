@@ -55,14 +55,20 @@ def _run(cmd: list[str], cwd: Path | None = None) -> None:
             sys.stderr.write(line + "\n")
 
 
-def build_hip(jobs: int = 8) -> Path:
+def build_hip(jobs: int = 8, incremental: bool = False) -> Path:
+    """Compiles every HIP source (incremental: only those whose object is older than
+    the source or any header) and links the library."""
     BUILD.mkdir(exist_ok=True)
     sources = sorted(CSRC.glob("*.hip"))
     if not sources:
         raise RuntimeError(f"no HIP sources under {CSRC}")
+    headers = [*CSRC.glob("*.hpp"), *(ROOT / "include").glob("*.h")]
+    newest_header = max((h.stat().st_mtime for h in headers), default=0.0)
 
     def compile_one(src: Path) -> Path:
         obj = BUILD / (src.stem + ".o")
+        if incremental and obj.exists() and obj.stat().st_mtime > max(src.stat().st_mtime, newest_header):
+            return obj
         _run([HIPCC, *HIP_FLAGS, "-c", str(src), "-o", str(obj)])
         return obj
 
@@ -87,9 +93,11 @@ def main(argv: list[str] | None = None) -> None:
     ap.add_argument("--hip-only", action="store_true")
     ap.add_argument("--oracle-only", action="store_true")
     ap.add_argument("-j", type=int, default=8)
+    ap.add_argument("--incremental", action="store_true",
+                    help="recompile only sources older than their object (or a header)")
     args = ap.parse_args(argv)
     if not args.oracle_only:
-        print(build_hip(args.j))
+        print(build_hip(args.j, args.incremental))
     if not args.hip_only:
         print(build_oracle())
 

@@ -24,13 +24,43 @@ __device__ __forceinline__ uint64_t splitmix64(uint64_t x) {
     return x ^ (x >> 31);
 }
 
-// N(0, std^2) from one 64-bit hash: two 24-bit uniforms, Box-Muller cosine branch.
-__global__ void randn_kernel(float* out, uint64_t n, uint64_t seed, float std) {
+// Random-init value i of a stream: four 16-bit fields of one splitmix64 hash summed
+// (an Irwin-Hall(4) variate: mean 0, bell-shaped, within +-3.46 standard
+// deviations) and scaled by c = std * sqrt(3) / 65536. The sum is an exact integer
+// (|s| <= 131070) and the scale is one IEEE multiply, so the host restatement
+// computes every value bit for bit (a Box-Muller draw would depend on the device's
+// log / cos, which differ from the host's in the last bits).
+__global__ void randn_kernel(float* out, uint64_t n, uint64_t seed, float c) {
     for (uint64_t i = blockIdx.x * 256ull + threadIdx.x; i < n; i += static_cast<uint64_t>(gridDim.x) * 256) {
         const uint64_t h = splitmix64(seed ^ (i * 0xd1342543de82ef95ull));
-        const float u1 = (static_cast<float>(h >> 40) + 1.0f) * (1.0f / 16777216.0f);
-        const float u2 = static_cast<float>(h & 0xffffff) * (1.0f / 16777216.0f);
-        out[i] = std * sqrtf(-2.0f * logf(u1)) * cosf(6.283185307179586f * u2);
+        const int32_t s = static_cast<int32_t>((h & 0xffff) + ((h >> 16) & 0xffff) + ((h >> 32) & 0xffff) + (h >> 48)) -
+                          131070;
+        out[i] = static_cast<float>(s) * c;
+    }
+}
+
+// Scale of randn_kernel for a standard deviation (host f64 arithmetic, one rounding).
+float randn_scale(float std) { return static_cast<float>(static_cast<double>(std) * 1.7320508075688772 / 65536.0); }
+
+// One thread per (group, block, lane) of a packed matrix: the inverse of
+// kanso_q8_0_pack (GGUF [rows][in/32] blocks from the packed tiles).
+__global__ __launch_bounds__(256) void unpack_q8_0_kernel(const uint8_t* __restrict__ src, uint32_t rows,
+                                                          uint32_t nb, uint8_t* __restrict__ dst, uint32_t stride,
+                                                          uint32_t offset) {
+    const uint64_t total = static_cast<uint64_t>((rows + 15) / 16) * nb * 64;
+    for (uint64_t e = blockIdx.x * 256ull + threadIdx.x; e < total; e += static_cast<uint64_t>(gridDim.x) * 256) {
+        const uint32_t lane = static_cast<uint32_t>(e % 64);
+        const uint32_t b = static_cast<uint32_t>((e / 64) % nb);
+        const uint32_t g = static_cast<uint32_t>(e / (64ull * nb));
+        const uint32_t row = g * 16 + (lane & 15);
+        if (row >= rows) continue;
+        const uint8_t* tile = src + (static_cast<size_t>(g * stride + offset) * nb + b) * 544;
+        uint8_t* blk = dst + (static_cast<size_t>(row) * nb + b) * 34;
+        for (int j = 0; j < 8; ++j) blk[2 + 8 * (lane >> 4) + j] = tile[8 * lane + j];
+        if (lane < 16) {
+            blk[0] = tile[512 + 2 * lane];
+            blk[1] = tile[512 + 2 * lane + 1];
+        }
     }
 }
 
@@ -571,7 +601,7 @@ int kanso_model_init_random(kanso_model* m, uint64_t seed, float std) {
         if (!matrix_slot(m, kind, layer, ms)) return KANSO_E_INVALID_ARG;
         const uint64_t n = static_cast<uint64_t>(ms.rows) * ms.in;
         const uint64_t sd = seed * 0x100000001b3ull + (++stream_id) * 0x9e3779b97f4a7c15ull;
-        hipLaunchKernelGGL(randn_kernel, dim3(grid_for(n)), dim3(256), 0, nullptr, f, n, sd, std);
+        hipLaunchKernelGGL(randn_kernel, dim3(grid_for(n)), dim3(256), 0, nullptr, f, n, sd, randn_scale(std));
         hipLaunchKernelGGL(quantize_q8_0_kernel, dim3(grid_for(n / 32)), dim3(256), 0, nullptr, f, n / 32, g);
         KANSO_LAUNCH_CHECK();
         return kanso_q8_0_pack(m->ctx, g, ms.rows, ms.in, ms.dst, ms.stride, ms.offset, nullptr);
@@ -600,6 +630,46 @@ int kanso_model_init_random(kanso_model* m, uint64_t seed, float std) {
         return KANSO_E_HIP;
     }
     return rc;
+}
+
+int kanso_model_get_weight(kanso_model* m, uint32_t kind, uint32_t layer, void* host_out, size_t bytes) {
+    int rc = model_check(m, "kanso_model_get_weight");
+    if (rc) return rc;
+    if (!host_out) {
+        set_error("kanso_model_get_weight: null output");
+        return KANSO_E_INVALID_ARG;
+    }
+    if (float* nw = norm_slot(m, kind, layer)) {
+        if (bytes != m->cfg.hidden * sizeof(float)) {
+            set_error("kanso_model_get_weight: norm of %zu bytes, expected %zu", bytes, m->cfg.hidden * sizeof(float));
+            return KANSO_E_INVALID_SHAPE;
+        }
+        KANSO_HIP_TRY(hipMemcpy(host_out, nw, bytes, hipMemcpyDeviceToHost));
+        return KANSO_OK;
+    }
+    MatrixSlot ms;
+    if ((kind == KANSO_W_LM_HEAD && m->cfg.tied_embeddings) || !matrix_slot(m, kind, layer, ms)) {
+        set_error("kanso_model_get_weight: kind %u / layer %u not a weight of this model", kind, layer);
+        return KANSO_E_INVALID_ARG;
+    }
+    const size_t want = static_cast<size_t>(ms.rows) * (ms.in / 32) * 34;
+    if (bytes != want) {
+        set_error("kanso_model_get_weight: kind %u has %zu bytes, expected %zu", kind, want, bytes);
+        return KANSO_E_INVALID_SHAPE;
+    }
+    void* tmp = nullptr;
+    KANSO_HIP_TRY(hipMalloc(&tmp, bytes));
+    const uint64_t total = static_cast<uint64_t>((ms.rows + 15) / 16) * (ms.in / 32) * 64;
+    hipLaunchKernelGGL(unpack_q8_0_kernel, dim3(grid_for(total)), dim3(256), 0, nullptr, ms.dst, ms.rows, ms.in / 32,
+                       static_cast<uint8_t*>(tmp), ms.stride, ms.offset);
+    hipError_t e = hipGetLastError();
+    if (e == hipSuccess) e = hipMemcpy(host_out, tmp, bytes, hipMemcpyDeviceToHost);
+    (void)hipFree(tmp);
+    if (e != hipSuccess) {
+        set_error("kanso_model_get_weight: %s", hipGetErrorString(e));
+        return KANSO_E_HIP;
+    }
+    return KANSO_OK;
 }
 
 int kanso_model_alloc_kv_quant(kanso_model* m, uint32_t num_blocks, uint32_t block_size, uint32_t max_tokens,

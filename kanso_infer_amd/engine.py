@@ -150,6 +150,30 @@ class Model:
     def init_random(self, seed: int = 0x5EED0057, std: float = 0.02) -> None:
         _check(self._lib.kanso_model_init_random(self.handle, seed, std))
 
+    def get_weight(self, kind: int, layer: int = 0) -> np.ndarray:
+        """One weight back on the host: GGUF Q8_0 bytes of a matrix (uint8), or an f32
+        norm vector."""
+        c = self.config
+        if kind in (_capi.KANSO_W_FINAL_NORM, _capi.KANSO_W_ATTN_NORM, _capi.KANSO_W_FFN_NORM):
+            out = np.empty(c.hidden_size, np.float32)
+        else:
+            hd = c.head_dim
+            rows, cols = {
+                _capi.KANSO_W_EMBED: (c.vocab_size, c.hidden_size),
+                _capi.KANSO_W_LM_HEAD: (c.vocab_size, c.hidden_size),
+                _capi.KANSO_W_Q: (c.num_attention_heads * hd, c.hidden_size),
+                _capi.KANSO_W_K: (c.num_key_value_heads * hd, c.hidden_size),
+                _capi.KANSO_W_V: (c.num_key_value_heads * hd, c.hidden_size),
+                _capi.KANSO_W_O: (c.hidden_size, c.num_attention_heads * hd),
+                _capi.KANSO_W_GATE: (c.intermediate_size, c.hidden_size),
+                _capi.KANSO_W_UP: (c.intermediate_size, c.hidden_size),
+                _capi.KANSO_W_DOWN: (c.hidden_size, c.intermediate_size),
+            }[kind]
+            out = np.empty(rows * cols // 32 * 34, np.uint8)
+        _check(self._lib.kanso_model_get_weight(self.handle, kind, layer,
+                                                out.ctypes.data_as(C.c_void_p), out.nbytes))
+        return out
+
     def alloc_kv(self, num_blocks: int, block_size: int, max_tokens: int, max_seqs: int,
                  kv_dtype: int = 0) -> None:
         """The paged KV pool; kv_dtype (KANSO_KV_*) as Engine::new_with_budget_and_kv's

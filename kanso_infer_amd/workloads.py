@@ -158,3 +158,34 @@ def small_mixed(seed: int, num_decodes: int = 5, num_chunks: int = 2, num_heads:
     return AttnBatch(q_lens, ctx, tables, nb, num_heads=num_heads, num_kv_heads=num_kv_heads,
                      head_dim=head_dim, block_size=block_size,
                      scale=1.0 / float(np.sqrt(head_dim)), label=f"small_mixed[{seed}]")
+
+
+# Config 5: the engine run's request trace and its model / pool settings
+# (create_engine_for_model_profile, src/bench.rs:598-614).
+CONFIG5_SEED = 0x5EED0005
+CONFIG5_WEIGHT_SEED = 0x5EED0057
+CONFIG5_STD = 0.02
+CONFIG5_BUDGET = 512
+CONFIG5_MAX_RUNNING = 64
+
+
+def config5_workload(seed: int = CONFIG5_SEED, num_requests: int = 64, rate: float = 40.0,
+                     step_secs: float = 0.005) -> list:
+    """Config 5 requests: prompt lengths log-uniform [16, 2048], generation lengths
+    uniform [32, 512], Poisson arrivals at `rate` requests/s mapped to steps of
+    `step_secs` (the reference's sweep constants, src/bench/traffic.rs:5-9, 153-160),
+    synthetic prompts (req*10 + p) % 30 (src/bench.rs:470-474). numpy PCG64 seeded."""
+    from .engine import generate_poisson_schedule, schedule_to_trace
+    rng = np.random.default_rng(seed)
+    plen = np.rint(np.exp(rng.uniform(np.log(16), np.log(2048), num_requests))).astype(int)
+    glen = rng.integers(32, 513, num_requests)
+    sched = generate_poisson_schedule(num_requests, rate, seed + 1)
+    return schedule_to_trace(sched, plen, glen, step_secs)
+
+
+def config5_total_blocks(requests: list, block_size: int = BLOCK_SIZE) -> int:
+    """Pool size of the config-5 engine: one sequence's worst case plus a block, per
+    request (src/bench.rs:598-614), at least 128."""
+    max_tokens = max(r.prompt_len + r.gen_len for r in requests)
+    blocks_per_seq = -(-max_tokens // block_size) + 1
+    return max(blocks_per_seq * len(requests), 128)

@@ -125,6 +125,14 @@ void oracle_quantize_row_q4_k(const float* x, uint32_t n, void* blocks);
 
 /* ---- decoder glue (config 5) -------------------------------------------- */
 
+/* kanso_model_init_random restated (include/kanso_hip.h): splitmix64 (the
+ * published output function), the Irwin-Hall(4) draw of one hash times
+ * c = oracle_randn_scale(std), then oracle_quantize_row_q8_0 per row. Writes GGUF
+ * Q8_0 bytes [rows][cols/32]. */
+uint64_t oracle_splitmix64(uint64_t x);
+float oracle_randn_scale(float std_dev);
+int oracle_init_random_q8_0(uint64_t stream_seed, uint32_t rows, uint32_t cols, float c, void* gguf_out);
+
 /* Model::rmsnorm (src/model.rs:653-659): x / sqrt(mean(x^2) + eps) * w, rows of n. */
 void oracle_rmsnorm(const float* x, const float* w, float* y, uint32_t rows, uint32_t n,
                     float eps);

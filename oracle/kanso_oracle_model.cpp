@@ -17,6 +17,39 @@
 
 extern "C" {
 
+uint64_t oracle_splitmix64(uint64_t x) {
+    // splitmix64's output function for state x + golden gamma (Steele, Lea & Flood,
+    // "Fast splittable pseudorandom number generators", OOPSLA 2014)
+    x += 0x9e3779b97f4a7c15ull;
+    x = (x ^ (x >> 30)) * 0xbf58476d1ce4e5b9ull;
+    x = (x ^ (x >> 27)) * 0x94d049bb133111ebull;
+    return x ^ (x >> 31);
+}
+
+float oracle_randn_scale(float std_dev) {
+    return static_cast<float>(static_cast<double>(std_dev) * 1.7320508075688772 / 65536.0);
+}
+
+int oracle_init_random_q8_0(uint64_t stream_seed, uint32_t rows, uint32_t cols, float c, void* gguf_out) {
+    // kanso_model_init_random's matrix: element i = (sum of the four 16-bit fields of
+    // splitmix64(seed ^ i * 0xd1342543de82ef95) - 131070) * c, then Q8_0 per row.
+    if (cols % 32 != 0) return -1;
+    std::vector<float> row(cols);
+    uint8_t* out = static_cast<uint8_t*>(gguf_out);
+    for (uint32_t r = 0; r < rows; ++r) {
+        for (uint32_t k = 0; k < cols; ++k) {
+            const uint64_t i = static_cast<uint64_t>(r) * cols + k;
+            const uint64_t h = oracle_splitmix64(stream_seed ^ (i * 0xd1342543de82ef95ull));
+            const int32_t s = static_cast<int32_t>((h & 0xffff) + ((h >> 16) & 0xffff) + ((h >> 32) & 0xffff) +
+                                                   (h >> 48)) -
+                              131070;
+            row[k] = static_cast<float>(s) * c;
+        }
+        oracle_quantize_row_q8_0(row.data(), cols, out + static_cast<size_t>(r) * (cols / 32) * 34);
+    }
+    return 0;
+}
+
 int oracle_forward_batch_rows(const oracle_model_config* cfg, const oracle_model_weights* w,
                               const uint32_t* tokens, const int32_t* positions,
                               const int64_t* slot_mapping, uint32_t T, void* const* k_pools,

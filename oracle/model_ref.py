@@ -34,6 +34,36 @@ def random_weights(cfg: dict, seed: int, std: float = 0.02) -> dict:
     return w
 
 
+def device_init_weights(cfg: dict, seed: int, std: float = 0.02) -> dict:
+    """The weights kanso_model_init_random draws on the device, restated on the host
+    (bit for bit): matrix j (1 = embedding, 2 = untied lm_head, then per layer Q, K,
+    V, O, gate, up, down) uses stream seed seed * 0x100000001b3 + j *
+    0x9e3779b97f4a7c15 mod 2^64; norms are 1."""
+    h, D, I, V = cfg["hidden"], cfg["head_dim"], cfg["intermediate"], cfg["vocab"]
+    H, KV = cfg["num_heads"], cfg["num_kv_heads"]
+    M = 2**64 - 1
+    j = 0
+
+    def mat(rows, cols):
+        nonlocal j
+        j += 1
+        return oracle.init_random_q8_0((seed * 0x100000001b3 + j * 0x9e3779b97f4a7c15) & M,
+                                       rows, cols, std)
+
+    ones = np.ones(h, np.float32)
+    w = {"embed": mat(V, h), "final_norm": ones, "layers": []}
+    if not cfg.get("tied", True):
+        w["lm_head"] = mat(V, h)
+    for _ in range(cfg["num_layers"]):
+        L = {"attn_norm": ones, "ffn_norm": ones}
+        for name, rows, cols in (("wq", H * D, h), ("wk", KV * D, h), ("wv", KV * D, h),
+                                 ("wo", h, H * D), ("w_gate", I, h), ("w_up", I, h),
+                                 ("w_down", h, I)):
+            L[name] = mat(rows, cols)
+        w["layers"].append(L)
+    return w
+
+
 class OracleModel:
     """kv_dtype: the pool kind (oracle.KV_*): F32, or a 1-byte pool whose rows are
     quantized by oracle_kv_append (Engine::new_with_budget_and_kv, src/engine.rs:62-100)."""

@@ -69,12 +69,28 @@ def lib() -> C.CDLL:
             "oracle_silu_mul": (None, [V, V, V, U]),
             "oracle_greedy": (U, [V, U]),
             "oracle_fnv1a_64": (C.c_uint64, [V, C.c_size_t]),
+            "oracle_splitmix64": (C.c_uint64, [C.c_uint64]),
+            "oracle_randn_scale": (F, [F]),
+            "oracle_init_random_q8_0": (I, [C.c_uint64, U, U, F, V]),
         }
         for name, (res, args) in sig.items():
             fn = getattr(_lib, name)
             fn.restype = res
             fn.argtypes = args
     return _lib
+
+
+def splitmix64(x: int) -> int:
+    return int(lib().oracle_splitmix64(x & (2**64 - 1)))
+
+
+def init_random_q8_0(stream_seed: int, rows: int, cols: int, std: float) -> np.ndarray:
+    """kanso_model_init_random's matrix (GGUF Q8_0 bytes, uint8) for one stream seed."""
+    out = np.empty(rows * cols // 32 * 34, np.uint8)
+    c = lib().oracle_randn_scale(std)
+    if lib().oracle_init_random_q8_0(stream_seed & (2**64 - 1), rows, cols, c, _p(out)) != 0:
+        raise ValueError("cols must be a multiple of 32")
+    return out
 
 
 def _f32(a) -> np.ndarray:

@@ -249,3 +249,39 @@ def test_model_from_gguf_matches_oracle(ctx, tmp_path):
         ctx.check_device_status()
         assert_close(host(logits).reshape(S, SMALL["vocab"]), om.logits(plan),
                      what=f"gguf logits step {step}")
+
+
+@pytest.mark.parametrize("tied", [True, False])
+def test_init_random_matches_oracle(ctx, tied):
+    """kanso_model_init_random's weights equal the host restatement
+    (model_ref.device_init_weights) byte for byte: every matrix's GGUF Q8_0 bytes,
+    read back through kanso_model_get_weight, and the unit norms."""
+    cfg = dict(SMALL, tied=tied)
+    mc = ModelConfig(cfg["hidden"], cfg["num_heads"], cfg["num_kv_heads"], cfg["num_layers"],
+                     cfg["intermediate"], cfg["vocab"], max_position=512, tied_embeddings=tied)
+    m = Model(ctx, mc)
+    m.init_random(seed=0x1234, std=0.02)
+    from model_ref import device_init_weights
+    want = device_init_weights(cfg, 0x1234, 0.02)
+    assert np.array_equal(m.get_weight(_capi.KANSO_W_EMBED), want["embed"])
+    if not tied:
+        assert np.array_equal(m.get_weight(_capi.KANSO_W_LM_HEAD), want["lm_head"])
+    assert np.array_equal(m.get_weight(_capi.KANSO_W_FINAL_NORM), want["final_norm"])
+    kinds = {"attn_norm": _capi.KANSO_W_ATTN_NORM, "ffn_norm": _capi.KANSO_W_FFN_NORM,
+             "wq": _capi.KANSO_W_Q, "wk": _capi.KANSO_W_K, "wv": _capi.KANSO_W_V,
+             "wo": _capi.KANSO_W_O, "w_gate": _capi.KANSO_W_GATE, "w_up": _capi.KANSO_W_UP,
+             "w_down": _capi.KANSO_W_DOWN}
+    for li in range(cfg["num_layers"]):
+        for name, kind in kinds.items():
+            assert np.array_equal(m.get_weight(kind, li), want["layers"][li][name]), (li, name)
+    m.close()
+
+
+def test_get_weight_round_trip(ctx):
+    """kanso_model_get_weight returns the bytes kanso_model_set_weight took."""
+    w = random_weights(SMALL, seed=21)
+    m = gpu_model(ctx, SMALL, w, 16, 16)
+    assert np.array_equal(m.get_weight(_capi.KANSO_W_EMBED), w["embed"])
+    assert np.array_equal(m.get_weight(_capi.KANSO_W_V, 1), w["layers"][1]["wv"])
+    assert np.array_equal(m.get_weight(_capi.KANSO_W_FFN_NORM, 0), w["layers"][0]["ffn_norm"])
+    m.close()
