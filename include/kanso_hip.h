@@ -209,6 +209,24 @@ int kanso_ragged_paged_attention(kanso_ctx* ctx, const kanso_ragged_attention_pa
                                  const uint32_t* context_lens, float* out,
                                  kanso_stream_t stream);
 
+/* kanso_ragged_paged_attention without any allocation: the same kernels, with
+ * their split-K partials, statistics and per-row partition counts in a fixed
+ * 64 MiB device array that each GPU holds for the life of the process (its
+ * address is resolved at kanso_create), and no profiling events. A call whose
+ * scratch (rows x heads x partitions x (head_dim + 2) x 4 B, plus 4 B per row)
+ * exceeds 64 MiB is rejected with KANSO_E_INVALID_SHAPE. Every call on one GPU
+ * shares that array: calls that overlap on one GPU (several streams or threads)
+ * race, and must be serialised by the caller. Nothing in the array needs to start
+ * at zero (each call writes before it reads). No counterpart in the reference:
+ * for callers that cannot allocate (code under graph capture, serving loops that
+ * forbid hipMalloc). */
+int kanso_ragged_paged_attention_noalloc(kanso_ctx* ctx, const kanso_ragged_attention_params* p,
+                                         const float* q, const void* k_pool, const void* v_pool,
+                                         const void* k_scales, const void* v_scales,
+                                         const uint32_t* block_tables, const int32_t* cu_seqlens,
+                                         const uint32_t* context_lens, float* out,
+                                         kanso_stream_t stream);
+
 /* Packs one scheduler step on the device (src/engine.rs:376-402 and the padding
  * rule of src/model.rs:64-116). `plan` is a device array of num_seqs entries in plan
  * order; total_q = sum of q_len and max_blocks = max_s ceil((start+q_len)/bs) (at

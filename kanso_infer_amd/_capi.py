@@ -150,6 +150,8 @@ SIGNATURES: dict[str, tuple] = {
     "kanso_ragged_chunk_partition_size": (C.c_uint32, [_P, C.POINTER(RaggedAttentionParamsC), _P, _P]),
     "kanso_ragged_paged_attention": (
         _I, [_P, C.POINTER(RaggedAttentionParamsC), _P, _P, _P, _P, _P, _P, _P, _P, _P, _P]),
+    "kanso_ragged_paged_attention_noalloc": (
+        _I, [_P, C.POINTER(RaggedAttentionParamsC), _P, _P, _P, _P, _P, _P, _P, _P, _P, _P]),
     "kanso_pack_step": (_I, [_P, _P, _U, _P, _P, _U, _U, _U, C.POINTER(PackedStepC), _P]),
     "kanso_kv_append": (_I, [_P, _U, _P, _P, _P, _U, _U, _U, _U, _U, _P, _P, _P, _P, _P]),
     "kanso_kv_reset_blocks": (_I, [_P, _U, _P, _U, _U, _U, _U, _U, _P, _P, _P, _P, _P]),

@@ -47,6 +47,14 @@
 namespace kanso {
 namespace {
 
+// Split-K scratch of kanso_ragged_paged_attention_noalloc: a fixed array in device
+// memory (each GPU holds its own copy for the life of the process). Host code
+// never passes the array's name to a kernel (on the host it is only a stand-in
+// for the symbol): its device address is resolved once per context by
+// noalloc_scratch_init and the kernels take that pointer.
+constexpr size_t kNoAllocScratchBytes = 64ull << 20;
+__device__ __align__(256) unsigned char scratch[kNoAllocScratchBytes];
+
 constexpr int kThreads = 256;
 constexpr int kWaves = kThreads / kWave;
 constexpr float kLog2e = 1.4426950408889634f;
@@ -1497,10 +1505,12 @@ uint32_t host_row_limit(uint32_t ctx_len, uint32_t q_len, uint32_t i, uint32_t c
     return static_cast<uint32_t>(std::min<int64_t>(std::max<int64_t>(lim, 0), cap));
 }
 
+// fixed_scratch: the device address of the fixed scratch array (no allocation, no
+// profiling events); null: the context's grow-only scratch.
 int run_ragged(kanso_ctx* ctx, const kanso_ragged_attention_params* p, const float* q,
                const void* kp, const void* vp, const void* ks, const void* vs,
                const uint32_t* tables, const int32_t* cu, const uint32_t* ctx_lens, float* out,
-               hipStream_t stream, const char* who, bool out_tiled = false) {
+               hipStream_t stream, const char* who, bool out_tiled = false, void* fixed_scratch = nullptr) {
     const uint32_t S = p->num_seqs, H = p->num_heads, HKV = p->num_kv_heads, D = p->head_dim;
     if (!q || !kp || !vp || !tables || !cu || !ctx_lens || !out) {
         set_error("%s: null buffer", who);
@@ -1578,9 +1588,21 @@ int run_ragged(kanso_ctx* ctx, const kanso_ragged_attention_params* p, const flo
     const size_t off_part = align_up(static_cast<size_t>(T) * H * max_parts * sizeof(float2), 256);
     const size_t off_np = align_up(off_part + partial_elems * sizeof(float), 256);
     const size_t total = off_np + static_cast<size_t>(T) * sizeof(uint32_t);
-    int rc = ensure_scratch(ctx, total);
-    if (rc) return rc;
-    char* base = static_cast<char*>(ctx->scratch);
+    int rc = KANSO_OK;
+    char* base = nullptr;
+    if (fixed_scratch) {
+        if (total > kNoAllocScratchBytes) {
+            set_error("%s: this call needs %zu bytes of split-K scratch, above the fixed %zu (fewer rows or "
+                      "partitions, or the allocating entry point)",
+                      who, total, kNoAllocScratchBytes);
+            return KANSO_E_INVALID_SHAPE;
+        }
+        base = static_cast<char*>(fixed_scratch);
+    } else {
+        if ((rc = ensure_scratch(ctx, total))) return rc;
+        base = static_cast<char*>(ctx->scratch);
+    }
+    const bool prof = fixed_scratch == nullptr;  // profiling events come from a pool that grows
 
     AttnArgs a;
     a.q = q;
@@ -1637,19 +1659,19 @@ int run_ragged(kanso_ctx* ctx, const kanso_ragged_attention_params* p, const flo
     }
 
     // nothing in the grid depends on device data
-    hipEvent_t ev;
+    hipEvent_t ev = nullptr;
     const uint32_t grid = main_grid(ctx, T, max_parts, HKV, a.use_mfma != 0);
-    if ((rc = prof_begin(ctx, "attention", stream, &ev))) return rc;
+    if (prof && (rc = prof_begin(ctx, "attention", stream, &ev))) return rc;
     hipLaunchKernelGGL(main_fn, dim3(grid), dim3(kThreads), 0, stream, a);
     KANSO_LAUNCH_CHECK();
-    if ((rc = prof_end(ctx, "attention", stream, ev))) return rc;
+    if (prof && (rc = prof_end(ctx, "attention", stream, ev))) return rc;
     const uint64_t merges_per_wg = wide_merge ? kWaves : kThreads / std::max<uint32_t>(16, std::min<uint32_t>(D / 4, kWave));
     const uint32_t rgrid = static_cast<uint32_t>(std::max<uint64_t>(
         1, std::min<uint64_t>((static_cast<uint64_t>(T) * H + merges_per_wg - 1) / merges_per_wg, ctx->num_cus * 8)));
-    if ((rc = prof_begin(ctx, "reduce", stream, &ev))) return rc;
+    if (prof && (rc = prof_begin(ctx, "reduce", stream, &ev))) return rc;
     hipLaunchKernelGGL(reduce, dim3(rgrid), dim3(kThreads), 0, stream, a);
     KANSO_LAUNCH_CHECK();
-    return prof_end(ctx, "reduce", stream, ev);
+    return prof ? prof_end(ctx, "reduce", stream, ev) : KANSO_OK;
 }
 
 }  // namespace
@@ -1665,6 +1687,18 @@ int op_ragged_attention(kanso_ctx* ctx, const kanso_ragged_attention_params* p, 
     }
     return run_ragged(ctx, p, q, k_pool, v_pool, k_scales, v_scales, block_tables, cu_seqlens, context_lens, out, s,
                       "ragged attention", out_tiled);
+}
+
+int noalloc_scratch_init(void** ptr) {
+    *ptr = nullptr;
+    void* p = nullptr;
+    const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || p == nullptr) {
+        set_error("kanso_create: no device address for the fixed attention scratch: %s", hipGetErrorString(e));
+        return KANSO_E_HIP;
+    }
+    *ptr = p;
+    return KANSO_OK;
 }
 
 }  // namespace kanso
@@ -1853,6 +1887,23 @@ int kanso_ragged_paged_attention(kanso_ctx* ctx, const kanso_ragged_attention_pa
     }
     return run_ragged(ctx, p, q, k_pool, v_pool, k_scales, v_scales, block_tables, cu_seqlens,
                       context_lens, out, as_stream(stream), "kanso_ragged_paged_attention");
+}
+
+int kanso_ragged_paged_attention_noalloc(kanso_ctx* ctx, const kanso_ragged_attention_params* p, const float* q,
+                                         const void* k_pool, const void* v_pool, const void* k_scales,
+                                         const void* v_scales, const uint32_t* block_tables,
+                                         const int32_t* cu_seqlens, const uint32_t* context_lens, float* out,
+                                         kanso_stream_t stream) {
+    if (!ctx || !p) {
+        set_error("kanso_ragged_paged_attention_noalloc: null context or params");
+        return KANSO_E_INVALID_ARG;
+    }
+    if (!ctx->noalloc_scratch) {
+        set_error("kanso_ragged_paged_attention_noalloc: context has no fixed scratch");
+        return KANSO_E_INVALID_ARG;
+    }
+    return run_ragged(ctx, p, q, k_pool, v_pool, k_scales, v_scales, block_tables, cu_seqlens, context_lens, out,
+                      as_stream(stream), "kanso_ragged_paged_attention_noalloc", false, ctx->noalloc_scratch);
 }
 
 }  // extern "C"

@@ -45,6 +45,9 @@ struct kanso_ctx {
     // Grow-only buffer of 64-bit argmax keys (lm_head epilogue).
     void* keys = nullptr;
     size_t keys_bytes = 0;
+    // Device address of this device's copy of attention.hip's fixed scratch array
+    // (kanso_ragged_paged_attention_noalloc), resolved once at kanso_create.
+    void* noalloc_scratch = nullptr;
     bool profiling = false;
     std::vector<kanso::ProfileRecord> pending;
     std::vector<std::pair<std::string, kanso::ProfileTotal>> totals;
@@ -65,6 +68,9 @@ namespace kanso {
 // Makes ctx->scratch at least `bytes` large. Scratch may still be read by work
 // enqueued earlier, so growth waits for the device before freeing the old buffer.
 int ensure_scratch(kanso_ctx* ctx, size_t bytes);
+// Resolves the device address of the fixed attention scratch array on the current
+// device (attention.hip); called once per context by kanso_create.
+int noalloc_scratch_init(void** ptr);
 int ensure_aux(kanso_ctx* ctx, size_t bytes);
 int ensure_keys(kanso_ctx* ctx, size_t bytes);
 

@@ -143,6 +143,11 @@ int kanso_create(int device, kanso_ctx** out) {
         delete ctx;
         return KANSO_E_HIP;
     }
+    if (int rc = noalloc_scratch_init(&ctx->noalloc_scratch)) {
+        (void)hipFree(ctx->status);
+        delete ctx;
+        return rc;
+    }
 
     *out = ctx;
     return KANSO_OK;
