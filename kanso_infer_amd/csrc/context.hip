@@ -191,6 +191,8 @@ int kanso_check_device_status(kanso_ctx* ctx, kanso_stream_t stream, uint32_t* f
         if (host & KANSO_DEV_TABLE_SHORT) msg += " block table shorter than a position needs;";
         if (host & KANSO_DEV_SLOT_OOB) msg += " slot outside the KV pool;";
         if (host & KANSO_DEV_BLOCK_OOB) msg += " physical block id outside the pool;";
+        if (host & KANSO_DEV_POSITION_OOB) msg += " position beyond the RoPE table;";
+        if (host & KANSO_DEV_TOKEN_OOB) msg += " token id beyond the vocabulary;";
         set_error("%s", msg.c_str());
         return KANSO_E_DEVICE_CHECK;
     }

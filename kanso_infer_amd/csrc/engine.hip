@@ -479,6 +479,20 @@ int kanso_engine_add_request(kanso_engine* e, const uint32_t* prompt, uint32_t p
         set_error("kanso_engine_add_request: null argument");
         return KANSO_E_INVALID_ARG;
     }
+    // An empty prompt has no row to sample from (the reference's server rejects it
+    // before the engine, src/server/routes.rs:109).
+    if (prompt_len == 0) {
+        set_error("kanso_engine_add_request: empty prompt");
+        return KANSO_E_INVALID_ARG;
+    }
+    // Token ids index the embedding table: ids past the vocabulary are refused here
+    // rather than read as row 0 on the device.
+    const uint32_t vocab = e->model ? kanso_model_vocab(e->model) : 0;
+    for (uint32_t i = 0; vocab && i < prompt_len; ++i)
+        if (prompt[i] >= vocab) {
+            set_error("kanso_engine_add_request: token %u at %u outside the vocabulary (%u)", prompt[i], i, vocab);
+            return KANSO_E_INVALID_ARG;
+        }
     Sequence s;
     s.id = e->next_id++;
     s.prompt.assign(prompt, prompt + prompt_len);

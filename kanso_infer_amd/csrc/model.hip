@@ -254,7 +254,7 @@ int ensure_step_buffers(kanso_model* m, uint32_t T, uint32_t S, uint32_t tables,
         if ((rc = dev_alloc(m, &m->ctx_lens, sq * 4ull))) return rc;
         if ((rc = dev_alloc(m, &m->next, sq * 4ull))) return rc;
         void* h = nullptr;
-        KANSO_HIP_TRY(hipHostMalloc(&h, sq * 4ull));
+        KANSO_HIP_TRY(hipHostMalloc(&h, (sq + 1) * 4ull));  // + the status word
         if (m->h_next) (void)hipHostFree(m->h_next);
         m->h_next = static_cast<uint32_t*>(h);
         m->cap_tokens = t;
@@ -474,12 +474,19 @@ int model_forward(kanso_model* m, const HostStep& step, float* logits, uint32_t*
     if ((rc = op_lm_head_argmax(m->ctx, m->lm_head, m->hidden, d_last, m->final_norm, c.eps, R, c.hidden, c.vocab,
                                 logits, m->next, s, true)))
         return rc;
+    // the sampled tokens and the device status word come back at the same sync: a
+    // flag raised by any kernel of the step (slot, block, position, token bounds)
+    // fails the step instead of passing wrong tokens on
     KANSO_HIP_TRY(hipMemcpyAsync(m->h_next, m->next, R * 4ull, hipMemcpyDeviceToHost, s));
+    KANSO_HIP_TRY(hipMemcpyAsync(m->h_next + m->cap_seqs, m->ctx->status, 4, hipMemcpyDeviceToHost, s));
     KANSO_HIP_TRY(hipStreamSynchronize(s));
+    if (m->h_next[m->cap_seqs]) return kanso_check_device_status(m->ctx, reinterpret_cast<kanso_stream_t>(s), nullptr);
     std::memcpy(next, m->h_next, R * 4ull);
     ++m->forward_calls;
     return KANSO_OK;
 }
+
+uint32_t kanso_model_vocab(const kanso_model* m) { return m ? m->cfg.vocab : 0; }
 
 }  // namespace kanso
 
@@ -801,11 +808,17 @@ int model_forward_entry(kanso_model* m, const char* name, const kanso_seq_plan* 
             set_error("%s: table range outside the table arena", name);
             return KANSO_E_OUT_OF_BOUNDS;
         }
-        for (uint32_t i = 0; i < p.q_len; ++i)
-            if (static_cast<uint32_t>(p.token_offset + p.start_pos + i) >= token_arena_len) {
+        for (uint32_t i = 0; i < p.q_len; ++i) {
+            const uint32_t at = static_cast<uint32_t>(p.token_offset + p.start_pos + i);
+            if (at >= token_arena_len) {
                 set_error("%s: token outside the token arena", name);
                 return KANSO_E_OUT_OF_BOUNDS;
             }
+            if (token_arena[at] >= m->cfg.vocab) {
+                set_error("%s: token id %u outside the vocabulary (%u)", name, token_arena[at], m->cfg.vocab);
+                return KANSO_E_INVALID_ARG;
+            }
+        }
     }
     return model_forward(m, hs, logits, next_tokens, as_stream(stream), all_rows);
 }

@@ -90,6 +90,9 @@ struct kanso_model {
 
 namespace kanso {
 
+// The model's vocabulary size (token ids must be below it).
+uint32_t kanso_model_vocab(const kanso_model* m);
+
 // Erases blocks (host list) of every layer's K and V pool (allocate_zeroed,
 // src/kv_cache/mod.rs:25-35).
 int model_reset_blocks(kanso_model* m, const uint32_t* blocks, uint32_t n, hipStream_t s);

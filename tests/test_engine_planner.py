@@ -203,3 +203,16 @@ def test_continuous_batching_staggered_arrival():
     st = cpp.stats()
     assert st["running"] == 0 and st["waiting"] == 0
     assert cpp.free_blocks_count() == 20 == ref.block_pool.free_blocks_count()
+
+
+def test_empty_prompt_rejected():
+    """An empty prompt is refused at admission (the reference's server refuses it,
+    src/server/routes.rs:109): the engine stays usable for the other requests."""
+    from kanso_infer_amd import EngineError
+    cpp, ref = pair(4, 16, 4, 8)
+    with pytest.raises(EngineError, match="empty prompt"):
+        cpp.add_request([], 4)
+    cpp.add_request([1, 2, 3], 3)
+    ref.add_request([1, 2, 3], 3)
+    while cpp.has_unfinished_requests():
+        assert_same_step(cpp, ref, "after a refused request")

@@ -245,14 +245,17 @@ def test_chunk_partition_from_host_lengths(ctx, decodes):
     assert_close(got, want, what=f"{b.label} P {P} CP {cp}")
 
 
-@pytest.mark.parametrize("variant", ["config1", "config2_small_pool", "config3_int8",
-                                     "config3_q8_0", "config3_fp8"])
+@pytest.mark.parametrize("variant", ["config1", "config2_small_pool", "config2_bench_pool",
+                                     "config3_int8", "config3_q8_0", "config3_fp8"])
 def test_baseline_shapes(ctx, variant):
-    """The BASELINE configs at their real shapes (pools sized to what the tables use)."""
+    """The BASELINE configs at their real shapes (pools sized to what the tables use;
+    config2_bench_pool: the 64k-block pool of 2.7 GB the headline is timed on)."""
     if variant == "config1":
         b, kv = workloads.config1_decode(), oracle.KV_F32
     elif variant == "config2_small_pool":
         b, kv = workloads.config2_mixed(num_blocks=10000), oracle.KV_F32
+    elif variant == "config2_bench_pool":
+        b, kv = workloads.config2_mixed(num_blocks=65536), oracle.KV_F32
     else:
         b = workloads.config3_quant_decode()
         kv = {"int8": oracle.KV_INT8, "q8_0": oracle.KV_Q8_0,

@@ -153,9 +153,9 @@ def test_quantize_q8_0_bit_exact(ctx):
 
 
 def test_init_random_statistics(ctx):
-    """Device random init: N(0, 0.02^2) weights, unit norms. The final RMSNorm makes
-    the last hidden row unit-RMS, so logits have a standard deviation near
-    0.02 * sqrt(960) ~ 0.62."""
+    """Device random init: weights of standard deviation 0.02 (an Irwin-Hall(4) draw),
+    unit norms. The final RMSNorm makes the last hidden row unit-RMS, so logits have
+    a standard deviation near 0.02 * sqrt(960) ~ 0.62."""
     cfg = ModelConfig.smollm2_360m(num_hidden_layers=2, max_position=64)
     m = Model(ctx, cfg)
     m.init_random(seed=7, std=0.02)
@@ -284,4 +284,22 @@ def test_get_weight_round_trip(ctx):
     assert np.array_equal(m.get_weight(_capi.KANSO_W_EMBED), w["embed"])
     assert np.array_equal(m.get_weight(_capi.KANSO_W_V, 1), w["layers"][1]["wv"])
     assert np.array_equal(m.get_weight(_capi.KANSO_W_FFN_NORM, 0), w["layers"][0]["ffn_norm"])
+    m.close()
+
+
+def test_forward_refuses_bad_tokens_and_reports_device_flags(ctx):
+    """A token id past the vocabulary is refused on the host; a block id past the pool
+    (clamped by every kernel, so the step completes) fails the step through the
+    device status word instead of returning tokens."""
+    from kanso_infer_amd import EngineError
+    w = random_weights(SMALL, seed=31)
+    m = gpu_model(ctx, SMALL, w, 16, 16)
+    plan = np.array([[0, 3, 0, 1, 0]], np.uint32)
+    with pytest.raises(EngineError, match="vocabulary"):
+        m.forward(plan, np.array([1, SMALL["vocab"], 2], np.uint32), np.array([0], np.uint32))
+    with pytest.raises(EngineError, match="device check failed"):
+        m.forward(plan, np.array([1, 2, 3], np.uint32), np.array([16], np.uint32))
+    # the flag was cleared with the error: the next good step succeeds
+    toks = m.forward(plan, np.array([1, 2, 3], np.uint32), np.array([0], np.uint32))
+    assert toks.shape == (1,)
     m.close()
