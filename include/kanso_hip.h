@@ -377,6 +377,12 @@ typedef struct {
     float rope_theta;       /* 10000                                             */
     uint32_t max_position;  /* RoPE table rows (positions 0 .. max_position-1)   */
     uint32_t tied_embeddings; /* 1: lm_head is the embedding table              */
+    /* Granite multipliers (src/weights.rs:395-406, applied as src/model.rs:424-430,
+     * 739-760); 0 = absent (llama: identity, attention 1/sqrt(head_dim)). */
+    float embedding_scale;  /* embedding rows x embedding_scale                 */
+    float attention_scale;  /* replaces 1/sqrt(head_dim) when non-zero          */
+    float residual_scale;   /* attention / FFN outputs x residual_scale before the add */
+    float logit_scale;      /* logits x (1 / logit_scale)                       */
 } kanso_model_config;
 
 /* Weight kinds of kanso_model_set_weight. Matrices are GGUF Q8_0 bytes [rows][in/32]
@@ -403,6 +409,15 @@ int kanso_model_destroy(kanso_model* model);
  * re-lays matrices into the packed layout. */
 int kanso_model_set_weight(kanso_model* model, uint32_t kind, uint32_t layer,
                            const void* host_data, size_t bytes);
+
+/* Uploads one projection matrix in GGUF Q4_K blocks ([rows][in/256] x 144 B;
+ * in a multiple of 256), kept in that format and multiplied by the Q4_K loader of
+ * the product kernels (the reference keeps any GGUF block type as a QMatMul,
+ * src/weights.rs:33-39). Kinds: Q, K, V, O, GATE, UP, DOWN. A layer's Q, K and V
+ * (and its gate and up) run in one fused product, so they must all be Q4_K or
+ * all Q8_0: a forward over a layer with a mix is refused. */
+int kanso_model_set_weight_q4_k(kanso_model* model, uint32_t kind, uint32_t layer,
+                                const void* host_data, size_t bytes);
 
 /* Random-init weights generated on the device (create_mock_*, src/model.rs:520-651,
  * with SmolLM2's std of 0.02 in place of N(0,1)): matrix j (embedding 1, untied

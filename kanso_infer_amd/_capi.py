@@ -119,6 +119,10 @@ class ModelConfigC(C.Structure):
         ("rope_theta", C.c_float),
         ("max_position", C.c_uint32),
         ("tied_embeddings", C.c_uint32),
+        ("embedding_scale", C.c_float),
+        ("attention_scale", C.c_float),
+        ("residual_scale", C.c_float),
+        ("logit_scale", C.c_float),
     ]
 
 
@@ -172,6 +176,7 @@ SIGNATURES: dict[str, tuple] = {
     "kanso_model_set_weight": (_I, [_P, _U, _U, _P, C.c_size_t]),
     "kanso_model_init_random": (_I, [_P, C.c_uint64, C.c_float]),
     "kanso_model_get_weight": (_I, [_P, _U, _U, _P, C.c_size_t]),
+    "kanso_model_set_weight_q4_k": (_I, [_P, _U, _U, _P, C.c_size_t]),
     "kanso_model_alloc_kv": (_I, [_P, _U, _U, _U, _U]),
     "kanso_model_alloc_kv_quant": (_I, [_P, _U, _U, _U, _U, _U]),
     "kanso_model_kv_pool": (_I, [_P, _U, C.POINTER(_P), C.POINTER(_P)]),

@@ -18,7 +18,7 @@ namespace {
 __global__ __launch_bounds__(256) void embed_q8_0_kernel(const uint8_t* __restrict__ table, uint32_t vocab,
                                                          uint32_t hidden, const uint32_t* __restrict__ tokens,
                                                          uint32_t T, float* __restrict__ out, uint32_t* status,
-                                                         uint32_t tiled) {
+                                                         uint32_t tiled, float scale) {
     const uint32_t nb = hidden / 32;
     const uint64_t total = static_cast<uint64_t>(T) * hidden / 8;
     for (uint64_t e = blockIdx.x * 256ull + threadIdx.x; e < total; e += static_cast<uint64_t>(gridDim.x) * 256) {
@@ -35,7 +35,7 @@ __global__ __launch_bounds__(256) void embed_q8_0_kernel(const uint8_t* __restri
         const float d = f16_bits_to_f32(*reinterpret_cast<const uint16_t*>(tile + 512 + 2 * rr));
         float v[8];
 #pragma unroll
-        for (int j = 0; j < 8; ++j) v[j] = d * static_cast<float>(static_cast<int8_t>((q >> (8 * j)) & 0xff));
+        for (int j = 0; j < 8; ++j) v[j] = d * static_cast<float>(static_cast<int8_t>((q >> (8 * j)) & 0xff)) * scale;
         float* o0 = tiled ? out + act_tile_off(m, k, nb) : out + static_cast<size_t>(m) * hidden + k;
         float* o1 = tiled ? out + act_tile_off(m, k + 4, nb) : o0 + 4;
         *reinterpret_cast<float4*>(o0) = make_float4(v[0], v[1], v[2], v[3]);
@@ -67,20 +67,20 @@ bool aligned16(const void* p) { return reinterpret_cast<uintptr_t>(p) % 16 == 0;
 
 // Internal entry points shared with the model forward (model.hip).
 int op_embed(kanso_ctx* ctx, const void* table, uint32_t vocab, uint32_t hidden, const uint32_t* tokens,
-             uint32_t T, float* out, hipStream_t s, bool tiled) {
+             uint32_t T, float* out, hipStream_t s, bool tiled, float scale) {
     if (T == 0) return KANSO_OK;
     const uint64_t total = static_cast<uint64_t>(T) * hidden / 8;
     const uint32_t grid = static_cast<uint32_t>(std::min<uint64_t>((total + 255) / 256, 4096));
     hipLaunchKernelGGL(embed_q8_0_kernel, dim3(grid), dim3(256), 0, s, static_cast<const uint8_t*>(table), vocab,
-                       hidden, tokens, T, out, ctx->status, tiled ? 1u : 0u);
+                       hidden, tokens, T, out, ctx->status, tiled ? 1u : 0u, scale);
     KANSO_LAUNCH_CHECK();
     return KANSO_OK;
 }
 
 int op_qkv_rope_append(kanso_ctx* ctx, const kanso_qkv_params* p, const void* w, const float* x,
                        const float* norm_w, const int32_t* positions, const int64_t* slots, const float* cos_t,
-                       const float* sin_t, float* q, float* k_pool, float* v_pool, hipStream_t s, bool tiled) {
-    WPacked wl{static_cast<const uint8_t*>(w), p->hidden / 32};
+                       const float* sin_t, float* q, float* k_pool, float* v_pool, hipStream_t s, bool tiled,
+                       bool q4k) {
     XIn xa{x, nullptr, norm_w, p->eps, p->hidden, p->num_tokens, p->hidden, tiled ? 1u : 0u};
     EpiQkvRope epi;
     epi.q = q;
@@ -95,28 +95,31 @@ int op_qkv_rope_append(kanso_ctx* ctx, const kanso_qkv_params* p, const void* w,
     epi.num_kv_heads = p->num_kv_heads;
     epi.max_pos = p->max_pos;
     epi.num_slots = static_cast<int64_t>(p->num_blocks) * p->block_size;
-    return launch_q8_gemm(wl, xa, epi, 2 * (p->num_heads + 2 * p->num_kv_heads), s);
+    const uint32_t pairs = 2 * (p->num_heads + 2 * p->num_kv_heads);
+    if (q4k)
+        return launch_q8_gemm(WQ4K{static_cast<const uint8_t*>(w), p->hidden / 256, 32 * pairs}, xa, epi, pairs, s);
+    return launch_q8_gemm(WPacked{static_cast<const uint8_t*>(w), p->hidden / 32}, xa, epi, pairs, s);
 }
 
 int op_gemm_residual(const void* w, const float* x, float* y, uint32_t out, uint32_t in, uint32_t T,
-                     hipStream_t s, bool tiled) {
-    WPacked wl{static_cast<const uint8_t*>(w), in / 32};
+                     hipStream_t s, bool tiled, bool q4k, float scale) {
     XIn xa{x, nullptr, nullptr, 0.f, in, T, in, tiled ? 1u : 0u};
-    EpiStore<true> epi{y, out, out, tiled ? 1u : 0u};
-    return launch_q8_gemm(wl, xa, epi, (out + 31) / 32, s);
+    EpiStore<true> epi{y, out, out, tiled ? 1u : 0u, scale};
+    if (q4k) return launch_q8_gemm(WQ4K{static_cast<const uint8_t*>(w), in / 256, out}, xa, epi, (out + 31) / 32, s);
+    return launch_q8_gemm(WPacked{static_cast<const uint8_t*>(w), in / 32}, xa, epi, (out + 31) / 32, s);
 }
 
 int op_gate_up_swiglu(const void* w, const float* x, const float* norm_w, float eps, uint32_t T,
-                      uint32_t hidden, uint32_t inter, float* h, hipStream_t s, bool tiled) {
-    WPacked wl{static_cast<const uint8_t*>(w), hidden / 32};
+                      uint32_t hidden, uint32_t inter, float* h, hipStream_t s, bool tiled, bool q4k) {
     XIn xa{x, nullptr, norm_w, eps, hidden, T, hidden, tiled ? 1u : 0u};
     EpiSwiGLU epi{h, inter, inter, tiled ? 1u : 0u};
-    return launch_q8_gemm(wl, xa, epi, inter / 16, s);
+    if (q4k) return launch_q8_gemm(WQ4K{static_cast<const uint8_t*>(w), hidden / 256, 2 * inter}, xa, epi, inter / 16, s);
+    return launch_q8_gemm(WPacked{static_cast<const uint8_t*>(w), hidden / 32}, xa, epi, inter / 16, s);
 }
 
 int op_lm_head_argmax(kanso_ctx* ctx, const void* w, const float* x, const int32_t* rows, const float* norm_w,
                       float eps, uint32_t S, uint32_t hidden, uint32_t vocab, float* logits, uint32_t* tokens,
-                      hipStream_t s, bool tiled) {
+                      hipStream_t s, bool tiled, float logit_mul) {
     if (S == 0) return KANSO_OK;
     const uint32_t pairs = (vocab + 31) / 32;
     int rc = ensure_keys(ctx, static_cast<size_t>(S) * pairs * sizeof(unsigned long long));
@@ -124,7 +127,7 @@ int op_lm_head_argmax(kanso_ctx* ctx, const void* w, const float* x, const int32
     auto* keys = static_cast<unsigned long long*>(ctx->keys);
     WPacked wl{static_cast<const uint8_t*>(w), hidden / 32};
     XIn xa{x, rows, norm_w, eps, hidden, S, hidden, tiled ? 1u : 0u};
-    EpiArgmax epi{logits, vocab, vocab, keys, pairs};
+    EpiArgmax epi{logits, vocab, vocab, keys, pairs, logit_mul};
     if ((rc = launch_q8_gemm(wl, xa, epi, pairs, s))) return rc;
     hipLaunchKernelGGL(argmax_finish_kernel, dim3(S), dim3(256), 0, s, keys, pairs, tokens);
     KANSO_LAUNCH_CHECK();
@@ -147,7 +150,7 @@ int kanso_embed_q8_0(kanso_ctx* ctx, const void* packed_table, uint32_t vocab, u
         set_error("kanso_embed_q8_0: vocab %u / hidden %u (multiple of 32, out 16-byte aligned)", vocab, hidden);
         return KANSO_E_INVALID_SHAPE;
     }
-    return op_embed(ctx, packed_table, vocab, hidden, tokens, num_tokens, out, as_stream(stream), false);
+    return op_embed(ctx, packed_table, vocab, hidden, tokens, num_tokens, out, as_stream(stream), false, 1.f);
 }
 
 int kanso_qkv_rope_append(kanso_ctx* ctx, const kanso_qkv_params* p, const void* packed_qkv, const float* x,
@@ -170,7 +173,7 @@ int kanso_qkv_rope_append(kanso_ctx* ctx, const kanso_qkv_params* p, const void*
         return KANSO_E_INVALID_SHAPE;
     }
     return op_qkv_rope_append(ctx, p, packed_qkv, x, norm_w, positions, slot_mapping, cos_table, sin_table, q_out,
-                              k_pool, v_pool, as_stream(stream), false);
+                              k_pool, v_pool, as_stream(stream), false, false);
 }
 
 int kanso_gemm_q8_0_residual(kanso_ctx* ctx, const void* packed, const float* x, float* y, uint32_t out_features,
@@ -184,7 +187,8 @@ int kanso_gemm_q8_0_residual(kanso_ctx* ctx, const void* packed, const float* x,
                   num_tokens);
         return KANSO_E_INVALID_SHAPE;
     }
-    return op_gemm_residual(packed, x, y, out_features, in_features, num_tokens, as_stream(stream), false);
+    return op_gemm_residual(packed, x, y, out_features, in_features, num_tokens, as_stream(stream), false, false,
+                            1.f);
 }
 
 int kanso_gate_up_swiglu(kanso_ctx* ctx, const void* packed_gate_up, const float* x, const float* norm_w,
@@ -201,7 +205,7 @@ int kanso_gate_up_swiglu(kanso_ctx* ctx, const void* packed_gate_up, const float
         return KANSO_E_INVALID_SHAPE;
     }
     return op_gate_up_swiglu(packed_gate_up, x, norm_w, eps, num_tokens, hidden, intermediate, h,
-                             as_stream(stream), false);
+                             as_stream(stream), false, false);
 }
 
 int kanso_lm_head_argmax(kanso_ctx* ctx, const void* packed, const float* x, const int32_t* rows,
@@ -216,7 +220,7 @@ int kanso_lm_head_argmax(kanso_ctx* ctx, const void* packed, const float* x, con
         return KANSO_E_INVALID_SHAPE;
     }
     return op_lm_head_argmax(ctx, packed, x, rows, norm_w, eps, num_rows, hidden, vocab, logits, tokens,
-                             as_stream(stream), false);
+                             as_stream(stream), false, 1.f);
 }
 
 }  // extern "C"

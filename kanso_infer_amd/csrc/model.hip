@@ -355,6 +355,15 @@ int model_forward(kanso_model* m, const HostStep& step, float* logits, uint32_t*
         set_error("forward_batch: KV pool not allocated (kanso_model_alloc_kv)");
         return KANSO_E_INVALID_ARG;
     }
+    for (uint32_t l = 0; l < c.num_layers; ++l) {
+        // a fused product needs all its matrices in one format
+        const uint32_t parts = m->layers[l].q4k_parts;
+        const uint32_t qkv = parts & 7u, gu = (parts >> (KANSO_W_GATE - KANSO_W_Q)) & 3u;
+        if ((qkv != 0 && qkv != 7u) || (gu != 0 && gu != 3u)) {
+            set_error("forward_batch: layer %u mixes Q4_K and Q8_0 in its Q/K/V or gate/up matrices", l);
+            return KANSO_E_INVALID_ARG;
+        }
+    }
     // Shapes from the plan (PaddedDecodeTables::new, src/model.rs:84-88).
     uint32_t T = 0, max_blocks = 1, max_q = 0;
     for (const auto& p : step.plan) {
@@ -406,7 +415,12 @@ int model_forward(kanso_model* m, const HostStep& step, float* logits, uint32_t*
         return rc;
     // hidden, attn and act are in the tiled activation order (act_tile_off): the
     // products read them as contiguous 1 KB slices
-    if ((rc = op_embed(m->ctx, m->embed, c.vocab, c.hidden, m->tokens, T, m->hidden, s, true))) return rc;
+    // Granite multipliers: the reference multiplies by the f64 scale on f32 tensors,
+    // i.e. by the scale rounded to f32 (src/model.rs:424-430, 739-760)
+    const float emb_mul = c.embedding_scale != 0.f ? c.embedding_scale : 1.f;
+    const float res_mul = c.residual_scale != 0.f ? c.residual_scale : 1.f;
+    const float logit_mul = c.logit_scale != 0.f ? static_cast<float>(1.0 / static_cast<double>(c.logit_scale)) : 1.f;
+    if ((rc = op_embed(m->ctx, m->embed, c.vocab, c.hidden, m->tokens, T, m->hidden, s, true, emb_mul))) return rc;
 
     kanso_qkv_params qp{T, c.hidden, c.num_heads, c.num_kv_heads, 64, c.max_position, c.eps, m->num_blocks,
                         m->block_size};
@@ -417,7 +431,8 @@ int model_forward(kanso_model* m, const HostStep& step, float* logits, uint32_t*
     ap.head_dim = c.head_dim;
     ap.block_size = m->block_size;
     ap.max_num_blocks_per_seq = max_blocks;
-    ap.scale = static_cast<float>(1.0 / std::sqrt(static_cast<double>(c.head_dim)));  // src/model.rs:757-762
+    ap.scale = c.attention_scale != 0.f ? c.attention_scale
+                                        : static_cast<float>(1.0 / std::sqrt(static_cast<double>(c.head_dim)));  // src/model.rs:757-762
     ap.total_q = T;
     ap.kv_dtype = m->kv_dtype;
     ap.num_blocks = m->num_blocks;
@@ -444,18 +459,21 @@ int model_forward(kanso_model* m, const HostStep& step, float* logits, uint32_t*
     qs.block_size = 1;
     for (uint32_t l = 0; l < c.num_layers; ++l) {
         const auto& L = m->layers[l];
+        const uint32_t bits = L.q4k_parts;
+        const bool qkv4 = (bits & 7u) == 7u, gu4 = ((bits >> (KANSO_W_GATE - KANSO_W_Q)) & 3u) == 3u;
+        const bool o4 = (bits >> (KANSO_W_O - KANSO_W_Q)) & 1u, down4 = (bits >> (KANSO_W_DOWN - KANSO_W_Q)) & 1u;
         uint8_t* kp = reinterpret_cast<uint8_t*>(m->k_pool) + l * m->layer_pool_bytes;
         uint8_t* vp = reinterpret_cast<uint8_t*>(m->v_pool) + l * m->layer_pool_bytes;
         uint8_t* ks = quant ? m->k_scales + l * m->layer_scale_bytes : nullptr;
         uint8_t* vs = quant ? m->v_scales + l * m->layer_scale_bytes : nullptr;
         if (!quant) {
-            if ((rc = op_qkv_rope_append(m->ctx, &qp, L.qkv, m->hidden, L.attn_norm, m->positions, m->slots,
-                                         m->cos_t, m->sin_t, m->q, reinterpret_cast<float*>(kp),
-                                         reinterpret_cast<float*>(vp), s, true)))
+            if ((rc = op_qkv_rope_append(m->ctx, &qp, qkv4 ? L.qkv_q4k : L.qkv, m->hidden, L.attn_norm, m->positions,
+                                         m->slots, m->cos_t, m->sin_t, m->q, reinterpret_cast<float*>(kp),
+                                         reinterpret_cast<float*>(vp), s, true, qkv4)))
                 return rc;
         } else {
-            if ((rc = op_qkv_rope_append(m->ctx, &qs, L.qkv, m->hidden, L.attn_norm, m->positions, m->iota,
-                                         m->cos_t, m->sin_t, m->q, m->k_stage, m->v_stage, s, true)))
+            if ((rc = op_qkv_rope_append(m->ctx, &qs, qkv4 ? L.qkv_q4k : L.qkv, m->hidden, L.attn_norm, m->positions,
+                                         m->iota, m->cos_t, m->sin_t, m->q, m->k_stage, m->v_stage, s, true, qkv4)))
                 return rc;
             if ((rc = kanso_kv_append(m->ctx, m->kv_dtype, m->k_stage, m->v_stage, m->slots, T, m->num_blocks,
                                       m->block_size, c.num_kv_heads, c.head_dim, kp, vp, ks, vs,
@@ -465,14 +483,17 @@ int model_forward(kanso_model* m, const HostStep& step, float* logits, uint32_t*
         if ((rc = op_ragged_attention(m->ctx, &ap, m->q, kp, vp, ks, vs, m->tables, m->cu, m->ctx_lens, m->attn, s,
                                       true)))
             return rc;
-        if ((rc = op_gemm_residual(L.o, m->attn, m->hidden, c.hidden, qd, T, s, true))) return rc;
-        if ((rc = op_gate_up_swiglu(L.gate_up, m->hidden, L.ffn_norm, c.eps, T, c.hidden, c.intermediate, m->act,
-                                    s, true)))
+        if ((rc = op_gemm_residual(o4 ? L.o_q4k : L.o, m->attn, m->hidden, c.hidden, qd, T, s, true, o4, res_mul)))
             return rc;
-        if ((rc = op_gemm_residual(L.down, m->act, m->hidden, c.hidden, c.intermediate, T, s, true))) return rc;
+        if ((rc = op_gate_up_swiglu(gu4 ? L.gate_up_q4k : L.gate_up, m->hidden, L.ffn_norm, c.eps, T, c.hidden,
+                                    c.intermediate, m->act, s, true, gu4)))
+            return rc;
+        if ((rc = op_gemm_residual(down4 ? L.down_q4k : L.down, m->act, m->hidden, c.hidden, c.intermediate, T, s,
+                                   true, down4, res_mul)))
+            return rc;
     }
     if ((rc = op_lm_head_argmax(m->ctx, m->lm_head, m->hidden, d_last, m->final_norm, c.eps, R, c.hidden, c.vocab,
-                                logits, m->next, s, true)))
+                                logits, m->next, s, true, logit_mul)))
         return rc;
     // the sampled tokens and the device status word come back at the same sync: a
     // flag raised by any kernel of the step (slot, block, position, token bounds)
@@ -524,6 +545,11 @@ int kanso_model_create(kanso_ctx* ctx, const kanso_model_config* cfg, kanso_mode
                   c.head_dim, c.hidden, c.intermediate, c.num_heads, c.num_kv_heads);
         return KANSO_E_INVALID_SHAPE;
     }
+    for (float v : {c.embedding_scale, c.attention_scale, c.residual_scale, c.logit_scale})
+        if (!std::isfinite(v) || v < 0.f) {
+            set_error("kanso_model_create: Granite multipliers must be finite and >= 0 (0 = absent)");
+            return KANSO_E_INVALID_SHAPE;
+        }
     KANSO_HIP_TRY(hipSetDevice(ctx->device));
     auto* m = new kanso_model();
     m->ctx = ctx;
@@ -573,6 +599,7 @@ int kanso_model_set_weight(kanso_model* m, uint32_t kind, uint32_t layer, const 
                   want, ms.rows, ms.in);
         return KANSO_E_INVALID_SHAPE;
     }
+    if (kind >= KANSO_W_Q && kind <= KANSO_W_DOWN) m->layers[layer].q4k_parts &= ~(1u << (kind - KANSO_W_Q));
     void* tmp = nullptr;
     KANSO_HIP_TRY(hipMalloc(&tmp, bytes));
     hipError_t e = hipMemcpy(tmp, host_data, bytes, hipMemcpyHostToDevice);
@@ -586,6 +613,69 @@ int kanso_model_set_weight(kanso_model* m, uint32_t kind, uint32_t layer, const 
         return KANSO_E_HIP;
     }
     return rc;
+}
+
+int kanso_model_set_weight_q4_k(kanso_model* m, uint32_t kind, uint32_t layer, const void* host_data, size_t bytes) {
+    int rc = model_check(m, "kanso_model_set_weight_q4_k");
+    if (rc) return rc;
+    const kanso_model_config& c = m->cfg;
+    if (!host_data || kind < KANSO_W_Q || kind > KANSO_W_DOWN || layer >= c.num_layers) {
+        set_error("kanso_model_set_weight_q4_k: kind %u / layer %u is not a projection of this model", kind, layer);
+        return KANSO_E_INVALID_ARG;
+    }
+    MatrixSlot ms;
+    matrix_slot(m, kind, layer, ms);
+    if (ms.in % 256 != 0) {
+        set_error("kanso_model_set_weight_q4_k: in_features %u is not a multiple of 256 (Q4_K super-blocks)", ms.in);
+        return KANSO_E_INVALID_SHAPE;
+    }
+    const size_t row_bytes = static_cast<size_t>(ms.in / 256) * 144;
+    if (bytes != ms.rows * row_bytes) {
+        set_error("kanso_model_set_weight_q4_k: kind %u has %zu bytes, expected %zu (GGUF Q4_K [%u][%u])", kind, bytes,
+                  ms.rows * row_bytes, ms.rows, ms.in);
+        return KANSO_E_INVALID_SHAPE;
+    }
+    auto& L = m->layers[layer];
+    const auto alloc = [&](uint8_t*& buf, size_t rows) -> int {
+        if (buf) return KANSO_OK;
+        void* p = nullptr;
+        KANSO_HIP_TRY(hipMalloc(&p, rows * row_bytes));
+        m->allocations.push_back(p);
+        buf = static_cast<uint8_t*>(p);
+        return KANSO_OK;
+    };
+    const char* src = static_cast<const char*>(host_data);
+    switch (kind) {
+        case KANSO_W_Q:
+        case KANSO_W_K:
+        case KANSO_W_V: {
+            // rows of [Wq; Wk; Wv], as the packed layout concatenates them
+            if ((rc = alloc(L.qkv_q4k, qkv_rows(c)))) return rc;
+            const size_t row0 = kind == KANSO_W_Q ? 0 : kind == KANSO_W_K ? c.num_heads * 64ull
+                                                                            : (c.num_heads + c.num_kv_heads) * 64ull;
+            KANSO_HIP_TRY(hipMemcpy(L.qkv_q4k + row0 * row_bytes, src, bytes, hipMemcpyHostToDevice));
+            break;
+        }
+        case KANSO_W_GATE:
+        case KANSO_W_UP: {
+            // 16-row groups interleaved: gate rows 16j.. at 32j, up rows 16j.. at 32j + 16
+            if ((rc = alloc(L.gate_up_q4k, 2ull * c.intermediate))) return rc;
+            const size_t off = kind == KANSO_W_GATE ? 0 : 16 * row_bytes;
+            KANSO_HIP_TRY(hipMemcpy2D(L.gate_up_q4k + off, 32 * row_bytes, src, 16 * row_bytes, 16 * row_bytes,
+                                      c.intermediate / 16, hipMemcpyHostToDevice));
+            break;
+        }
+        case KANSO_W_O:
+            if ((rc = alloc(L.o_q4k, c.hidden))) return rc;
+            KANSO_HIP_TRY(hipMemcpy(L.o_q4k, src, bytes, hipMemcpyHostToDevice));
+            break;
+        default:
+            if ((rc = alloc(L.down_q4k, c.hidden))) return rc;
+            KANSO_HIP_TRY(hipMemcpy(L.down_q4k, src, bytes, hipMemcpyHostToDevice));
+            break;
+    }
+    L.q4k_parts |= 1u << (kind - KANSO_W_Q);
+    return KANSO_OK;
 }
 
 int kanso_model_init_random(kanso_model* m, uint64_t seed, float std) {
@@ -603,6 +693,7 @@ int kanso_model_init_random(kanso_model* m, uint64_t seed, float std) {
         return KANSO_E_HIP;
     }
     uint64_t stream_id = 0;
+    for (auto& L : m->layers) L.q4k_parts = 0;  // every matrix Q8_0
     auto one = [&](uint32_t kind, uint32_t layer) -> int {
         MatrixSlot ms;
         if (!matrix_slot(m, kind, layer, ms)) return KANSO_E_INVALID_ARG;
@@ -657,6 +748,10 @@ int kanso_model_get_weight(kanso_model* m, uint32_t kind, uint32_t layer, void* 
     MatrixSlot ms;
     if ((kind == KANSO_W_LM_HEAD && m->cfg.tied_embeddings) || !matrix_slot(m, kind, layer, ms)) {
         set_error("kanso_model_get_weight: kind %u / layer %u not a weight of this model", kind, layer);
+        return KANSO_E_INVALID_ARG;
+    }
+    if (kind >= KANSO_W_Q && kind <= KANSO_W_DOWN && (m->layers[layer].q4k_parts >> (kind - KANSO_W_Q) & 1u)) {
+        set_error("kanso_model_get_weight: kind %u of layer %u is stored as Q4_K", kind, layer);
         return KANSO_E_INVALID_ARG;
     }
     const size_t want = static_cast<size_t>(ms.rows) * (ms.in / 32) * 34;

@@ -10,17 +10,18 @@ namespace kanso {
 
 // Fused decoder ops (decoder.hip).
 int op_embed(kanso_ctx* ctx, const void* table, uint32_t vocab, uint32_t hidden, const uint32_t* tokens,
-             uint32_t T, float* out, hipStream_t s, bool tiled);
+             uint32_t T, float* out, hipStream_t s, bool tiled, float scale);
 int op_qkv_rope_append(kanso_ctx* ctx, const kanso_qkv_params* p, const void* w, const float* x,
                        const float* norm_w, const int32_t* positions, const int64_t* slots, const float* cos_t,
-                       const float* sin_t, float* q, float* k_pool, float* v_pool, hipStream_t s, bool tiled);
+                       const float* sin_t, float* q, float* k_pool, float* v_pool, hipStream_t s, bool tiled,
+                       bool q4k);
 int op_gemm_residual(const void* w, const float* x, float* y, uint32_t out, uint32_t in, uint32_t T,
-                     hipStream_t s, bool tiled);
+                     hipStream_t s, bool tiled, bool q4k, float scale);
 int op_gate_up_swiglu(const void* w, const float* x, const float* norm_w, float eps, uint32_t T,
-                      uint32_t hidden, uint32_t inter, float* h, hipStream_t s, bool tiled);
+                      uint32_t hidden, uint32_t inter, float* h, hipStream_t s, bool tiled, bool q4k);
 int op_lm_head_argmax(kanso_ctx* ctx, const void* w, const float* x, const int32_t* rows, const float* norm_w,
                       float eps, uint32_t S, uint32_t hidden, uint32_t vocab, float* logits, uint32_t* tokens,
-                      hipStream_t s, bool tiled);
+                      hipStream_t s, bool tiled, float logit_mul);
 // The ragged attention with its output in the tiled activation order (the O
 // projection's input) when out_tiled is set (attention.hip).
 int op_ragged_attention(kanso_ctx* ctx, const kanso_ragged_attention_params* p, const float* q, const void* k_pool,
@@ -48,6 +49,14 @@ struct kanso_model {
         uint8_t* down = nullptr;     // packed Wdown
         float* attn_norm = nullptr;
         float* ffn_norm = nullptr;
+        // GGUF Q4_K storage (kanso_model_set_weight_q4_k): [Wq; Wk; Wv] rows, gate / up
+        // rows interleaved by 16-row groups, Wo, Wdown; null while that matrix is Q8_0.
+        // q4k_parts: bit per kind (1 << (kind - KANSO_W_Q)) uploaded as Q4_K.
+        uint8_t* qkv_q4k = nullptr;
+        uint8_t* gate_up_q4k = nullptr;
+        uint8_t* o_q4k = nullptr;
+        uint8_t* down_q4k = nullptr;
+        uint32_t q4k_parts = 0;
     };
     std::vector<Layer> layers;
     uint8_t* embed = nullptr;    // packed [vocab][hidden]

@@ -436,6 +436,7 @@ struct EpiStore {
     uint32_t ldy;
     uint32_t rows;
     uint32_t tiled = 0;
+    float scale = 1.f;  // products x scale before the store / add (Granite residual_scale)
     __device__ __forceinline__ size_t at(uint32_t m, uint32_t r) const {
         return tiled ? act_tile_off(m, r, rows / 32) : static_cast<size_t>(m) * ldy + r;
     }
@@ -467,8 +468,8 @@ struct EpiStore {
         for (int r = 0; r < 4; ++r) {
             const uint32_t m = m0 + r;
             if (m >= T) break;
-            if (r0 < rows) y[at(m, r0)] = ADD ? pr.a0[r] + v0[r] : v0[r];
-            if (NG == 2 && r1 < rows) y[at(m, r1)] = ADD ? pr.a1[r] + v1[r] : v1[r];
+            if (r0 < rows) y[at(m, r0)] = ADD ? pr.a0[r] + v0[r] * scale : v0[r] * scale;
+            if (NG == 2 && r1 < rows) y[at(m, r1)] = ADD ? pr.a1[r] + v1[r] * scale : v1[r] * scale;
         }
     }
 };
@@ -606,15 +607,17 @@ struct EpiArgmax {
     uint32_t rows;
     unsigned long long* keys;  // [T][pairs]
     uint32_t pairs;
+    float scale = 1.f;  // logits x scale (Granite: 1 / logit_scale)
     __device__ __forceinline__ void groups(uint32_t p, uint32_t& g0, uint32_t& g1) const {
         g0 = 2 * p;
         g1 = 2 * p + 1;
     }
     struct Pre {};
     __device__ __forceinline__ Pre pre(uint32_t, int, uint32_t, uint32_t) const { return {}; }
-    __device__ __forceinline__ void apply(uint32_t p, int lane, uint32_t m0, uint32_t T, const floatx4& v0,
-                                          const floatx4& v1, const Pre&) const {
+    __device__ __forceinline__ void apply(uint32_t p, int lane, uint32_t m0, uint32_t T, const floatx4& u0,
+                                          const floatx4& u1, const Pre&) const {
         const uint32_t r0 = 32 * p + (lane & 15), r1 = r0 + 16;
+        const floatx4 v0 = u0 * scale, v1 = u1 * scale;
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
             const uint32_t m = m0 + r;
@@ -676,7 +679,7 @@ struct SingleGroup {
 template <bool ADD>
 struct SingleGroup<EpiStore<ADD, 2>> {
     static constexpr bool kOk = true;
-    static EpiStore<ADD, 1> make(const EpiStore<ADD, 2>& e) { return {e.y, e.ldy, e.rows, e.tiled}; }
+    static EpiStore<ADD, 1> make(const EpiStore<ADD, 2>& e) { return {e.y, e.ldy, e.rows, e.tiled, e.scale}; }
 };
 
 // Units per workgroup for 16-token tiles. At these sizes a product's time follows

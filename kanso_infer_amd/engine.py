@@ -47,6 +47,11 @@ class ModelConfig:
     rope_theta: float = 10000.0
     max_position: int = 8192
     tied_embeddings: bool = True
+    # Granite multipliers (src/weights.rs:395-406); 0 = absent
+    embedding_scale: float = 0.0
+    attention_scale: float = 0.0
+    residual_scale: float = 0.0
+    logit_scale: float = 0.0
 
     @property
     def head_dim(self) -> int:
@@ -65,7 +70,8 @@ class ModelConfig:
         return ModelConfigC(self.hidden_size, self.num_attention_heads, self.num_key_value_heads,
                             self.head_dim, self.num_hidden_layers, self.intermediate_size,
                             self.vocab_size, self.rms_norm_eps, self.rope_theta,
-                            self.max_position, int(self.tied_embeddings))
+                            self.max_position, int(self.tied_embeddings), self.embedding_scale,
+                            self.attention_scale, self.residual_scale, self.logit_scale)
 
     def kv_cache_bytes_per_token_f32(self) -> int:
         """K and V of every layer for one token (src/config.rs kv_cache_bytes_per_token_f32)."""
@@ -121,9 +127,17 @@ class Model:
         _check(self._lib.kanso_model_set_weight(self.handle, kind, layer,
                                                 a.ctypes.data_as(C.c_void_p), a.nbytes))
 
+    def set_weight_q4_k(self, kind: int, layer: int, data: np.ndarray) -> None:
+        """GGUF Q4_K bytes of a projection matrix, kept in that format."""
+        a = np.ascontiguousarray(data)
+        _check(self._lib.kanso_model_set_weight_q4_k(self.handle, kind, layer,
+                                                     a.ctypes.data_as(C.c_void_p), a.nbytes))
+
     def load_weights(self, weights: dict) -> None:
         """weights: {"embed", "lm_head"?, "final_norm", "layers": [{"attn_norm",
-        "ffn_norm", "wq", "wk", "wv", "wo", "w_gate", "w_up", "w_down"}]}."""
+        "ffn_norm", "wq", "wk", "wv", "wo", "w_gate", "w_up", "w_down", "fmt"?}]};
+        a layer's optional "fmt" maps matrix names to their GGUF type (8 = Q8_0, the
+        default; 12 = Q4_K)."""
         self.set_weight(_capi.KANSO_W_EMBED, 0, weights["embed"])
         if not self.config.tied_embeddings:
             self.set_weight(_capi.KANSO_W_LM_HEAD, 0, weights["lm_head"])
@@ -133,8 +147,12 @@ class Model:
                  "wo": _capi.KANSO_W_O, "w_gate": _capi.KANSO_W_GATE,
                  "w_up": _capi.KANSO_W_UP, "w_down": _capi.KANSO_W_DOWN}
         for li, layer in enumerate(weights["layers"]):
+            fmt = layer.get("fmt", {})
             for name, kind in kinds.items():
-                self.set_weight(kind, li, layer[name])
+                if fmt.get(name, 8) == 12:
+                    self.set_weight_q4_k(kind, li, layer[name])
+                else:
+                    self.set_weight(kind, li, layer[name])
 
     @classmethod
     def from_gguf(cls, ctx: Context, path, max_position: int = 8192) -> "Model":

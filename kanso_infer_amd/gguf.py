@@ -7,8 +7,10 @@ pairs, one info record per tensor (name, dims with ne[0] innermost, ggml type,
 offset), then the tensor data at `general.alignment` (default 32). Tensor bytes
 are memory-mapped, never read whole.
 
-Weights go to the device model as GGUF Q8_0 rows. Two steps differ from a plain
-copy, both on the host at load time:
+Weights go to the device model as GGUF Q8_0 rows, or as GGUF Q4_K rows, which the
+model keeps in that format (the reference keeps every GGUF type as a QMatMul,
+src/weights.rs:33-39). Three steps differ from a plain copy, all on the host at
+load time:
 
 * Q / K rows are reordered per head from llama.cpp's interleaved layout
   (x0, y0, x1, y1, ...) to the rotate-half layout the RoPE epilogue uses (evens,
@@ -17,7 +19,13 @@ copy, both on the host at load time:
   matrix is one output feature, so reordering whole rows is the same map, exactly.
 * F32 / F16 / BF16 matrices are quantized to Q8_0 with this library's rounding
   (BlockQ8_0::from_f32_slice, src/quant/q8_0.rs:13-32); the reference would run
-  them in their own format. Other block formats are rejected with an error.
+  them in their own format.
+* Q6_K matrices, Q4_K embedding tables, and Q4_K matrices that share a fused
+  product with a matrix of another type (a layer's Q / K / V, its gate / up) or
+  whose rows are not whole 256-element super-blocks, are dequantized and
+  quantized again to Q8_0: an approximation of the file's weights (Q8_0 keeps
+  1/254 of each block's range), where the reference would use them exactly.
+Other block formats are rejected with an error.
 """
 from __future__ import annotations
 
@@ -31,6 +39,7 @@ GGUF_MAGIC = b"GGUF"
 
 # ggml tensor types (the public ggml enum)
 GGML_F32, GGML_F16, GGML_Q8_0, GGML_BF16 = 0, 1, 8, 30
+GGML_Q4_K, GGML_Q6_K = 12, 14
 # (block elements, block bytes) of the types this loader sizes
 _BLOCK = {GGML_F32: (1, 4), GGML_F16: (1, 2), GGML_BF16: (1, 2), GGML_Q8_0: (32, 34),
           2: (32, 18), 3: (32, 20), 6: (32, 22), 7: (32, 24), 9: (32, 36), 10: (256, 84),
@@ -150,16 +159,76 @@ class GGUFFile:
 
     def q8_0_rows(self, name: str, quantize) -> np.ndarray:
         """A matrix as GGUF Q8_0 rows ([rows][in/32] x 34 B): stored Q8_0 bytes as they
-        are; dense matrices quantized by `quantize` (f32 [rows, in] -> Q8_0 bytes)."""
+        are; dense, Q4_K and Q6_K matrices (dequantized) quantized by `quantize`
+        (f32 [rows, in] -> Q8_0 bytes)."""
         t = self._info(name)
         if len(t.shape) != 2:
             raise GGUFError(f"tensor {name}: expected a matrix, got shape {t.shape}")
+        rows, cols = t.shape[1], t.shape[0]
         if t.ggml_type == GGML_Q8_0:
             return np.asarray(self.raw(name))
         if t.ggml_type in (GGML_F32, GGML_F16, GGML_BF16):
-            return quantize(self.f32(name).reshape(t.shape[1], t.shape[0]))
-        raise GGUFError(f"tensor {name}: ggml type {t.ggml_type} cannot feed the Q8_0 model "
-                        "(Q8_0, F32, F16 and BF16 load)")
+            return quantize(self.f32(name).reshape(rows, cols))
+        if t.ggml_type == GGML_Q4_K:
+            return quantize(dequant_q4_k(self.raw(name)).reshape(rows, cols))
+        if t.ggml_type == GGML_Q6_K:
+            return quantize(dequant_q6_k(self.raw(name)).reshape(rows, cols))
+        raise GGUFError(f"tensor {name}: ggml type {t.ggml_type} cannot feed the model "
+                        "(Q8_0, Q4_K, Q6_K, F32, F16 and BF16 load)")
+
+    def ggml_type(self, name: str) -> int:
+        return self._info(name).ggml_type
+
+
+def _f16(raw: np.ndarray, at: int) -> np.ndarray:
+    return raw[:, at:at + 2].copy().view(np.float16).astype(np.float32)[:, 0]
+
+
+def dequant_q4_k(raw) -> np.ndarray:
+    """GGUF block_q4_K bytes (256 elements: f16 d, f16 dmin, 12 bytes of packed 6-bit
+    scales / mins, 128 nibble bytes) to f32: element 64 j + l is
+    d * sc(2j) * (qs[32 j + l] & 15) - dmin * m(2j), element 64 j + 32 + l the same
+    with the high nibble and sub-block 2j + 1 (BlockQ4_K::dequantize,
+    src/quant/q4_k.rs:16-55)."""
+    b = np.asarray(raw, np.uint8).reshape(-1, 144)
+    d, dmin = _f16(b, 0), _f16(b, 2)
+    sc = b[:, 4:16].astype(np.uint32)
+    scale = np.empty((b.shape[0], 8), np.float32)
+    mins = np.empty((b.shape[0], 8), np.float32)
+    for j in range(8):  # get_scale_min_k4
+        if j < 4:
+            s_, m_ = sc[:, j] & 63, sc[:, j + 4] & 63
+        else:
+            s_ = (sc[:, j + 4] & 0xF) | ((sc[:, j - 4] >> 6) << 4)
+            m_ = (sc[:, j + 4] >> 4) | ((sc[:, j] >> 6) << 4)
+        scale[:, j] = d * s_.astype(np.float32)
+        mins[:, j] = dmin * m_.astype(np.float32)
+    qs = b[:, 16:144].reshape(-1, 4, 32)
+    out = np.empty((b.shape[0], 4, 2, 32), np.float32)
+    out[:, :, 0, :] = scale[:, 0::2, None] * (qs & 15).astype(np.float32) - mins[:, 0::2, None]
+    out[:, :, 1, :] = scale[:, 1::2, None] * (qs >> 4).astype(np.float32) - mins[:, 1::2, None]
+    return out.reshape(-1)
+
+
+def dequant_q6_k(raw) -> np.ndarray:
+    """GGUF block_q6_K bytes (256 elements: 128 bytes of low nibbles, 64 bytes of high
+    bit pairs, 16 int8 sub-block scales, f16 d) to f32, from the public GGUF layout:
+    in each 128-element half h, element 32 k + l (k = 0..3, l = 0..31) takes the low
+    or high nibble of ql[64 h + 32 (k % 2) + l] (high for k >= 2) and bits 2k, 2k+1
+    of qh[32 h + l] as its top two bits; w = d * scale[8 h + 2 k + l / 16] * (q - 32)."""
+    b = np.asarray(raw, np.uint8).reshape(-1, 210)
+    ql = b[:, 0:128].reshape(-1, 2, 2, 32).astype(np.int32)   # [half][k % 2][l]
+    qh = b[:, 128:192].reshape(-1, 2, 32).astype(np.int32)     # [half][l]
+    sc = b[:, 192:208].view(np.int8).astype(np.float32).reshape(-1, 2, 8)
+    d = _f16(b, 208)
+    q = np.empty((b.shape[0], 2, 4, 32), np.int32)
+    for k in range(4):
+        low = ql[:, :, k % 2, :]
+        nib = (low >> 4) if k >= 2 else (low & 15)
+        q[:, :, k, :] = (nib | (((qh >> (2 * k)) & 3) << 4)) - 32
+    s_idx = (2 * np.arange(4)[:, None] + np.arange(32)[None, :] // 16)  # [k][l] -> scale slot
+    scale = sc[:, :, s_idx]                                              # [blk][half][k][l]
+    return (d[:, None, None, None] * scale * q.astype(np.float32)).reshape(-1)
 
 
 def interleaved_permutation(num_heads: int, head_dim: int) -> np.ndarray:
@@ -189,12 +258,7 @@ def model_config(g: GGUFFile, max_position: int = 8192):
     arch = g.metadata.get("general.architecture")
     if arch is None:
         raise GGUFError("Missing GGUF metadata key 'general.architecture'")
-    if arch == "granite":
-        scales = [k for k in ("granite.embedding_scale", "granite.attention.scale",
-                              "granite.residual_scale", "granite.logit_scale") if k in g.metadata]
-        if scales:
-            raise GGUFError(f"granite multipliers {scales} are not implemented by the device model")
-    elif arch != "llama":
+    if arch not in ("llama", "granite"):
         raise GGUFError(f"unsupported GGUF architecture '{arch}': only 'llama' and 'granite' load")
     heads = int(_meta(g, f"{arch}.attention.head_count"))
     kv_heads = int(_meta(g, f"{arch}.attention.head_count_kv"))
@@ -215,7 +279,13 @@ def model_config(g: GGUFFile, max_position: int = 8192):
         intermediate_size=int(_meta(g, f"{arch}.feed_forward_length")), vocab_size=vocab,
         rms_norm_eps=float(g.metadata.get(f"{arch}.attention.layer_norm_rms_epsilon", 1e-5)),
         rope_theta=float(g.metadata.get(f"{arch}.rope.freq_base", 10000.0)),
-        max_position=max_position, tied_embeddings="output.weight" not in g.tensors)
+        max_position=max_position, tied_embeddings="output.weight" not in g.tensors,
+        # Granite multipliers (src/weights.rs:395-406); absent = 0 = identity
+        **({k: float(g.metadata.get(key, 0.0)) for k, key in (
+            ("embedding_scale", "granite.embedding_scale"),
+            ("attention_scale", "granite.attention.scale"),
+            ("residual_scale", "granite.residual_scale"),
+            ("logit_scale", "granite.logit_scale"))} if arch == "granite" else {}))
 
 
 def load_weights(g: GGUFFile, cfg, quantize) -> dict:
@@ -224,23 +294,29 @@ def load_weights(g: GGUFFile, cfg, quantize) -> dict:
     a dense f32 [rows, in] matrix into Q8_0 rows (Model.from_gguf passes the
     device quantizer)."""
     hd = cfg.head_dim
+    H, KV = cfg.num_attention_heads, cfg.num_key_value_heads
     w = {"embed": g.q8_0_rows("token_embd.weight", quantize),
          "final_norm": g.f32("output_norm.weight"), "layers": []}
     if not cfg.tied_embeddings:
         w["lm_head"] = g.q8_0_rows("output.weight", quantize)
+    # names of each fused product (one format for all its matrices)
+    groups = (("wq", "wk", "wv"), ("wo",), ("w_gate", "w_up"), ("w_down",))
+    files = {"wq": "attn_q", "wk": "attn_k", "wv": "attn_v", "wo": "attn_output",
+             "w_gate": "ffn_gate", "w_up": "ffn_up", "w_down": "ffn_down"}
+    heads = {"wq": H, "wk": KV}
     for i in range(cfg.num_hidden_layers):
         p = f"blk.{i}."
-        w["layers"].append({
-            "attn_norm": g.f32(p + "attn_norm.weight"),
-            "ffn_norm": g.f32(p + "ffn_norm.weight"),
-            "wq": permute_q8_0_rows(g.q8_0_rows(p + "attn_q.weight", quantize),
-                                    cfg.num_attention_heads, hd),
-            "wk": permute_q8_0_rows(g.q8_0_rows(p + "attn_k.weight", quantize),
-                                    cfg.num_key_value_heads, hd),
-            "wv": g.q8_0_rows(p + "attn_v.weight", quantize),
-            "wo": g.q8_0_rows(p + "attn_output.weight", quantize),
-            "w_gate": g.q8_0_rows(p + "ffn_gate.weight", quantize),
-            "w_up": g.q8_0_rows(p + "ffn_up.weight", quantize),
-            "w_down": g.q8_0_rows(p + "ffn_down.weight", quantize),
-        })
+        layer = {"attn_norm": g.f32(p + "attn_norm.weight"),
+                 "ffn_norm": g.f32(p + "ffn_norm.weight"), "fmt": {}}
+        for names in groups:
+            tnames = [f"{p}{files[n]}.weight" for n in names]
+            q4k = all(g.ggml_type(t) == GGML_Q4_K and g.tensors[t].shape[0] % 256 == 0
+                      for t in tnames)
+            for n, t in zip(names, tnames):
+                rows = np.asarray(g.raw(t)) if q4k else g.q8_0_rows(t, quantize)
+                if n in heads:  # whole rows: the same reorder in either format
+                    rows = permute_q8_0_rows(rows, heads[n], hd)
+                layer[n] = rows
+                layer["fmt"][n] = GGML_Q4_K if q4k else GGML_Q8_0
+        w["layers"].append(layer)
     return w

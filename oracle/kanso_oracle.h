@@ -160,6 +160,12 @@ typedef struct {
     float eps, rope_theta;
     uint32_t weight_format;
     uint32_t kv_dtype; /* KANSO_KV_* of the pools passed to the forward */
+    /* Granite multipliers (src/weights.rs:395-406), 0 = absent: embedding rows x
+     * embedding_scale (model.rs:424-430); attention_scale replaces 1/sqrt(head_dim)
+     * (:755-760); attention / FFN outputs x residual_scale before each residual add
+     * (:739-744); logits x (1 / logit_scale) (:747-752). Each multiplies f32 values by
+     * the f64 factor rounded to f32, as candle's affine does. */
+    float embedding_scale, attention_scale, residual_scale, logit_scale;
 } oracle_model_config;
 
 /* Matrices in the config's weight_format and f32 norm weights; per-layer
@@ -177,6 +183,10 @@ typedef struct {
     const void* const* w_down;
     const float* const* attn_norm;
     const float* const* ffn_norm;
+    /* Q8_0 weights only: the GGUF type of each projection, [num_layers][7] in the
+     * order wq, wk, wv, wo, w_gate, w_up, w_down (8 = Q8_0, 12 = Q4_K); NULL = all
+     * Q8_0. */
+    const uint32_t* formats;
 } oracle_model_weights;
 
 /* Model::forward_batch_rows with RowSelection::LastPerSequence (src/model.rs:

@@ -65,10 +65,14 @@ int oracle_forward_batch_rows(const oracle_model_config* cfg, const oracle_model
     if (T == 0 || S == 0 || H % HKV != 0 || D % 2 != 0) return -1;
     if (!f32w && (Hd % 32 != 0 || I % 32 != 0)) return -1;
     if (static_cast<uint32_t>(cu_seqlens[S]) != T) return -1;
-    // y[t] = x[t] @ W^T for every token (LinearWeight::forward, src/weights.rs:43-45)
-    const auto linear = [&](const void* m, const float* x, float* y, uint32_t rows, uint32_t cols) {
+    // y[t] = x[t] @ W^T for every token (LinearWeight::forward, src/weights.rs:43-45);
+    // fmt: the GGUF type of a quantized matrix (8 = Q8_0, 12 = Q4_K)
+    const auto linear = [&](const void* m, const float* x, float* y, uint32_t rows, uint32_t cols, uint32_t fmt) {
         if (!f32w) {
-            oracle_gemv_q8_0(m, x, y, rows, cols, T, nthreads);
+            if (fmt == 12)
+                oracle_gemv_q4_k(m, x, y, rows, cols, T, nthreads);
+            else
+                oracle_gemv_q8_0(m, x, y, rows, cols, T, nthreads);
             return;
         }
         const float* wm = static_cast<const float*>(m);
@@ -80,7 +84,8 @@ int oracle_forward_batch_rows(const oracle_model_config* cfg, const oracle_model
                 y[static_cast<size_t>(t) * rows + r] = acc;
             }
     };
-    // Model::embed (src/model.rs:425-431): table rows (dequantized for Q8_0).
+    // Model::embed (src/model.rs:425-431): table rows (dequantized for Q8_0), times
+    // the Granite embedding scale when present.
     std::vector<float> hidden(static_cast<size_t>(T) * Hd);
     for (uint32_t t = 0; t < T; ++t) {
         if (tokens[t] >= V) return -1;
@@ -92,6 +97,8 @@ int oracle_forward_batch_rows(const oracle_model_config* cfg, const oracle_model
         const uint8_t* blocks = static_cast<const uint8_t*>(w->embed) + static_cast<size_t>(tokens[t]) * (Hd / 32) * 34;
         oracle_dequant_row_q8_0(blocks, Hd, &hidden[static_cast<size_t>(t) * Hd]);
     }
+    if (cfg->embedding_scale != 0.f)
+        for (float& v : hidden) v = v * cfg->embedding_scale;
     // rope_cos_sin (src/model.rs:667-696): rows of a table grown in 1024 steps; a
     // row depends only on its position.
     int32_t max_pos = 0;
@@ -114,7 +121,8 @@ int oracle_forward_batch_rows(const oracle_model_config* cfg, const oracle_model
     ap.block_size = block_size;
     ap.max_num_blocks_per_seq = max_blocks;
     // attention_scale: 1 / sqrt(head_dim) (src/model.rs:757-762), applied in f32.
-    ap.scale = static_cast<float>(1.0 / std::sqrt(static_cast<double>(D)));
+    ap.scale = cfg->attention_scale != 0.f ? cfg->attention_scale
+                                           : static_cast<float>(1.0 / std::sqrt(static_cast<double>(D)));
     ap.total_q = T;
     ap.kv_dtype = cfg->kv_dtype;
     if (cfg->kv_dtype > KANSO_KV_FP8 || (cfg->kv_dtype != KANSO_KV_F32 && (!k_scales || !v_scales))) return -1;
@@ -122,11 +130,13 @@ int oracle_forward_batch_rows(const oracle_model_config* cfg, const oracle_model
     ap.max_q_len = 0;
     ap.pool_layout = KANSO_POOL_TOKEN_MAJOR;
 
+    const float res_mul = cfg->residual_scale;
+    const auto fmt = [&](uint32_t l, uint32_t j) -> uint32_t { return w->formats ? w->formats[l * 7 + j] : 8u; };
     for (uint32_t l = 0; l < cfg->num_layers; ++l) {
         oracle_rmsnorm(hidden.data(), w->attn_norm[l], normed.data(), T, Hd, cfg->eps);
-        linear(w->wq[l], normed.data(), q.data(), H * D, Hd);
-        linear(w->wk[l], normed.data(), k.data(), HKV * D, Hd);
-        linear(w->wv[l], normed.data(), v.data(), HKV * D, Hd);
+        linear(w->wq[l], normed.data(), q.data(), H * D, Hd, fmt(l, 0));
+        linear(w->wk[l], normed.data(), k.data(), HKV * D, Hd, fmt(l, 1));
+        linear(w->wv[l], normed.data(), v.data(), HKV * D, Hd, fmt(l, 2));
         oracle_rope_apply(q.data(), T, H, D, positions, cos_t.data(), sin_t.data());
         oracle_rope_apply(k.data(), T, HKV, D, positions, cos_t.data(), sin_t.data());
         // write_kv_slots (src/model.rs:1673; storage.rs:219-254)
@@ -139,14 +149,18 @@ int oracle_forward_batch_rows(const oracle_model_config* cfg, const oracle_model
                                     context_lens, &ap, attn.data(), nthreads) != 0)
             return -1;
         // hidden = hidden + attn_output(attn) (src/model.rs:1716-1717)
-        linear(w->wo[l], attn.data(), proj.data(), Hd, H * D);
+        linear(w->wo[l], attn.data(), proj.data(), Hd, H * D, fmt(l, 3));
+        if (res_mul != 0.f)  // Granite: scale_residual (src/model.rs:739-744)
+            for (float& p : proj) p = p * res_mul;
         for (size_t i = 0; i < hidden.size(); ++i) hidden[i] = hidden[i] + proj[i];
         // ffn: rmsnorm, gate/up, silu * up, down, residual (src/model.rs:1719-1721, 367-380)
         oracle_rmsnorm(hidden.data(), w->ffn_norm[l], normed.data(), T, Hd, cfg->eps);
-        linear(w->w_gate[l], normed.data(), gate.data(), I, Hd);
-        linear(w->w_up[l], normed.data(), up.data(), I, Hd);
+        linear(w->w_gate[l], normed.data(), gate.data(), I, Hd, fmt(l, 4));
+        linear(w->w_up[l], normed.data(), up.data(), I, Hd, fmt(l, 5));
         oracle_silu_mul(gate.data(), up.data(), act.data(), T * I);
-        linear(w->w_down[l], act.data(), proj.data(), Hd, I);
+        linear(w->w_down[l], act.data(), proj.data(), Hd, I, fmt(l, 6));
+        if (res_mul != 0.f)
+            for (float& p : proj) p = p * res_mul;
         for (size_t i = 0; i < hidden.size(); ++i) hidden[i] = hidden[i] + proj[i];
     }
     // final norm, then lm_head on every row (RowSelection::EveryToken) or on each
@@ -171,6 +185,10 @@ int oracle_forward_batch_rows(const oracle_model_config* cfg, const oracle_model
             }
     } else {
         oracle_gemv_q8_0(w->lm_head, last_normed.data(), logits, V, Hd, R, nthreads);
+    }
+    if (cfg->logit_scale != 0.f) {  // Granite: scale_logits (src/model.rs:747-752)
+        const float mul = static_cast<float>(1.0 / static_cast<double>(cfg->logit_scale));
+        for (size_t i = 0; i < static_cast<size_t>(R) * V; ++i) logits[i] = logits[i] * mul;
     }
     return 0;
 }

@@ -344,13 +344,15 @@ class ModelConfigC(C.Structure):
     _fields_ = [(n, C.c_uint32) for n in ("hidden", "num_heads", "num_kv_heads", "head_dim",
                                           "num_layers", "intermediate", "vocab")] + [
         ("eps", C.c_float), ("rope_theta", C.c_float), ("weight_format", C.c_uint32),
-        ("kv_dtype", C.c_uint32)]
+        ("kv_dtype", C.c_uint32), ("embedding_scale", C.c_float), ("attention_scale", C.c_float),
+        ("residual_scale", C.c_float), ("logit_scale", C.c_float)]
 
 
 class ModelWeightsC(C.Structure):
     _fields_ = [("embed", C.c_void_p), ("lm_head", C.c_void_p), ("final_norm", C.c_void_p)] + [
         (n, C.POINTER(C.c_void_p)) for n in ("wq", "wk", "wv", "wo", "w_gate", "w_up", "w_down",
-                                             "attn_norm", "ffn_norm")]
+                                             "attn_norm", "ffn_norm")] + [
+        ("formats", C.c_void_p)]
 
 
 def forward_batch(cfg: dict, weights: dict, k_pools, v_pools, num_blocks, block_size, tokens,
@@ -363,7 +365,9 @@ def forward_batch(cfg: dict, weights: dict, k_pools, v_pools, num_blocks, block_
     c = ModelConfigC(cfg["hidden"], cfg["num_heads"], cfg["num_kv_heads"], cfg["head_dim"], L,
                      cfg["intermediate"], cfg["vocab"], cfg.get("eps", 1e-5),
                      cfg.get("rope_theta", 10000.0), cfg.get("weight_format", 0),
-                     cfg.get("kv_dtype", KV_F32))
+                     cfg.get("kv_dtype", KV_F32), cfg.get("embedding_scale", 0.0),
+                     cfg.get("attention_scale", 0.0), cfg.get("residual_scale", 0.0),
+                     cfg.get("logit_scale", 0.0))
     keep = []
 
     def arr(name):
@@ -373,9 +377,12 @@ def forward_batch(cfg: dict, weights: dict, k_pools, v_pools, num_blocks, block_
         return C.cast(a, C.POINTER(C.c_void_p))
 
     lm = weights.get("lm_head", weights["embed"])
+    names = ("wq", "wk", "wv", "wo", "w_gate", "w_up", "w_down")
+    fmts = np.array([[layer.get("fmt", {}).get(n, 8) for n in names] for layer in weights["layers"]],
+                    np.uint32)
+    keep.append(fmts)
     w = ModelWeightsC(_p(weights["embed"]), _p(lm), _p(weights["final_norm"]),
-                      *[arr(n) for n in ("wq", "wk", "wv", "wo", "w_gate", "w_up", "w_down",
-                                         "attn_norm", "ffn_norm")])
+                      *[arr(n) for n in (*names, "attn_norm", "ffn_norm")], _p(fmts))
     kp = (C.c_void_p * L)(*[_p(k).value for k in k_pools])
     vp = (C.c_void_p * L)(*[_p(v).value for v in v_pools])
     quant = cfg.get("kv_dtype", KV_F32) != KV_F32

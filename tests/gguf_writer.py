@@ -58,10 +58,11 @@ def interleave_rows(rot_half_rows: np.ndarray, num_heads: int, head_dim: int) ->
     return out
 
 
-def llama_file(path, cfg: dict, weights: dict, dense=(), arch="llama", extra_meta=()) -> None:
+def llama_file(path, cfg: dict, weights: dict, dense=(), arch="llama", extra_meta=(), q4k=()) -> None:
     """A llama GGUF holding `weights` (the Model.load_weights dict, rotate-half Q/K) with
     Q/K rows interleaved as llama.cpp stores them. Names in `dense` are written as F16
-    (quantized again by the loader)."""
+    (quantized again by the loader), names in `q4k` as Q4_K (this build's quantizer
+    over the dequantized Q8_0 rows)."""
     h, H, KV, D = cfg["hidden"], cfg["num_heads"], cfg["num_kv_heads"], cfg["head_dim"]
     meta = [("general.architecture", T_STRING, arch),
             (f"{arch}.block_count", T_U32, cfg["num_layers"]),
@@ -79,6 +80,10 @@ def llama_file(path, cfg: dict, weights: dict, dense=(), arch="llama", extra_met
             import oracle
             f = oracle.dequant_q8_0_rows(rows_q8, cols).astype(np.float16)
             tensors.append((name, 1, (cols, rows), f.tobytes()))
+        elif name in q4k:
+            import oracle
+            f = oracle.dequant_q8_0_rows(rows_q8, cols)
+            tensors.append((name, 12, (cols, rows), oracle.quantize_row_q4_k(f).tobytes()))
         else:
             tensors.append((name, 8, (cols, rows), np.asarray(rows_q8).tobytes()))
 

@@ -55,7 +55,7 @@ def test_reader_rejects_bad_files(tmp_path):
     p.write_bytes(p.read_bytes()[:-20])  # data cut short
     with pytest.raises(gguf.GGUFError):
         gguf.GGUFFile(p)
-    write_gguf(p, [], [("w", 12, (256, 2), bytes(2 * 144))])  # Q4_K matrix
+    write_gguf(p, [], [("w", 13, (256, 2), bytes(2 * 176))])  # Q5_K matrix: no loader
     g = gguf.GGUFFile(p)
     with pytest.raises(gguf.GGUFError):
         g.q8_0_rows("w", host_quantize)
@@ -110,11 +110,78 @@ def test_model_config_rejections(tmp_path):
     with pytest.raises(gguf.GGUFError):
         gguf.model_config(gguf.GGUFFile(p))
     llama_file(p, CFG, w, arch="granite", extra_meta=[("granite.residual_scale", T_F32, 0.2)])
-    with pytest.raises(gguf.GGUFError):
-        gguf.model_config(gguf.GGUFFile(p))
+    c = gguf.model_config(gguf.GGUFFile(p))  # Granite multipliers load (absent ones stay 0)
+    assert c.residual_scale == np.float32(0.2) and c.embedding_scale == 0.0 and c.logit_scale == 0.0
     llama_file(p, CFG, w, arch="granite")  # no multipliers: the llama decoder
     assert gguf.model_config(gguf.GGUFFile(p)).num_hidden_layers == 2
     odd = dict(CFG, num_heads=4)  # head_dim 32
     llama_file(p, odd, random_weights(dict(odd, head_dim=32), seed=4))
     with pytest.raises(gguf.GGUFError):
         gguf.model_config(gguf.GGUFFile(p))
+
+
+def test_dequant_q4_k_matches_oracle():
+    """The loader's numpy Q4_K decode equals the oracle's restatement of
+    BlockQ4_K::dequantize (src/quant/q4_k.rs:16-55) bit for bit."""
+    import oracle
+    x = np.random.default_rng(5).standard_normal((6, 512)).astype(np.float32)
+    q = oracle.quantize_row_q4_k(x)
+    want = np.concatenate([oracle.dequant_q4_k(q[i:i + 144]) for i in range(0, q.size, 144)])
+    np.testing.assert_array_equal(gguf.dequant_q4_k(q), want)
+
+
+def _pack_q6_k(q, scales, d):
+    """One block_q6_K from 256 6-bit values (0..63), 16 int8 scales and d, by the public
+    bit layout: for half h and l < 32, ql[64 h + l] holds the low nibbles of elements
+    32 0 + l (low) and 64 + l (high) of that half, ql[64 h + 32 + l] those of 32 + l
+    and 96 + l; qh[32 h + l] holds the top bit pairs of elements l, 32 + l, 64 + l and
+    96 + l at bits 0-1, 2-3, 4-5, 6-7."""
+    ql = np.zeros(128, np.uint8)
+    qh = np.zeros(64, np.uint8)
+    for h in range(2):
+        e = q[128 * h:128 * (h + 1)]
+        for l in range(32):
+            ql[64 * h + l] = (e[l] & 15) | ((e[64 + l] & 15) << 4)
+            ql[64 * h + 32 + l] = (e[32 + l] & 15) | ((e[96 + l] & 15) << 4)
+            qh[32 * h + l] = ((e[l] >> 4) | ((e[32 + l] >> 4) << 2) | ((e[64 + l] >> 4) << 4)
+                              | ((e[96 + l] >> 4) << 6))
+    return np.concatenate([ql, qh, np.asarray(scales, np.int8).view(np.uint8),
+                           np.array([d], np.float16).view(np.uint8)])
+
+
+def test_dequant_q6_k_closed_form():
+    """w = d * scale[j / 16] * (q - 32) for every element j of a block packed by the
+    bit layout; parity with candle's Q6_K decode is unpinned beyond this (candle is
+    not available), and only the loader's Q8_0 re-quantization consumes it."""
+    rng = np.random.default_rng(9)
+    for _ in range(4):
+        q = rng.integers(0, 64, 256)
+        scales = rng.integers(-128, 128, 16)
+        d = np.float16(rng.uniform(0.001, 0.1))
+        got = gguf.dequant_q6_k(_pack_q6_k(q, scales, d))
+        want = np.float32(d) * scales[np.arange(256) // 16].astype(np.float32) * (q - 32).astype(np.float32)
+        np.testing.assert_array_equal(got, want)
+
+
+def test_q4_k_matrices_kept_and_mixed_groups_requantized(tmp_path):
+    """Q4_K projections stay Q4_K bytes (Q / K rows reordered whole); a Q4_K gate whose
+    up is Q8_0 is decoded and quantized again to Q8_0 (the pair shares one product)."""
+    import oracle
+    cfg = dict(CFG, hidden=256, intermediate=512, num_heads=4)
+    w = random_weights(cfg, seed=6)
+    p = tmp_path / "k.gguf"
+    q4 = ("blk.0.attn_q.weight", "blk.0.attn_k.weight", "blk.0.attn_v.weight",
+          "blk.0.ffn_down.weight", "blk.1.ffn_gate.weight")
+    llama_file(p, cfg, w, q4k=q4)
+    g = gguf.GGUFFile(p)
+    got = gguf.load_weights(g, gguf.model_config(g), host_quantize)
+    L0, L1 = got["layers"]
+    assert L0["fmt"] == dict(wq=12, wk=12, wv=12, wo=8, w_gate=8, w_up=8, w_down=12)
+    assert L1["fmt"]["w_gate"] == 8 and L1["fmt"]["w_up"] == 8
+    # Q4_K rows: the file's rows in rotate-half order
+    want_q = oracle.quantize_row_q4_k(oracle.dequant_q8_0_rows(w["layers"][0]["wq"], 256))
+    np.testing.assert_array_equal(np.asarray(L0["wq"]).ravel(), want_q)
+    # the mixed gate: Q4_K decoded, then Q8_0
+    gate_q4 = oracle.quantize_row_q4_k(oracle.dequant_q8_0_rows(w["layers"][1]["w_gate"], 256))
+    np.testing.assert_array_equal(np.asarray(L1["w_gate"]).ravel(),
+                                  host_quantize(gguf.dequant_q4_k(gate_q4).reshape(512, 256)).ravel())

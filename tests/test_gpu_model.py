@@ -303,3 +303,45 @@ def test_forward_refuses_bad_tokens_and_reports_device_flags(ctx):
     toks = m.forward(plan, np.array([1, 2, 3], np.uint32), np.array([0], np.uint32))
     assert toks.shape == (1,)
     m.close()
+
+
+@pytest.mark.parametrize("variant", ["q4_k", "granite_q4_k"])
+def test_model_from_gguf_q4_k_and_granite(ctx, tmp_path, variant):
+    """GGUF files with Q4_K projections kept in that format on the device (every
+    projection of layer 0; layer 1's down, and a Q4_K gate next to a Q8_0 up, which
+    the loader turns into Q8_0) and, for Granite, the four multipliers
+    (src/weights.rs:395-406; src/model.rs:424-430, 739-760): logits equal the oracle
+    model's on the weights the host reader maps from the same file."""
+    from gguf_writer import llama_file, T_F32
+    from kanso_infer_amd import gguf
+    bs, nblocks = 16, 40
+    w = random_weights(SMALL, seed=41)
+    q4 = tuple(f"blk.0.{n}.weight" for n in ("attn_q", "attn_k", "attn_v", "attn_output",
+                                              "ffn_gate", "ffn_up", "ffn_down")) + (
+        "blk.1.ffn_down.weight", "blk.1.ffn_gate.weight")
+    granite = variant.startswith("granite")
+    meta = [("granite.embedding_scale", T_F32, 12.0), ("granite.attention.scale", T_F32, 0.0078125),
+            ("granite.residual_scale", T_F32, 0.22), ("granite.logit_scale", T_F32, 8.0)] if granite else []
+    path = tmp_path / f"{variant}.gguf"
+    llama_file(path, SMALL, w, q4k=q4, arch="granite" if granite else "llama", extra_meta=meta)
+    gm = Model.from_gguf(ctx, path, max_position=4096)
+    gm.alloc_kv(nblocks, bs, 512, 64)
+    g = gguf.GGUFFile(path)
+    mc = gguf.model_config(g)
+    w_host = gguf.load_weights(g, mc, lambda a: oracle.quantize_row_q8_0(np.ascontiguousarray(a, np.float32)))
+    assert w_host["layers"][0]["fmt"]["w_gate"] == 12 and w_host["layers"][1]["fmt"]["w_gate"] == 8
+    ocfg = dict(SMALL, embedding_scale=mc.embedding_scale, attention_scale=mc.attention_scale,
+                residual_scale=mc.residual_scale, logit_scale=mc.logit_scale)
+    if granite:
+        assert mc.logit_scale == 8.0 and mc.residual_scale == np.float32(0.22)
+    om = OracleModel(ocfg, w_host, nblocks, bs)
+    rng = np.random.default_rng(13)
+    for step, plan in enumerate(mixed_plans(rng, bs, SMALL["vocab"], nblocks)):
+        rows, toks, tabs = compact(plan, bs)
+        S = rows.shape[0]
+        logits = torch.empty(S * SMALL["vocab"], device="cuda:0")
+        gm.forward(rows, toks, tabs, logits=logits)
+        ctx.check_device_status()
+        assert_close(host(logits).reshape(S, SMALL["vocab"]), om.logits(plan),
+                     what=f"{variant} logits step {step}")
+    gm.close()
