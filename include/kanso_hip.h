@@ -180,7 +180,9 @@ int kanso_paged_attention_v2(kanso_ctx* ctx, const kanso_paged_attention_params*
  * context_lens[s] - q_len + i and attends keys 0..=that position (the offset causal
  * mask of src/model.rs:1510-1527; a decode row attends its whole context).
  * q and out are [total_q][num_heads][head_dim] f32. k_scales/v_scales are unused
- * for KANSO_KV_F32. Query head h reads KV head h / (num_heads/num_kv_heads). */
+ * for KANSO_KV_F32. Query head h reads KV head h / (num_heads/num_kv_heads).
+ * cu_seqlens may be null for a decode batch (total_q == num_seqs, max_q_len 1):
+ * one row per sequence. */
 /* The split-K partition for kanso_ragged_paged_attention's partition_size, from the
  * step's host-side query and context lengths (num_seqs entries each), which the
  * caller that planned the step holds (Engine::step's query_lens / context_lens,

@@ -199,7 +199,7 @@ def gpu_paged_attention_v2(ctx: Context, q, k_cache, v_cache, block_tables, cont
 
 def ragged_paged_attention(ctx: Context, *, q: torch.Tensor, k_pool: torch.Tensor,
                            v_pool: torch.Tensor, block_tables: torch.Tensor,
-                           cu_seqlens: torch.Tensor, context_lens: torch.Tensor,
+                           cu_seqlens: torch.Tensor | None, context_lens: torch.Tensor,
                            out: torch.Tensor, num_heads: int, num_kv_heads: int, head_dim: int,
                            block_size: int, scale: float, kv_dtype: int = KANSO_KV_F32,
                            k_scales: torch.Tensor | None = None,
@@ -207,8 +207,9 @@ def ragged_paged_attention(ctx: Context, *, q: torch.Tensor, k_pool: torch.Tenso
                            max_q_len: int = 0, pool_layout: int = 0, partition_size: int = 0,
                            chunk_partition_size: int = 0,
                            stream: torch.cuda.Stream | None = None) -> None:
-    """Mixed prefill + decode attention over the paged pool (kanso_ragged_paged_attention)."""
-    num_seqs = cu_seqlens.numel() - 1
+    """Mixed prefill + decode attention over the paged pool (kanso_ragged_paged_attention).
+    cu_seqlens None: a decode batch, one query row per sequence."""
+    num_seqs = cu_seqlens.numel() - 1 if cu_seqlens is not None else context_lens.numel()
     max_blocks = block_tables.numel() // max(num_seqs, 1)
     total_q = q.numel() // (num_heads * head_dim)
     p = RaggedAttentionParamsC(num_seqs, num_heads, num_kv_heads, head_dim, block_size, max_blocks,

@@ -147,7 +147,7 @@ template <bool CHUNK>
 __device__ void load_seq_table(const AttnArgs& a, SeqTable& st) {
     const uint32_t tid = threadIdx.x, S = a.num_seqs;
     for (uint32_t s = tid; s <= S; s += kThreads) {
-        st.cu[s] = a.cu[s];
+        st.cu[s] = a.cu ? a.cu[s] : static_cast<int32_t>(s);  // null: one row per sequence
         if (s < S) st.ctx[s] = static_cast<int32_t>(a.ctx_lens[s]);
     }
     __syncthreads();
@@ -1366,11 +1366,6 @@ __global__ __launch_bounds__(kThreads) void attn_reduce(AttnArgs a) {
     }
 }
 
-__global__ void iota_cu(int32_t* cu, uint32_t n) {
-    const uint32_t i = blockIdx.x * blockDim.x + threadIdx.x;
-    if (i <= n) cu[i] = static_cast<int32_t>(i);
-}
-
 using Stage1Fn = void (*)(AttnArgs);
 
 // Batches with prefill chunks get the kernel with the MFMA chunk path (it needs
@@ -1512,7 +1507,8 @@ int run_ragged(kanso_ctx* ctx, const kanso_ragged_attention_params* p, const flo
                const uint32_t* tables, const int32_t* cu, const uint32_t* ctx_lens, float* out,
                hipStream_t stream, const char* who, bool out_tiled = false, void* fixed_scratch = nullptr) {
     const uint32_t S = p->num_seqs, H = p->num_heads, HKV = p->num_kv_heads, D = p->head_dim;
-    if (!q || !kp || !vp || !tables || !cu || !ctx_lens || !out) {
+    const bool one_row_each = p->total_q == S && p->max_q_len == 1;
+    if (!q || !kp || !vp || !tables || (!cu && !one_row_each) || !ctx_lens || !out) {
         set_error("%s: null buffer", who);
         return KANSO_E_INVALID_ARG;
     }
@@ -1851,13 +1847,8 @@ int kanso_paged_attention_v2(kanso_ctx* ctx, const kanso_paged_attention_params*
     int rc = kanso_validate_paged_attention_params(p);
     if (rc) return rc;
     hipStream_t s = as_stream(stream);
-    // One query row per sequence: cu_seqlens = 0..=num_seqs in the context's
-    // auxiliary buffer (kept apart from scratch, which run_ragged may grow).
-    rc = ensure_aux(ctx, (static_cast<size_t>(p->num_seqs) + 1) * sizeof(int32_t));
-    if (rc) return rc;
-    int32_t* cu_buf = static_cast<int32_t*>(ctx->aux);
-    hipLaunchKernelGGL(iota_cu, dim3((p->num_seqs + 256) / 256), dim3(256), 0, s, cu_buf, p->num_seqs);
-    KANSO_LAUNCH_CHECK();
+    // One query row per sequence: the kernel reads a null cu_seqlens as 0..=num_seqs
+    // (no extra launch to write it).
     kanso_ragged_attention_params rp{};
     rp.num_seqs = p->num_seqs;
     rp.num_heads = p->num_heads;
@@ -1871,7 +1862,7 @@ int kanso_paged_attention_v2(kanso_ctx* ctx, const kanso_paged_attention_params*
     rp.num_blocks = 0;  // the reference call carries no pool size
     rp.max_q_len = 1;
     rp.pool_layout = KANSO_POOL_TOKEN_MAJOR;
-    return run_ragged(ctx, &rp, q, k_cache, v_cache, nullptr, nullptr, block_tables, cu_buf,
+    return run_ragged(ctx, &rp, q, k_cache, v_cache, nullptr, nullptr, block_tables, nullptr,
                       context_lens, out, s, "kanso_paged_attention_v2");
 }
 

@@ -39,9 +39,6 @@ struct kanso_ctx {
     size_t scratch_bytes = 0;
     // Events reused by the profiling hooks.
     std::vector<hipEvent_t> event_pool;
-    // Grow-only auxiliary buffer for small per-call index arrays.
-    void* aux = nullptr;
-    size_t aux_bytes = 0;
     // Grow-only buffer of 64-bit argmax keys (lm_head epilogue).
     void* keys = nullptr;
     size_t keys_bytes = 0;
@@ -71,7 +68,6 @@ int ensure_scratch(kanso_ctx* ctx, size_t bytes);
 // Resolves the device address of the fixed attention scratch array on the current
 // device (attention.hip); called once per context by kanso_create.
 int noalloc_scratch_init(void** ptr);
-int ensure_aux(kanso_ctx* ctx, size_t bytes);
 int ensure_keys(kanso_ctx* ctx, size_t bytes);
 
 // Profiling hooks around one kernel launch (no-ops unless ctx->profiling).

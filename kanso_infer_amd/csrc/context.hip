@@ -32,20 +32,6 @@ int ensure_scratch(kanso_ctx* ctx, size_t bytes) {
     return KANSO_OK;
 }
 
-int ensure_aux(kanso_ctx* ctx, size_t bytes) {
-    if (bytes <= ctx->aux_bytes) return KANSO_OK;
-    size_t want = align_up(bytes + bytes / 2, 1 << 16);
-    if (ctx->aux) {
-        KANSO_HIP_TRY(hipDeviceSynchronize());
-        KANSO_HIP_TRY(hipFree(ctx->aux));
-        ctx->aux = nullptr;
-        ctx->aux_bytes = 0;
-    }
-    KANSO_HIP_TRY(hipMalloc(&ctx->aux, want));
-    ctx->aux_bytes = want;
-    return KANSO_OK;
-}
-
 int ensure_keys(kanso_ctx* ctx, size_t bytes) {
     if (bytes <= ctx->keys_bytes) return KANSO_OK;
     size_t want = align_up(bytes + bytes / 2, 1 << 16);
@@ -162,7 +148,6 @@ int kanso_destroy(kanso_ctx* ctx) {
         (void)hipEventDestroy(rec.stop);
     }
     if (ctx->scratch) (void)hipFree(ctx->scratch);
-    if (ctx->aux) (void)hipFree(ctx->aux);
     if (ctx->keys) (void)hipFree(ctx->keys);
     if (ctx->status) (void)hipFree(ctx->status);
     for (hipEvent_t e : ctx->event_pool) (void)hipEventDestroy(e);

@@ -57,13 +57,13 @@ def fill_pool(batch, kv_dtype: int, seed: int):
 
 
 def run_ragged_gpu(ctx, batch, q, kp, vp, ks=None, vs=None, kv_dtype=0, partition_size=0,
-                   chunk_partition_size=0):
+                   chunk_partition_size=0, cu_seqlens=True):
     out = torch.empty(batch.total_q * batch.num_heads * batch.head_dim, dtype=torch.float32,
                       device="cuda:0")
     K.ragged_paged_attention(
         ctx, q=dev(q), k_pool=dev(kp), v_pool=dev(vp),
         k_scales=None if ks is None else dev(ks), v_scales=None if vs is None else dev(vs),
-        block_tables=dev(batch.block_tables.ravel()), cu_seqlens=dev(batch.cu_seqlens),
+        block_tables=dev(batch.block_tables.ravel()), cu_seqlens=dev(batch.cu_seqlens) if cu_seqlens else None,
         context_lens=dev(batch.context_lens.astype(np.uint32)), out=out,
         num_heads=batch.num_heads, num_kv_heads=batch.num_kv_heads, head_dim=batch.head_dim,
         block_size=batch.block_size, scale=batch.scale, kv_dtype=kv_dtype,

@@ -284,6 +284,22 @@ def test_ragged_equals_decode_entry(ctx):
     np.testing.assert_array_equal(host(out), ragged)
 
 
+def test_decode_batch_without_cu_seqlens(ctx):
+    """A null cu_seqlens reads as one row per sequence: bit-identical to passing 0..=S;
+    a batch with a multi-row sequence still needs it."""
+    b = workloads.config1_decode(seed_offset=4)
+    kp, vp, _, _ = fill_pool(b, oracle.KV_F32, 11)
+    q = np.random.default_rng(12).standard_normal(
+        b.total_q * b.num_heads * b.head_dim).astype(np.float32)
+    np.testing.assert_array_equal(run_ragged_gpu(ctx, b, q, kp, vp, cu_seqlens=False),
+                                  run_ragged_gpu(ctx, b, q, kp, vp))
+    m = workloads.small_mixed(3)
+    kp, vp, _, _ = fill_pool(m, oracle.KV_F32, 13)
+    q = np.zeros(m.total_q * m.num_heads * m.head_dim, np.float32)
+    with pytest.raises(K.EngineError, match="null buffer"):
+        run_ragged_gpu(ctx, m, q, kp, vp, cu_seqlens=False)
+
+
 def test_fp8_pool_decodes_every_finite_code(ctx):
     """Contexts of one token: the output is exactly that token's V row, so every
     finite E4M3 code (254 of 256) is decoded by the kernel and compared bit for bit."""
