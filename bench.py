@@ -166,6 +166,58 @@ class AttnBench:
                     call_gbps=abytes / (ms * 1e-3) / 1e9)
 
 
+def config3_append(ab, steps=200):
+    """Config 3's fused append + quantize of the step's new K/V rows (one token per
+    sequence, written at its last position), timed alone (HIP events around each
+    launch) and together with the attention call it precedes in a decode step.
+    Algorithmic bytes per token: K and V f32 rows read, the slot read, the quantized
+    rows and their scales written."""
+    torch, K, ctx = ab.torch, ab.K, ab.ctx
+    b0 = ab.batches[0]
+    hkv, d, bs = b0.num_kv_heads, b0.head_dim, b0.block_size
+    g = torch.Generator(device="cuda:0")
+    g.manual_seed(33)
+    calls = []
+    for b in ab.batches:
+        last = b.context_lens - 1
+        blk = b.block_tables[np.arange(b.num_seqs), last // bs].astype(np.int64)
+        slots = torch.from_numpy(blk * bs + last % bs).to("cuda:0")
+        kk = torch.randn(b.num_seqs * hkv * d, generator=g, device="cuda:0")
+        calls.append((slots, kk, torch.randn_like(kk)))
+
+    def append(i):
+        slots, kk, vv = calls[i % len(calls)]
+        K.kv_append(ctx, ab.kv_dtype, kk, vv, slots, ab.num_blocks, bs, hkv, d, ab.k, ab.v, ab.ks, ab.vs)
+
+    for i in range(10):
+        append(i)
+    torch.cuda.synchronize()
+    ctx.set_profiling(True)
+    for i in range(steps):
+        append(i)
+    torch.cuda.synchronize()
+    a_ms, a_n = ctx.kernel_time("append")
+    ctx.set_profiling(False)
+    s_ev, e_ev = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    s_ev.record()
+    for i in range(steps):
+        append(i)
+        ab.call(i)
+    e_ev.record()
+    torch.cuda.synchronize()
+    ctx.check_device_status()
+    n_tok = b0.num_seqs
+    scale_b = (2 * hkv * (d // 32) * 2) if ab.kv_dtype == K.KANSO_KV_Q8_0 else 2 * hkv * 4
+    per_tok = 2 * hkv * d * 4 + 8 + 2 * hkv * d + scale_b
+    us = a_ms / max(a_n, 1) * 1e3
+    return dict(tokens=n_tok, us=round(us, 2), bytes_per_token=per_tok,
+                gbps=round(n_tok * per_tok / (us * 1e-6) / 1e9, 1),
+                hbm_frac=round(n_tok * per_tok / (us * 1e-6) / HBM_PEAK, 5),
+                ms_per_step_append_plus_attention=round(s_ev.elapsed_time(e_ev) / steps, 4),
+                timing="append: HIP events around each launch; step: one event pair around "
+                       "append + attention calls")
+
+
 def copy_bandwidth(torch, nbytes=2 << 30, iters=10):
     a = torch.empty(nbytes // 4, dtype=torch.float32, device="cuda:0").normal_()
     b = torch.empty_like(a)
@@ -774,7 +826,8 @@ def main():
             r3 = b3.run(args.steps, args.warmup)
             r3["hbm_frac_stage1"] = r3["stage1_gbps"] * 1e9 / HBM_PEAK
             extras[name] = {k: (round(v, 4) if isinstance(v, float) else v) for k, v in r3.items()}
-            log(f"{name}: {r3}")
+            extras[name]["append"] = config3_append(b3, args.steps)
+            log(f"{name}: {extras[name]}")
             del b3
             torch.cuda.empty_cache()
 

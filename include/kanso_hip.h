@@ -335,6 +335,20 @@ int kanso_qkv_rope_append(kanso_ctx* ctx, const kanso_qkv_params* p, const void*
                           const float* sin_table, float* q_out, float* k_pool, float* v_pool,
                           kanso_stream_t stream);
 
+/* kanso_qkv_rope_append for a 1-byte pool (kv_dtype KANSO_KV_INT8, KANSO_KV_FP8 or
+ * KANSO_KV_Q8_0, the layouts of kanso_kv_append): each token's K and V rows are
+ * rotated, quantized (quantize_head_slice, src/kv_cache/quantized_storage.rs:452-486;
+ * BlockQ8_0::from_f32_slice, src/quant/q8_0.rs:13-32) and written with their scales
+ * to pool row slot_mapping[t] in the product's epilogue, the bytes
+ * kanso_qkv_rope_append into F32 rows followed by kanso_kv_append would write
+ * (write_kv_slots of the quantized storage, src/kv_cache/kind.rs:348-374), in one
+ * kernel. */
+int kanso_qkv_rope_append_quant(kanso_ctx* ctx, const kanso_qkv_params* p, const void* packed_qkv,
+                                const float* x, const float* norm_w, const int32_t* positions,
+                                const int64_t* slot_mapping, const float* cos_table,
+                                const float* sin_table, float* q_out, uint32_t kv_dtype, void* k_pool,
+                                void* v_pool, void* k_scales, void* v_scales, kanso_stream_t stream);
+
 /* h[t][j] = silu(g) * u with g, u the gate / up projections of RMSNorm(x[t]) *
  * norm_w (forward_mlp_block, src/model.rs:367-380); packed_gate_up interleaves the
  * gate and up groups (kanso_q8_0_pack stride 2). intermediate % 16 == 0. */

@@ -14,7 +14,7 @@ through the C ABI. It mirrors the reference's own entry points for the path:
   kv_append / kv_reset_blocks <- KvStorageKind::write_kv_slots / reset_block
   gemv_q8_0 / gemv_q4_k    <- LinearWeight::forward on Q8_0 / Q4_K weights
   q8_0_pack, gemm_q8_0, gemm_q8_0_residual, embed_q8_0, qkv_rope_append,
-  gate_up_swiglu, lm_head_argmax
+  qkv_rope_append_quant, gate_up_swiglu, lm_head_argmax
                            <- the layer body of Model::forward_batch_rows
                               (src/model.rs:1569-1739) on packed Q8_0 weights
 
@@ -39,6 +39,7 @@ __all__ = [
     "ragged_paged_attention", "pack_step", "kv_append", "kv_reset_blocks", "gemv_q8_0",
     "gemv_q4_k", "KANSO_KV_F32", "KANSO_KV_INT8", "KANSO_KV_Q8_0", "KANSO_KV_FP8", "ragged_partition_size", "ragged_chunk_partition_size", "q8_0_packed_bytes",
     "q8_0_pack", "gemm_q8_0", "gemm_q8_0_residual", "embed_q8_0", "qkv_rope_append",
+    "qkv_rope_append_quant",
     "gate_up_swiglu", "lm_head_argmax",
 ]
 
@@ -416,6 +417,25 @@ def qkv_rope_append(ctx: Context, packed_qkv: torch.Tensor, x: torch.Tensor, nor
         ctx.handle, C.byref(p), _ptr(packed_qkv), _ptr(x), _ptr(norm_w), _ptr(positions),
         _ptr(slot_mapping), _ptr(cos_t), _ptr(sin_t), _ptr(q_out), _ptr(k_pool), _ptr(v_pool),
         _stream(stream)))
+
+
+def qkv_rope_append_quant(ctx: Context, packed_qkv: torch.Tensor, x: torch.Tensor,
+                          norm_w: torch.Tensor, positions: torch.Tensor, slot_mapping: torch.Tensor,
+                          cos_t: torch.Tensor, sin_t: torch.Tensor, q_out: torch.Tensor,
+                          kv_dtype: int, k_pool: torch.Tensor, v_pool: torch.Tensor,
+                          k_scales: torch.Tensor, v_scales: torch.Tensor, *, hidden: int,
+                          num_heads: int, num_kv_heads: int, num_blocks: int, block_size: int,
+                          eps: float = 1e-5, head_dim: int = 64,
+                          stream: torch.cuda.Stream | None = None) -> None:
+    """qkv_rope_append into a 1-byte pool: K/V rows quantized (with their scales) into
+    pool row slot_mapping[t] in the product's epilogue."""
+    T = x.numel() // hidden
+    p = _capi.QkvParamsC(T, hidden, num_heads, num_kv_heads, head_dim,
+                         cos_t.numel() // (head_dim // 2), eps, num_blocks, block_size)
+    _check(ctx._lib.kanso_qkv_rope_append_quant(
+        ctx.handle, C.byref(p), _ptr(packed_qkv), _ptr(x), _ptr(norm_w), _ptr(positions),
+        _ptr(slot_mapping), _ptr(cos_t), _ptr(sin_t), _ptr(q_out), kv_dtype, _ptr(k_pool),
+        _ptr(v_pool), _ptr(k_scales), _ptr(v_scales), _stream(stream)))
 
 
 def gate_up_swiglu(ctx: Context, packed_gate_up: torch.Tensor, x: torch.Tensor,

@@ -168,6 +168,8 @@ SIGNATURES: dict[str, tuple] = {
     "kanso_embed_q8_0": (_I, [_P, _P, _U, _U, _P, _U, _P, _P]),
     "kanso_qkv_rope_append": (_I, [_P, C.POINTER(QkvParamsC), _P, _P, _P, _P, _P, _P, _P, _P, _P,
                                    _P, _P]),
+    "kanso_qkv_rope_append_quant": (_I, [_P, C.POINTER(QkvParamsC), _P, _P, _P, _P, _P, _P, _P, _P, _U,
+                                         _P, _P, _P, _P, _P]),
     "kanso_gate_up_swiglu": (_I, [_P, _P, _P, _P, C.c_float, _U, _U, _U, _P, _P]),
     "kanso_lm_head_argmax": (_I, [_P, _P, _P, _P, _P, C.c_float, _U, _U, _U, _P, _P, _P]),
     "kanso_quantize_q8_0": (_I, [_P, _P, C.c_uint64, _P, _P]),

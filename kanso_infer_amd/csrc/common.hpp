@@ -167,6 +167,28 @@ __device__ __forceinline__ uint32_t f32_to_e4m3(float x) {
     return sign | static_cast<uint32_t>(__builtin_rintf(__uint_as_float(a) * 512.0f));
 }
 
+// Row scales of the 1-byte KV quantizers, shared by the append kernel and the QKV
+// epilogue so both write the same bytes. quantize_head_slice
+// (quantized_storage.rs:452-486): INT8 scale = amax > 0 ? amax / 127 : 1, q =
+// round(x / scale) clamped to +-127; FP8 scale = 2^ceil(log2(amax / 64)) (1 for
+// amax = 0), q = E4M3(x / scale). BlockQ8_0::from_f32_slice (src/quant/q8_0.rs:13-32):
+// d = amax / 127, q = round(x / d) clamped to [-128, 127] (0 for d = 0). All steps
+// are IEEE-exact or correctly rounded: this library is built with correctly rounded
+// division, roundf rounds half away from zero like Rust's f32::round.
+__device__ __forceinline__ float int8_row_scale(float amax) { return amax > 0.f ? amax / 127.0f : 1.0f; }
+__device__ __forceinline__ float fp8_row_scale(float amax) {
+    float scale = 1.0f;
+    if (amax > 0.f) {
+        int e2;
+        const float fr = frexpf(amax / 64.0f, &e2);
+        scale = ldexpf(1.0f, fr == 0.5f ? e2 - 1 : e2);
+    }
+    return scale;
+}
+__device__ __forceinline__ int8_t quant_i8(float x, float inv, float lo) {
+    return static_cast<int8_t>(fminf(fmaxf(roundf(x * inv), lo), 127.0f));
+}
+
 // Four E4M3 bytes of a word -> f32 with gfx950's packed conversion
 // (v_cvt_pk_f32_fp8: OCP E4M3FN on CDNA4), two bytes per instruction.
 __device__ __forceinline__ void e4m3x4_to_f32(uint32_t w, float& a, float& b, float& c, float& d) {

@@ -101,6 +101,55 @@ int op_qkv_rope_append(kanso_ctx* ctx, const kanso_qkv_params* p, const void* w,
     return launch_q8_gemm(WPacked{static_cast<const uint8_t*>(w), p->hidden / 32}, xa, epi, pairs, s);
 }
 
+template <int KVT>
+int qkv_rope_quant(kanso_ctx* ctx, const kanso_qkv_params* p, const void* w, const XIn& xa, const int32_t* positions,
+                   const int64_t* slots, const float* cos_t, const float* sin_t, float* q, void* k_pool, void* v_pool,
+                   void* k_scales, void* v_scales, hipStream_t s, bool q4k) {
+    EpiQkvRopeQ<KVT> epi;
+    epi.q = q;
+    epi.k_pool = static_cast<uint8_t*>(k_pool);
+    epi.v_pool = static_cast<uint8_t*>(v_pool);
+    epi.k_scales = k_scales;
+    epi.v_scales = v_scales;
+    epi.positions = positions;
+    epi.slots = slots;
+    epi.cos_t = cos_t;
+    epi.sin_t = sin_t;
+    epi.status = ctx->status;
+    epi.num_heads = p->num_heads;
+    epi.num_kv_heads = p->num_kv_heads;
+    epi.max_pos = p->max_pos;
+    epi.num_slots = static_cast<int64_t>(p->num_blocks) * p->block_size;
+    const uint32_t pairs = 2 * (p->num_heads + 2 * p->num_kv_heads);
+    if (q4k)
+        return launch_q8_gemm_paired(WQ4K{static_cast<const uint8_t*>(w), p->hidden / 256, 32 * pairs}, xa, epi,
+                                     pairs, s);
+    return launch_q8_gemm_paired(WPacked{static_cast<const uint8_t*>(w), p->hidden / 32}, xa, epi, pairs, s);
+}
+
+// The QKV product with RoPE whose K / V rows are quantized into a 1-byte pool in its
+// epilogue (one kernel: the f32 path's op_qkv_rope_append plus kanso_kv_append).
+int op_qkv_rope_quant(kanso_ctx* ctx, const kanso_qkv_params* p, const void* w, const float* x, const float* norm_w,
+                      const int32_t* positions, const int64_t* slots, const float* cos_t, const float* sin_t,
+                      float* q, uint32_t kv_dtype, void* k_pool, void* v_pool, void* k_scales, void* v_scales,
+                      hipStream_t s, bool tiled, bool q4k) {
+    XIn xa{x, nullptr, norm_w, p->eps, p->hidden, p->num_tokens, p->hidden, tiled ? 1u : 0u};
+    switch (kv_dtype) {
+        case KANSO_KV_INT8:
+            return qkv_rope_quant<KANSO_KV_INT8>(ctx, p, w, xa, positions, slots, cos_t, sin_t, q, k_pool, v_pool,
+                                                 k_scales, v_scales, s, q4k);
+        case KANSO_KV_FP8:
+            return qkv_rope_quant<KANSO_KV_FP8>(ctx, p, w, xa, positions, slots, cos_t, sin_t, q, k_pool, v_pool,
+                                                k_scales, v_scales, s, q4k);
+        case KANSO_KV_Q8_0:
+            return qkv_rope_quant<KANSO_KV_Q8_0>(ctx, p, w, xa, positions, slots, cos_t, sin_t, q, k_pool, v_pool,
+                                                 k_scales, v_scales, s, q4k);
+        default:
+            set_error("qkv_rope_quant: kv dtype %u is not a 1-byte pool", kv_dtype);
+            return KANSO_E_INVALID_ARG;
+    }
+}
+
 int op_gemm_residual(const void* w, const float* x, float* y, uint32_t out, uint32_t in, uint32_t T,
                      hipStream_t s, bool tiled, bool q4k, float scale) {
     XIn xa{x, nullptr, nullptr, 0.f, in, T, in, tiled ? 1u : 0u};
@@ -174,6 +223,29 @@ int kanso_qkv_rope_append(kanso_ctx* ctx, const kanso_qkv_params* p, const void*
     }
     return op_qkv_rope_append(ctx, p, packed_qkv, x, norm_w, positions, slot_mapping, cos_table, sin_table, q_out,
                               k_pool, v_pool, as_stream(stream), false, false);
+}
+
+int kanso_qkv_rope_append_quant(kanso_ctx* ctx, const kanso_qkv_params* p, const void* packed_qkv, const float* x,
+                                const float* norm_w, const int32_t* positions, const int64_t* slot_mapping,
+                                const float* cos_table, const float* sin_table, float* q_out, uint32_t kv_dtype,
+                                void* k_pool, void* v_pool, void* k_scales, void* v_scales, kanso_stream_t stream) {
+    if (!ctx || !p || !packed_qkv || !x || !norm_w || !positions || !slot_mapping || !cos_table || !sin_table ||
+        !q_out || !k_pool || !v_pool || !k_scales || !v_scales) {
+        set_error("kanso_qkv_rope_append_quant: null argument");
+        return KANSO_E_INVALID_ARG;
+    }
+    if (p->head_dim != 64) {
+        set_error("kanso_qkv_rope_append_quant: head_dim %u (this kernel handles 64)", p->head_dim);
+        return KANSO_E_INVALID_SHAPE;
+    }
+    if (p->num_tokens == 0 || p->hidden == 0 || p->hidden % 32 != 0 || p->num_heads == 0 ||
+        p->num_kv_heads == 0 || p->max_pos == 0 || p->block_size == 0 || !aligned16(x)) {
+        set_error("kanso_qkv_rope_append_quant: bad shape (tokens %u, hidden %u, heads %u/%u, max_pos %u)",
+                  p->num_tokens, p->hidden, p->num_heads, p->num_kv_heads, p->max_pos);
+        return KANSO_E_INVALID_SHAPE;
+    }
+    return op_qkv_rope_quant(ctx, p, packed_qkv, x, norm_w, positions, slot_mapping, cos_table, sin_table, q_out,
+                             kv_dtype, k_pool, v_pool, k_scales, v_scales, as_stream(stream), false, false);
 }
 
 int kanso_gemm_q8_0_residual(kanso_ctx* ctx, const void* packed, const float* x, float* y, uint32_t out_features,

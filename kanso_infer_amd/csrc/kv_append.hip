@@ -69,15 +69,12 @@ __device__ void quant_row_int8(const float* __restrict__ x, uint32_t D, int lane
         amax = fmaxf(amax, fabsf(vals[k]));
     }
     amax = wave_max_all(amax);
-    const float scale = amax > 0.f ? amax / 127.0f : 1.0f;
+    const float scale = int8_row_scale(amax);
     const float inv = 1.0f / scale;
 #pragma unroll
     for (int k = 0; k < PER; ++k) {
         const uint32_t d = lane + k * kWave;
-        if (d < D) {
-            const float r = roundf(vals[k] * inv);
-            q[d] = static_cast<int8_t>(fminf(fmaxf(r, -127.0f), 127.0f));
-        }
+        if (d < D) q[d] = quant_i8(vals[k], inv, -127.0f);
     }
     if (lane == 0) *scale_out = scale;
 }
@@ -98,12 +95,7 @@ __device__ void quant_row_fp8(const float* __restrict__ x, uint32_t D, int lane,
         amax = fmaxf(amax, fabsf(vals[k]));
     }
     amax = wave_max_all(amax);
-    float scale = 1.0f;
-    if (amax > 0.f) {
-        int e2;
-        const float fr = frexpf(amax / 64.0f, &e2);
-        scale = ldexpf(1.0f, fr == 0.5f ? e2 - 1 : e2);
-    }
+    const float scale = fp8_row_scale(amax);
     const float inv = 1.0f / scale;
 #pragma unroll
     for (int k = 0; k < PER; ++k) {
@@ -127,8 +119,7 @@ __device__ void quant_row_q8_0(const float* __restrict__ x, uint32_t D, int lane
         const float sc = amax / 127.0f;
         const float id = sc != 0.f ? 1.0f / sc : 0.f;
         if (in) {
-            const float r = roundf(val * id);
-            q[d] = static_cast<int8_t>(fminf(fmaxf(r, -128.0f), 127.0f));
+            q[d] = quant_i8(val, id, -128.0f);
             if ((d & 31) == 0) d_out[d / 32] = __float2half_rn(sc);
         }
     }

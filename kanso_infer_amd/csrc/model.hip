@@ -109,11 +109,6 @@ __global__ void reset_blocks_kernel(float* k, float* v, const uint32_t* blocks, 
 
 uint32_t grid_for(uint64_t n) { return static_cast<uint32_t>(std::min<uint64_t>((n + 255) / 256, 8192)); }
 
-__global__ void iota_i64_kernel(int64_t* out, uint64_t n) {
-    for (uint64_t i = blockIdx.x * 256ull + threadIdx.x; i < n; i += static_cast<uint64_t>(gridDim.x) * 256)
-        out[i] = static_cast<int64_t>(i);
-}
-
 // Allocates a device buffer owned by the model. A buffer that *p already holds is
 // replaced: freed and dropped from the model's list (callers that grow a buffer
 // synchronise the device first, so no queued kernel still reads it).
@@ -261,15 +256,6 @@ int ensure_step_buffers(kanso_model* m, uint32_t T, uint32_t S, uint32_t tables,
         m->cap_seqs = sq;
         // per-pair argmax keys of the lm_head for every sampled row
         if ((rc = ensure_keys(m->ctx, static_cast<size_t>(sq) * ((c.vocab + 31) / 32) * 8))) return rc;
-        if (m->kv_dtype != KANSO_KV_F32) {
-            const size_t kv_row = static_cast<size_t>(c.num_kv_heads) * c.head_dim * 4;
-            if ((rc = dev_alloc(m, &m->k_stage, t * kv_row))) return rc;
-            if ((rc = dev_alloc(m, &m->v_stage, t * kv_row))) return rc;
-            if ((rc = dev_alloc(m, &m->iota, t * 8ull))) return rc;
-            hipLaunchKernelGGL(iota_i64_kernel, dim3(grid_for(t)), dim3(256), 0, 0, m->iota, static_cast<uint64_t>(t));
-            KANSO_LAUNCH_CHECK();
-            KANSO_HIP_TRY(hipDeviceSynchronize());
-        }
     }
     if (tables > m->cap_tables) {
         KANSO_HIP_TRY(hipDeviceSynchronize());
@@ -451,12 +437,8 @@ int model_forward(kanso_model* m, const HostStep& step, float* logits, uint32_t*
     }
     const uint32_t qd = c.num_heads * 64;
     const bool quant = m->kv_dtype != KANSO_KV_F32;
-    // 1-byte pools: the QKV epilogue writes K / V rows to the staging rows 0..T-1, and
-    // the fused append + quantize (kanso_kv_append, write_kv_slots of the quantized
-    // storage) takes them into the pool slots.
-    kanso_qkv_params qs = qp;
-    qs.num_blocks = m->cap_tokens;
-    qs.block_size = 1;
+    // 1-byte pools: the QKV epilogue quantizes each K / V row into its pool slot
+    // (write_kv_slots of the quantized storage) with no f32 staging rows.
     for (uint32_t l = 0; l < c.num_layers; ++l) {
         const auto& L = m->layers[l];
         const uint32_t bits = L.q4k_parts;
@@ -471,14 +453,10 @@ int model_forward(kanso_model* m, const HostStep& step, float* logits, uint32_t*
                                          m->slots, m->cos_t, m->sin_t, m->q, reinterpret_cast<float*>(kp),
                                          reinterpret_cast<float*>(vp), s, true, qkv4)))
                 return rc;
-        } else {
-            if ((rc = op_qkv_rope_append(m->ctx, &qs, qkv4 ? L.qkv_q4k : L.qkv, m->hidden, L.attn_norm, m->positions,
-                                         m->iota, m->cos_t, m->sin_t, m->q, m->k_stage, m->v_stage, s, true, qkv4)))
-                return rc;
-            if ((rc = kanso_kv_append(m->ctx, m->kv_dtype, m->k_stage, m->v_stage, m->slots, T, m->num_blocks,
-                                      m->block_size, c.num_kv_heads, c.head_dim, kp, vp, ks, vs,
-                                      reinterpret_cast<kanso_stream_t>(s))))
-                return rc;
+        } else if ((rc = op_qkv_rope_quant(m->ctx, &qp, qkv4 ? L.qkv_q4k : L.qkv, m->hidden, L.attn_norm,
+                                           m->positions, m->slots, m->cos_t, m->sin_t, m->q, m->kv_dtype, kp, vp, ks,
+                                           vs, s, true, qkv4))) {
+            return rc;
         }
         if ((rc = op_ragged_attention(m->ctx, &ap, m->q, kp, vp, ks, vs, m->tables, m->cu, m->ctx_lens, m->attn, s,
                                       true)))

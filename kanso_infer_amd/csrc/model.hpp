@@ -15,6 +15,10 @@ int op_qkv_rope_append(kanso_ctx* ctx, const kanso_qkv_params* p, const void* w,
                        const float* norm_w, const int32_t* positions, const int64_t* slots, const float* cos_t,
                        const float* sin_t, float* q, float* k_pool, float* v_pool, hipStream_t s, bool tiled,
                        bool q4k);
+int op_qkv_rope_quant(kanso_ctx* ctx, const kanso_qkv_params* p, const void* w, const float* x, const float* norm_w,
+                      const int32_t* positions, const int64_t* slots, const float* cos_t, const float* sin_t,
+                      float* q, uint32_t kv_dtype, void* k_pool, void* v_pool, void* k_scales, void* v_scales,
+                      hipStream_t s, bool tiled, bool q4k);
 int op_gemm_residual(const void* w, const float* x, float* y, uint32_t out, uint32_t in, uint32_t T,
                      hipStream_t s, bool tiled, bool q4k, float scale);
 int op_gate_up_swiglu(const void* w, const float* x, const float* norm_w, float eps, uint32_t T,
@@ -77,11 +81,6 @@ struct kanso_model {
     size_t layer_pool_elems = 0;   // elements of one layer's K (or V) pool
     size_t layer_pool_bytes = 0;
     size_t layer_scale_bytes = 0;
-    // 1-byte kinds: this step's K / V rows before quantization, [tokens][kv_heads][64]
-    // f32, and the identity slot map the QKV epilogue writes them through.
-    float* k_stage = nullptr;
-    float* v_stage = nullptr;
-    int64_t* iota = nullptr;
     // Step buffers sized for max_tokens rows / max_seqs sequences (grow-only).
     uint32_t cap_tokens = 0, cap_seqs = 0, cap_tables = 0, cap_arena = 0;
     float *hidden = nullptr, *q = nullptr, *attn = nullptr, *act = nullptr;

@@ -32,6 +32,7 @@
 #pragma once
 
 #include <atomic>
+#include <type_traits>
 
 #include "common.hpp"
 
@@ -259,11 +260,22 @@ struct XIn {
 // last block, its scale forced to 0; a unit past `units` by the workgroup's first
 // unit, never stored): a branch around them would make the compiler wait for each
 // block's loads at the join, serialising the round.
+// An epilogue with kPairedUnits = true takes the outputs of units u0 and u0 + 1
+// (even u0, NU = 2) in one wave: apply_pair(u0, lane, m0, T, v[4], pre) with v[n]
+// the rows of weight group g[n] (unit u0: g[0], g[1]; unit u0 + 1: g[2], g[3]), for
+// epilogues that need a whole row of outputs at once (a quantized KV row's scale).
+template <class E, class = void>
+struct PairedUnits : std::false_type {};
+template <class E>
+struct PairedUnits<E, std::void_t<decltype(E::kPairedUnits)>> : std::bool_constant<E::kPairedUnits> {};
+
 template <int KS, int U, int MT, int NU, bool NORM, class WL, class Epi>
 __global__ __launch_bounds__(KS * kWave) void q8_gemm_kernel(WL wl, XIn xa, Epi epi, uint32_t units) {
     constexpr int EG = Epi::kGroups;
     constexpr int NG = NU * EG;
-    constexpr int NC = MT * NU;  // (token tile, unit) combinations of the epilogue
+    constexpr bool PU = PairedUnits<Epi>::value;
+    static_assert(!PU || (NU == 2 && EG == 2), "paired units: two units of two groups per workgroup");
+    constexpr int NC = PU ? MT : MT * NU;  // (token tile, unit) combinations of the epilogue
     static_assert(NG * MT <= 8 && NC <= KS, "partial sums must fit 64 KB of LDS");
     __shared__ floatx4 s_part[KS][NG][MT][kWave];
     __shared__ float s_ss[KS][MT][16];
@@ -400,7 +412,29 @@ __global__ __launch_bounds__(KS * kWave) void q8_gemm_kernel(WL wl, XIn xa, Epi 
         }
     }
     __syncthreads();
-    if (cstore) {
+    if constexpr (PU) {
+        if (cstore) {
+            floatx4 v[4];
+#pragma unroll
+            for (int n = 0; n < 4; ++n) {
+                v[n] = s_part[0][n][ci][lane];
+#pragma unroll
+                for (int w = 1; w < KS; ++w) v[n] += s_part[w][n][ci][lane];
+            }
+            if (norm) {
+#pragma unroll
+                for (int r = 0; r < 4; ++r) {
+                    float s = s_ss[0][ci][4 * kq + r];
+#pragma unroll
+                    for (int w = 1; w < KS; ++w) s += s_ss[w][ci][4 * kq + r];
+                    const float rms = sqrtf(s / static_cast<float>(xa.in) + xa.eps);
+#pragma unroll
+                    for (int n = 0; n < 4; ++n) v[n][r] /= rms;
+                }
+            }
+            epi.apply_pair(cunit, lane, t0 + 16 * ci + 4 * kq, xa.T, v, pre);
+        }
+    } else if (cstore) {
         const int ga = EG * cj, gb = EG * cj + EG - 1;
         floatx4 v0 = s_part[0][ga][ci][lane], v1 = {0.f, 0.f, 0.f, 0.f};
         if constexpr (EG == 2) v1 = s_part[0][gb][ci][lane];
@@ -503,6 +537,18 @@ struct EpiSwiGLU {
     }
 };
 
+// Rotate-half RoPE of one dim pair (d, d + 32): [a cos - b sin, a sin + b cos]
+// (rope_apply, src/model.rs:720-737), each product rounded before the sum as in the
+// reference (no fused multiply-add: otherwise the compiler's choice of which product
+// to fuse may differ between kernels that inline this).
+__device__ __forceinline__ void rope_rotate(float& a, float& b, float c, float s) {
+#pragma clang fp contract(off)
+    const float ra = a * c - b * s;
+    const float rb = a * s + b * c;
+    a = ra;
+    b = rb;
+}
+
 // Fused Q/K/V projection epilogue for head_dim 64: weights are the row
 // concatenation [Wq; Wk; Wv] (heads of 64 rows = 4 groups). Pair p = (head p/2,
 // half p%2) takes groups 4h + half and 4h + half + 2, i.e. dims d and d + 32 of
@@ -562,13 +608,7 @@ struct EpiQkvRope {
             const uint32_t m = m0 + r;
             if (m >= T) break;
             float a = x1[r], b = x2[r];
-            if (!is_v) {
-                const float c = pr.c[r], s = pr.s[r];
-                const float ra = a * c - b * s;
-                const float rb = a * s + b * c;
-                a = ra;
-                b = rb;
-            }
+            if (!is_v) rope_rotate(a, b, pr.c[r], pr.s[r]);
             if (is_q) {
                 float* qr = q + (static_cast<size_t>(m) * num_heads + head) * 64;
                 qr[d] = a;
@@ -584,6 +624,131 @@ struct EpiQkvRope {
             float* dst = (is_v ? v_pool : k_pool) + (static_cast<size_t>(slot) * num_kv_heads + kvh) * 64;
             dst[d] = a;
             dst[d + 32] = b;
+        }
+    }
+};
+
+// EpiQkvRope for a 1-byte pool (INT8, FP8 or Q8_0 rows): the two halves of a head
+// (units 2h, 2h + 1) meet in one wave, so each K / V row of 64 values is rotated,
+// quantized and stored straight into its pool slot with its scale, in the bytes the
+// append kernel writes (quantize_head_slice, quantized_storage.rs:452-486;
+// BlockQ8_0::from_f32_slice, src/quant/q8_0.rs:13-32): no f32 staging rows and no
+// second kernel. Lane l holds dims l % 16 + {0, 32} (v[0], v[1]) and 16 + l % 16 +
+// {0, 32} (v[2], v[3]) of tokens m0 .. m0 + 3; a row's maximum is one 16-lane
+// reduction. Q rows go to q[m][h][64] as f32.
+template <int KVT>
+struct EpiQkvRopeQ {
+    static constexpr int kGroups = 2;
+    static constexpr bool kPairedUnits = true;
+    float* q;
+    uint8_t* k_pool;
+    uint8_t* v_pool;
+    void* k_scales;
+    void* v_scales;
+    const int32_t* positions;
+    const int64_t* slots;
+    const float* cos_t;  // [max_pos][32]
+    const float* sin_t;
+    uint32_t* status;
+    uint32_t num_heads, num_kv_heads, max_pos;
+    int64_t num_slots;
+    __device__ __forceinline__ void groups(uint32_t p, uint32_t& g0, uint32_t& g1) const {
+        g0 = 4 * (p / 2) + (p % 2);
+        g1 = g0 + 2;
+    }
+    struct Pre {
+        float c[2][4], s[2][4];  // RoPE cos / sin of dims l % 16 and 16 + l % 16
+        int64_t slot[4];
+    };
+    __device__ __forceinline__ Pre pre(uint32_t p, int lane, uint32_t m0, uint32_t T) const {
+        Pre r{};
+        const uint32_t head = p / 2;
+        const uint32_t d = lane & 15;
+        const bool is_q = head < num_heads, is_v = head >= num_heads + num_kv_heads;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const uint32_t m = m0 + i;
+            if (m >= T) break;
+            if (!is_v) {
+                uint32_t pos = static_cast<uint32_t>(positions[m]);
+                if (pos >= max_pos) {
+                    raise_status(status, KANSO_DEV_POSITION_OOB);
+                    pos = max_pos - 1;
+                }
+                r.c[0][i] = cos_t[static_cast<size_t>(pos) * 32 + d];
+                r.s[0][i] = sin_t[static_cast<size_t>(pos) * 32 + d];
+                r.c[1][i] = cos_t[static_cast<size_t>(pos) * 32 + 16 + d];
+                r.s[1][i] = sin_t[static_cast<size_t>(pos) * 32 + 16 + d];
+            }
+            if (!is_q) r.slot[i] = slots[m];
+        }
+        return r;
+    }
+    __device__ __forceinline__ void apply_pair(uint32_t p, int lane, uint32_t m0, uint32_t T, const floatx4 (&v)[4],
+                                               const Pre& pr) const {
+        const uint32_t head = p / 2;
+        const uint32_t d = lane & 15;
+        const bool is_q = head < num_heads, is_v = head >= num_heads + num_kv_heads;
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            // every lane runs every token (the 16-lane reductions below need the
+            // whole group); tokens past T store nothing
+            const uint32_t m = m0 + r;
+            const bool live = m < T;
+            float x[4] = {v[0][r], v[1][r], v[2][r], v[3][r]};  // dims d, d + 32, 16 + d, 48 + d
+            if (!is_v) {
+                rope_rotate(x[0], x[1], pr.c[0][r], pr.s[0][r]);
+                rope_rotate(x[2], x[3], pr.c[1][r], pr.s[1][r]);
+            }
+            if (is_q) {
+                if (live) {
+                    float* qr = q + (static_cast<size_t>(m) * num_heads + head) * 64;
+                    qr[d] = x[0];
+                    qr[d + 32] = x[1];
+                    qr[d + 16] = x[2];
+                    qr[d + 48] = x[3];
+                }
+                continue;
+            }
+            const int64_t slot = pr.slot[r];
+            const bool ok = live && slot >= 0 && slot < num_slots;
+            if (live && !ok) raise_status(status, KANSO_DEV_SLOT_OOB);
+            const uint32_t kvh = is_v ? head - num_heads - num_kv_heads : head - num_heads;
+            const size_t row = static_cast<size_t>(ok ? slot : 0) * num_kv_heads + kvh;
+            uint8_t* dst = (is_v ? v_pool : k_pool) + row * 64;
+            int8_t qv[4];
+            if constexpr (KVT == KANSO_KV_Q8_0) {
+                // blocks of 32: dims 0..31 are x[0], x[2]; dims 32..63 x[1], x[3]
+                const float a0 = group_max<16>(fmaxf(fabsf(x[0]), fabsf(x[2])));
+                const float a1 = group_max<16>(fmaxf(fabsf(x[1]), fabsf(x[3])));
+                const float d0 = a0 / 127.0f, d1 = a1 / 127.0f;
+                const float i0 = d0 != 0.f ? 1.0f / d0 : 0.f, i1 = d1 != 0.f ? 1.0f / d1 : 0.f;
+                qv[0] = quant_i8(x[0], i0, -128.0f);
+                qv[2] = quant_i8(x[2], i0, -128.0f);
+                qv[1] = quant_i8(x[1], i1, -128.0f);
+                qv[3] = quant_i8(x[3], i1, -128.0f);
+                if (ok && d == 0) {
+                    __half* sc = static_cast<__half*>(is_v ? v_scales : k_scales) + row * 2;
+                    sc[0] = __float2half_rn(d0);
+                    sc[1] = __float2half_rn(d1);
+                }
+            } else {
+                const float amax =
+                    group_max<16>(fmaxf(fmaxf(fabsf(x[0]), fabsf(x[1])), fmaxf(fabsf(x[2]), fabsf(x[3]))));
+                const float scale = KVT == KANSO_KV_FP8 ? fp8_row_scale(amax) : int8_row_scale(amax);
+                const float inv = 1.0f / scale;
+#pragma unroll
+                for (int j = 0; j < 4; ++j)
+                    qv[j] = KVT == KANSO_KV_FP8 ? static_cast<int8_t>(f32_to_e4m3(x[j] * inv))
+                                                : quant_i8(x[j], inv, -127.0f);
+                if (ok && d == 0) static_cast<float*>(is_v ? v_scales : k_scales)[row] = scale;
+            }
+            if (ok) {
+                dst[d] = static_cast<uint8_t>(qv[0]);
+                dst[d + 32] = static_cast<uint8_t>(qv[1]);
+                dst[d + 16] = static_cast<uint8_t>(qv[2]);
+                dst[d + 48] = static_cast<uint8_t>(qv[3]);
+            }
         }
     }
 };
@@ -748,6 +913,25 @@ inline void launch_norm(const WL& wl, const XIn& xa, const Epi& epi, uint32_t pa
         launch_mt1<NORM>(wl, xa, SingleGroup<Epi>::make(epi), (epi.rows + 15) / 16, nb, s);
     else
         launch_mt1<NORM>(wl, xa, epi, pairs, nb, s);
+}
+
+// Paired-unit epilogues (a whole 64-row head per wave): two units per workgroup,
+// 32-token tiles under the same rule as the other paired epilogues.
+template <class WL, class Epi>
+inline int launch_q8_gemm_paired(const WL& wl, const XIn& xa, const Epi& epi, uint32_t units, hipStream_t s) {
+    if (xa.T == 0 || units == 0) return KANSO_OK;
+    if (!xa.norm_w || units % 2 != 0) {
+        set_error("paired-unit product: needs the RMSNorm prologue and an even unit count");
+        return KANSO_E_INVALID_ARG;
+    }
+    const uint32_t nb = xa.in / 32;
+    const bool wide = xa.T > 16 && static_cast<uint64_t>(units / 2) * ((xa.T + 15) / 16) >= 4ull * device_cus();
+    if (xa.T > 256 || wide)
+        launch_mt<2, 2, true>(wl, xa, epi, units, nb, s);
+    else
+        launch_mt<1, 2, true>(wl, xa, epi, units, nb, s);
+    KANSO_LAUNCH_CHECK();
+    return KANSO_OK;
 }
 
 template <class WL, class Epi>

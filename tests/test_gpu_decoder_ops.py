@@ -144,6 +144,53 @@ def _qkv_case(T, H=15, HKV=5, hidden=960, seed=0, num_blocks=64, bs=16):
                 positions=positions, slots=slots, num_blocks=num_blocks, bs=bs)
 
 
+@pytest.mark.parametrize("kv", [K.KANSO_KV_INT8, K.KANSO_KV_FP8, K.KANSO_KV_Q8_0])
+@pytest.mark.parametrize("T", [1, 20, 70, 300])
+def test_qkv_rope_append_quant_matches_two_kernels(ctx, T, kv):
+    """The quantizing QKV epilogue writes the bytes of the two-kernel path (F32 rows
+    from qkv_rope_append, then kv_append's fused quantize), bit for bit: Q, the
+    written pool rows and their scales, and nothing else of the pool."""
+    c = _qkv_case(T, seed=100 + T)
+    H, HKV, hidden, D = c["H"], c["HKV"], c["hidden"], 64
+    rows = (H + 2 * HKV) * D
+    packed = torch.zeros(K.q8_0_packed_bytes(rows, hidden), dtype=torch.uint8, device="cuda:0")
+    K.q8_0_pack(ctx, dev(c["wq"]), H * D, hidden, packed, 1, 0)
+    K.q8_0_pack(ctx, dev(c["wk"]), HKV * D, hidden, packed, 1, 4 * H)
+    K.q8_0_pack(ctx, dev(c["wv"]), HKV * D, hidden, packed, 1, 4 * (H + HKV))
+    cos_t, sin_t = oracle.rope_table(2048, D)
+    nb, bs = c["num_blocks"], c["bs"]
+    nslots = nb * bs
+    x, nw, pos, sl = dev(c["x"]), dev(c["norm_w"]), dev(c["positions"]), dev(c["slots"])
+    # two kernels: F32 staging rows 0..T-1, then the fused append + quantize
+    ks_ = torch.zeros(T * HKV * D, device="cuda:0")
+    vs_ = torch.zeros_like(ks_)
+    q2 = torch.empty(T * H * D, device="cuda:0")
+    K.qkv_rope_append(ctx, packed, x, nw, pos, torch.arange(T, dtype=torch.int64, device="cuda:0"),
+                      dev(cos_t), dev(sin_t), q2, ks_, vs_, hidden=hidden, num_heads=H,
+                      num_kv_heads=HKV, num_blocks=T, block_size=1)
+
+    def pools():
+        kp = torch.full((nslots * HKV * D,), 7, dtype=torch.int8, device="cuda:0")
+        if kv == K.KANSO_KV_Q8_0:
+            sc = torch.full((nslots * HKV * D // 32,), 3.0, dtype=torch.float16, device="cuda:0")
+        else:
+            sc = torch.full((nslots * HKV,), 3.0, dtype=torch.float32, device="cuda:0")
+        return kp, kp.clone(), sc, sc.clone()
+
+    kp2, vp2, kS2, vS2 = pools()
+    K.kv_append(ctx, kv, ks_, vs_, sl, nb, bs, HKV, D, kp2, vp2, kS2, vS2)
+    kp1, vp1, kS1, vS1 = pools()
+    q1 = torch.empty(T * H * D, device="cuda:0")
+    K.qkv_rope_append_quant(ctx, packed, x, nw, pos, sl, dev(cos_t), dev(sin_t), q1, kv, kp1, vp1,
+                            kS1, vS1, hidden=hidden, num_heads=H, num_kv_heads=HKV,
+                            num_blocks=nb, block_size=bs)
+    ctx.check_device_status()
+    np.testing.assert_array_equal(host(q1), host(q2))
+    for a, b in ((kp1, kp2), (vp1, vp2), (kS1, kS2), (vS1, vS2)):
+        np.testing.assert_array_equal(host(a), host(b))
+    assert (host(kp1).reshape(nslots, -1)[c["slots"]] != 7).any()
+
+
 @pytest.mark.parametrize("T", [1, 20, 70, 300])
 def test_qkv_rope_append(ctx, T):
     c = _qkv_case(T, seed=T)
