@@ -38,6 +38,7 @@ PMC_COPY_BYTES = 512 << 20
 METRIC = "ragged paged-attn tokens/s + % HBM peak; batched decode tok/s at 1 MI355X"
 POOL_LAYOUT = 0  # KANSO_POOL_TOKEN_MAJOR unless --pool-layout head
 PARTITION = 0  # 0: kanso_ragged_partition_size per batch; -1: the library's choice; > 0: fixed
+CHUNK_PARTITION = 0  # > 0: a fixed chunk partition (else from the lengths, or the library's)
 
 
 def log(msg: str) -> None:
@@ -110,7 +111,7 @@ class AttnBench:
             d["P"] = self.partition(b)
             # the chunk partition from the same lengths (non-zero only for batches
             # without decode rows), unless a fixed or library partition is asked for
-            d["CP"] = 0 if PARTITION else self.K.ragged_chunk_partition_size(
+            d["CP"] = CHUNK_PARTITION if CHUNK_PARTITION else 0 if PARTITION else self.K.ragged_chunk_partition_size(
                 self.ctx, q_lens=b.q_lens, context_lens=b.context_lens, num_heads=b.num_heads,
                 num_kv_heads=b.num_kv_heads, head_dim=b.head_dim, block_size=b.block_size,
                 max_blocks=b.max_blocks, kv_dtype=self.kv_dtype, num_blocks=self.num_blocks)
@@ -681,14 +682,18 @@ def main():
     ap.add_argument("--partition", type=int, default=0,
                     help="split-K partition of the attention benchmarks: 0 = from the batch's "
                          "lengths (kanso_ragged_partition_size), -1 = the library's own choice")
+    ap.add_argument("--chunk-partition", type=int, default=0,
+                    help="fixed partition of the MFMA chunk rows (a multiple of 32; 0 = the "
+                         "library's rule)")
     ap.add_argument("--gemm-probe", action="store_true",
                     help="launches of the Q8_0 products only (for a rocprofv3 counter pass)")
     ap.add_argument("--decode-only", action="store_true",
                     help="also time the headline batches' decode rows alone")
     args = ap.parse_args()
-    global POOL_LAYOUT, PARTITION
+    global POOL_LAYOUT, PARTITION, CHUNK_PARTITION
     POOL_LAYOUT = 1 if args.pool_layout == "head" else 0
     PARTITION = args.partition
+    CHUNK_PARTITION = args.chunk_partition
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print("bench.py measures one GPU: this build has no multi-GPU component (the path "
               "would shard by sequences, one engine and KV pool per GPU); run with --gpus 1",
