@@ -319,7 +319,7 @@ typedef struct {
     uint32_t head_dim;   /* 64 */
     uint32_t max_pos;    /* rows of the cos / sin tables                          */
     float eps;           /* RMSNorm epsilon                                        */
-    uint32_t num_blocks; /* F32 pool geometry, for the slot bounds check           */
+    uint32_t num_blocks; /* pool geometry, for the slot bounds check               */
     uint32_t block_size;
 } kanso_qkv_params;
 

@@ -90,6 +90,38 @@ def test_batch_invariance(ctx, rows, cols):
         outs.append(host(y).reshape(T, rows)[0])
     for T, o in zip(sizes[1:], outs[1:]):
         assert np.array_equal(o, outs[0]), T
+    # every token of the largest batch (its 64-token tiles, the partial last one
+    # included) against the same tokens 16 at a time
+    y = torch.empty(max(sizes) * rows, dtype=torch.float32, device="cuda:0")
+    K.gemm_q8_0(ctx, packed, dev(x), y, rows, cols)
+    full = host(y).reshape(-1, rows)
+    for t0 in range(0, max(sizes), 16):
+        n = min(16, max(sizes) - t0)
+        yc = torch.empty(n * rows, dtype=torch.float32, device="cuda:0")
+        K.gemm_q8_0(ctx, packed, dev(x[t0:t0 + n]), yc, rows, cols)
+        assert np.array_equal(full[t0:t0 + n], host(yc).reshape(n, rows)), t0
+
+
+@pytest.mark.parametrize("T", [257, 300, 512])
+def test_batch_invariance_rmsnorm(ctx, T):
+    """The RMSNorm prologue's sum of squares too: gate/up + SwiGLU of T tokens at once
+    equals the same tokens 16 at a time, bit for bit."""
+    hidden, inter = 960, 2560
+    rng = np.random.default_rng(T)
+    wg, wu = q8_weights(inter, hidden, 3), q8_weights(inter, hidden, 4)
+    packed = torch.zeros(K.q8_0_packed_bytes(2 * inter, hidden), dtype=torch.uint8, device="cuda:0")
+    K.q8_0_pack(ctx, dev(wg), inter, hidden, packed, 2, 0)
+    K.q8_0_pack(ctx, dev(wu), inter, hidden, packed, 2, 1)
+    x = rng.standard_normal((T, hidden)).astype(np.float32)
+    nw = (1.0 + 0.1 * rng.standard_normal(hidden)).astype(np.float32)
+    h = torch.empty(T * inter, device="cuda:0")
+    K.gate_up_swiglu(ctx, packed, dev(x), dev(nw), h, hidden=hidden, intermediate=inter)
+    full = host(h).reshape(T, inter)
+    for t0 in range(0, T, 16):
+        n = min(16, T - t0)
+        hc = torch.empty(n * inter, device="cuda:0")
+        K.gate_up_swiglu(ctx, packed, dev(x[t0:t0 + n]), dev(nw), hc, hidden=hidden, intermediate=inter)
+        assert np.array_equal(full[t0:t0 + n], host(hc).reshape(n, inter)), t0
 
 
 @pytest.mark.parametrize("T", [37, 300])

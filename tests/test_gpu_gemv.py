@@ -77,6 +77,23 @@ def test_q4_k_ragged_row_counts(ctx, rows, cols, batch):
     assert_close(got, want, what=f"q4_k {rows}x{cols} b{batch}")
 
 
+@pytest.mark.parametrize("kind,rows,cols", [("q4_k", 1008, 2560), ("q8_0", 1008, 960)])
+def test_large_batch_equals_small_batches(ctx, kind, rows, cols):
+    """300 tokens at once (64-token output tiles) give every token exactly what the
+    same tokens give 16 at a time (the decode-sized kernel)."""
+    w, wd = weights(kind, rows, cols)
+    x = np.random.default_rng(9).standard_normal((300, cols)).astype(np.float32)
+    fn = K.gemv_q8_0 if kind == "q8_0" else K.gemv_q4_k
+    y = torch.empty(300 * rows, dtype=torch.float32, device="cuda:0")
+    fn(ctx, wd, dev(x), y, rows, cols)
+    full = host(y).reshape(300, rows)
+    for t0 in range(0, 300, 16):
+        n = min(16, 300 - t0)
+        yc = torch.empty(n * rows, dtype=torch.float32, device="cuda:0")
+        fn(ctx, wd, dev(x[t0:t0 + n]), yc, rows, cols)
+        assert np.array_equal(full[t0:t0 + n], host(yc).reshape(n, rows)), t0
+
+
 def test_reference_closed_form(ctx):
     # probes.rs:64-71 with an f16 scale: d = 0.01 (as f16), qs = 1, x = 1
     rows, cols = 64, 1024
