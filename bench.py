@@ -652,6 +652,47 @@ def gemm_probe(ctx, torch, K, oracle_mod, launches=10):
         torch.cuda.synchronize()
 
 
+def gemv_pass(ctx, torch, K, oracle_mod, launches=12):
+    """Launches only, for rocprofv3 (kernel trace, FETCH_SIZE, WRITE_SIZE): the
+    config-4 GEMVs (q8_0 GGUF blocks, q8_0 packed, q4_k; the SmolLM2 shapes; batch 1,
+    8 and 32), each `launches` times over rotating weight copies (> 1 GB, so every
+    launch reads cold weights), after a PMC_COPY_BYTES calibration copy. Prints the
+    launch order, one line per (kind, shape, batch), for matching the dispatches."""
+    dev = torch.device("cuda:0")
+    a = torch.empty(PMC_COPY_BYTES // 4, dtype=torch.float32, device=dev).normal_()
+    b = torch.empty_like(a)
+    torch.cuda.synchronize()
+    b.copy_(a)
+    torch.cuda.synchronize()
+    del a, b
+    shapes = [("q", 960, 960), ("kv", 320, 960), ("gate_up", 2560, 960), ("down", 960, 2560)]
+    for kind in ("q8_0", "q8_0_packed", "q4_k"):
+        for name, rows, cols in shapes:
+            cols_eff = cols if kind != "q4_k" or cols % 256 == 0 else 1024
+            rng = np.random.default_rng(rows + cols)
+            wf = (rng.standard_normal((rows, cols_eff)) * 0.02).astype(np.float32)
+            w = (oracle_mod.quantize_row_q8_0(wf) if kind != "q4_k"
+                 else oracle_mod.quantize_row_q4_k(wf))
+            one = torch.from_numpy(w).to(dev)
+            if kind == "q8_0_packed":
+                one = K.pack_q8_0_matrix(ctx, one, rows, cols_eff)
+            wbytes = one.numel()
+            copies = int(1.1e9 // wbytes) + 1
+            arena = one.repeat(copies)
+            fn = {"q8_0": K.gemv_q8_0, "q8_0_packed": K.gemm_q8_0, "q4_k": K.gemv_q4_k}[kind]
+            for batch in (1, 8, 32):
+                x = torch.randn(batch * cols_eff, device=dev)
+                y = torch.empty(batch * rows, device=dev)
+                torch.cuda.synchronize()
+                print(json.dumps(dict(kind=kind, shape=name, out=rows, inp=cols_eff, batch=batch,
+                                      weight_bytes=wbytes, launches=launches)), flush=True)
+                for i in range(launches):
+                    fn(ctx, arena[i * wbytes:(i + 1) * wbytes], x, y, rows, cols_eff)
+                torch.cuda.synchronize()
+            del arena
+            torch.cuda.empty_cache()
+
+
 def host_bandwidth(threads):
     """STREAM triad of the host (the oracle library, OpenMP), 1 thread and `threads`."""
     sys.path.insert(0, str(ROOT / "oracle"))
@@ -685,6 +726,9 @@ def main():
     ap.add_argument("--chunk-partition", type=int, default=0,
                     help="fixed partition of the MFMA chunk rows (a multiple of 32; 0 = the "
                          "library's rule)")
+    ap.add_argument("--gemv-pass", action="store_true",
+                    help="config-4 GEMV launches only (cold weights), for rocprofv3 kernel-trace "
+                         "and FETCH_SIZE / WRITE_SIZE passes")
     ap.add_argument("--gemm-probe", action="store_true",
                     help="launches of the Q8_0 products only (for a rocprofv3 counter pass)")
     ap.add_argument("--decode-only", action="store_true",
@@ -705,6 +749,12 @@ def main():
     from kanso_infer_amd import workloads
 
     ctx = K.Context(0)
+    if args.gemv_pass:
+        sys.path.insert(0, str(ROOT / "oracle"))
+        import oracle as oracle_mod
+        gemv_pass(ctx, torch, K, oracle_mod)
+        ctx.close()
+        return
     if args.gemm_probe:
         sys.path.insert(0, str(ROOT / "oracle"))
         import oracle as oracle_mod
