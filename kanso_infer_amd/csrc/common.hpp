@@ -93,7 +93,22 @@ inline size_t align_up(size_t x, size_t a) { return (x + a - 1) / a * a; }
 
 constexpr int kWave = 64;
 
-__device__ __forceinline__ float wave_xor(float v, int mask) { return __shfl_xor(v, mask, kWave); }
+// v of lane (this lane ^ mask). Masks 16 and 32 use gfx950's lane swaps
+// (v_permlane16_swap / v_permlane32_swap: a VALU op that hands each lane the values
+// of both lanes of its pair, no LDS round trip); other masks a lane permute
+// through LDS (ds_bpermute). Same values either way.
+__device__ __forceinline__ float wave_xor(float v, int mask) {
+    const uint32_t u = __float_as_uint(v);
+    if (mask == 32) {
+        const auto r = __builtin_amdgcn_permlane32_swap(u, u, false, false);  // {lane & ~32, lane | 32}
+        return __uint_as_float((__lane_id() & 32) ? r[0] : r[1]);
+    }
+    if (mask == 16) {
+        const auto r = __builtin_amdgcn_permlane16_swap(u, u, false, false);  // {lane & ~16, lane | 16}
+        return __uint_as_float((__lane_id() & 16) ? r[0] : r[1]);
+    }
+    return __shfl_xor(v, mask, kWave);
+}
 
 // DPP lane permutations inside a 16-lane row (no LDS traffic, no address registers).
 template <int CTRL>
