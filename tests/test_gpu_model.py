@@ -345,3 +345,32 @@ def test_model_from_gguf_q4_k_and_granite(ctx, tmp_path, variant):
         assert_close(host(logits).reshape(S, SMALL["vocab"]), om.logits(plan),
                      what=f"{variant} logits step {step}")
     gm.close()
+
+
+def test_step_buffers_grow_without_leaking(ctx):
+    """Step buffers grow with the batch (1.5x headroom) and the buffer each growth
+    replaces is freed: a model grown to 1024 tokens in 64 steps of 16 holds about
+    what a model sent 1024 tokens at once holds (the replaced buffers would add
+    about twice that again if they were kept)."""
+    cfg, bs, nblocks, T_max = SMALL, 16, 64, 1024
+    w = random_weights(cfg, seed=8)
+    rng = np.random.default_rng(3)
+    toks = rng.integers(0, cfg["vocab"], T_max).astype(np.uint32)
+    tabs = np.arange(nblocks, dtype=np.uint32)
+
+    def used_by_forwards(sizes):
+        m = gpu_model(ctx, cfg, w, nblocks, bs, max_tokens=16, max_seqs=1)
+        torch.cuda.synchronize()
+        free0 = torch.cuda.mem_get_info()[0]
+        for T in sizes:
+            plan = np.array([[0, T, 0, (T + bs - 1) // bs, 0]], np.uint32)
+            m.forward_all_rows(plan, toks[:T], tabs)
+        torch.cuda.synchronize()
+        used = free0 - torch.cuda.mem_get_info()[0]
+        m.close()
+        return used
+
+    direct = used_by_forwards([T_max])
+    stepped = used_by_forwards(range(16, T_max + 1, 16))
+    assert direct > 0
+    assert stepped <= 1.6 * direct + (8 << 20), (stepped, direct)
