@@ -720,6 +720,8 @@ def main():
                     help="only the speculative verify-step timing (one JSON line)")
     ap.add_argument("--config5-only", action="store_true",
                     help="run only the config-5 engine benchmark and print its JSON")
+    ap.add_argument("--config5-kv", choices=("f32", "int8", "fp8", "q8_0"), default="f32",
+                    help="KV pool kind of the --config5-only run")
     ap.add_argument("--partition", type=int, default=0,
                     help="split-K partition of the attention benchmarks: 0 = from the batch's "
                          "lengths (kanso_ragged_partition_size), -1 = the library's own choice")
@@ -766,8 +768,10 @@ def main():
         ctx.close()
         return
     if args.config5_only:
-        r5 = engine_bench(ctx, K, torch)
-        r5["checksum_parity"] = config5_checksum_parity(ctx, K, torch)
+        kv = {"f32": K.KANSO_KV_F32, "int8": K.KANSO_KV_INT8, "fp8": K.KANSO_KV_FP8,
+              "q8_0": K.KANSO_KV_Q8_0}[args.config5_kv]
+        r5 = engine_bench(ctx, K, torch, kv_dtype=kv)
+        r5["checksum_parity"] = config5_checksum_parity(ctx, K, torch, kv_dtype=kv)
         if not args.no_cpu:
             r5["cpu_baseline"] = config5_cpu_baseline()
         ctx.close()
