@@ -2,7 +2,7 @@
 
     python bench.py [--gpus 1] [--steps 200] [--warmup 20] [--quick]
 
-Headline: one mixed Sarathi step under a 512-token budget,
+Headline (the benchmark's configuration 2): one mixed Sarathi step under a 512-token budget,
 SmolLM2-360M attention shape (15 query / 5 KV heads, head_dim 64), 48 decode rows
 (context U[128,4096]) + 4 prefill chunks (U[32,256] rows truncated by the budget,
 prior context U[0,2048]), block size 16, block tables a random scatter over a

@@ -1458,7 +1458,7 @@ bool head_dim_supported(uint32_t d) {
 // partitions of a context assumed to be half the table capacity, the only context
 // size known on the host without reading device data) still reach one per
 // resident wave of one workgroup per CU, times four for 1-byte pools (whose items
-// move a quarter of the bytes). Calibrated on the BASELINE batches (config 2: 512
+// move a quarter of the bytes). Calibrated on the benchmark batches (config 2: 512
 // beats 256 by 5%; config 1: 64; config 3: 128). A device-side choice from the
 // actual contexts was measured too: its extra pass cost more than it saved.
 // Capped so a partition touches at most 62 table entries (one register lane each).
@@ -1726,7 +1726,7 @@ uint32_t kanso_ragged_partition_size(const kanso_ctx* ctx, const kanso_ragged_at
     // finish sooner, while items beyond the resident waves would run in a second
     // round. Chunk items (64 rows, their own partition of at least 512) hold one
     // resident workgroup each; a partition that gives them every one is not taken.
-    // Measured on the BASELINE batches: the optimum of a sweep over multiples of 32
+    // Measured on the benchmark batches: the optimum of a sweep over multiples of 32
     // is where the decode items just fit (config 2: 448; 48 decodes alone: 320;
     // config 1: 32; config 3: 160-192).
     if (!ctx || !p || !q_lens || !context_lens || p->num_seqs == 0 || p->num_kv_heads == 0 ||

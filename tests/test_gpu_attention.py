@@ -248,7 +248,7 @@ def test_chunk_partition_from_host_lengths(ctx, decodes):
 @pytest.mark.parametrize("variant", ["config1", "config2_small_pool", "config2_bench_pool",
                                      "config3_int8", "config3_q8_0", "config3_fp8"])
 def test_baseline_shapes(ctx, variant):
-    """The BASELINE configs at their real shapes (pools sized to what the tables use;
+    """The benchmark configurations at their real shapes (pools sized to what the tables use;
     config2_bench_pool: the 64k-block pool of 2.7 GB the headline is timed on)."""
     if variant == "config1":
         b, kv = workloads.config1_decode(), oracle.KV_F32
