@@ -82,7 +82,17 @@ struct AttnArgs {
     uint32_t pool_bytes, scale_bytes;  // per pool tensor, for buffer resources (< 4 GiB)
     float scale_log2;
     uint32_t out_nbk;  // 0: out is row-major [T][H][D]; else the tiled activation order, K / 32
+    // Optional decode work list (a batch of single-row sequences whose caller planned
+    // the step): n_work items of kWorkWords words, item i = (row, partition) with
+    // words 0 .. kWorkBlocks-1 the partition's physical block ids and the last four
+    // row, first key, end key, the row's key count. Null: items come from the
+    // sequence tables.
+    const uint32_t* work;
+    uint32_t n_work;
 };
+
+constexpr uint32_t kWorkWords = kanso_ragged_work_item_words;
+constexpr uint32_t kWorkBlocks = kWorkWords - 4;
 
 // Output of query row `head / H`, head `head % H`, dims d .. (up to 4 consecutive
 // floats starting at a multiple of 4: contiguous in both orders).
@@ -509,20 +519,17 @@ __device__ __forceinline__ void decode_compute(const AttnArgs& a, const PartView
     }
 }
 
+// One decode item: query row `row`, KV head kvh, keys [pv.t_begin, pv.t_end) of the
+// row's `limit` keys, the partition's block ids in pv.
 template <int D, int GMAX, int KVT, int NL, int NB, bool BUF>
-__device__ void decode_item(const AttnArgs& a, const SeqTable& st, const PoolRsrc& rs, uint32_t row, uint32_t part,
-                            uint32_t P,
-                            uint32_t seq, uint32_t kvh, int lane) {
+__device__ void decode_body(const AttnArgs& a, const PoolRsrc& rs, uint32_t row, uint32_t kvh, uint32_t limit,
+                            const PartView& pv, int lane) {
     constexpr int LPT = D / 4;
     constexpr int TT = (kWave / LPT) * NL;
     const int ts = lane / LPT, dl = lane % LPT;
     const uint32_t G = a.group;
-    const int32_t ql = st.cu[seq + 1] - st.cu[seq];
-    const uint32_t limit = row_limit(st.ctx[seq], ql,
-                                     static_cast<int32_t>(row) - st.cu[seq], a.capacity);
-    const uint32_t t_begin = part * P;
-    const uint32_t t_end = min(t_begin + P, limit);
-    const PartView pv = load_part(a, seq, t_begin, t_end, lane);
+    const uint32_t t_begin = pv.t_begin, t_end = pv.t_end;
+    const uint32_t part = t_begin / a.part_size;
 
     float4 qv[GMAX], acc[GMAX];
     float m[GMAX], l[GMAX];
@@ -584,6 +591,16 @@ __device__ void decode_item(const AttnArgs& a, const SeqTable& st, const PoolRsr
         if (ts == 0) *reinterpret_cast<float4*>(a.part_out + slot * D + dl * 4) = acc[g];
         if (lane == 0) a.part_stats[slot] = make_float2(m[g], l[g]);
     }
+}
+
+template <int D, int GMAX, int KVT, int NL, int NB, bool BUF>
+__device__ void decode_item(const AttnArgs& a, const SeqTable& st, const PoolRsrc& rs, uint32_t row, uint32_t part,
+                            uint32_t P, uint32_t seq, uint32_t kvh, int lane) {
+    const int32_t ql = st.cu[seq + 1] - st.cu[seq];
+    const uint32_t limit = row_limit(st.ctx[seq], ql, static_cast<int32_t>(row) - st.cu[seq], a.capacity);
+    const uint32_t t_begin = part * P;
+    const PartView pv = load_part(a, seq, t_begin, min(t_begin + P, limit), lane);
+    decode_body<D, GMAX, KVT, NL, NB, BUF>(a, rs, row, kvh, limit, pv, lane);
 }
 
 // ---------------------------------------------------------------- decode rows, 1-byte pools
@@ -716,19 +733,14 @@ __device__ __forceinline__ void decode_compute_q(const AttnArgs& a, const PartVi
 }
 
 template <int D, int GMAX, int KVT, int NL, int NB>
-__device__ void decode_item_q(const AttnArgs& a, const SeqTable& st, const PoolRsrc& rs, uint32_t row,
-                              uint32_t part, uint32_t P,
-                              uint32_t seq, uint32_t kvh, int lane) {
+__device__ void decode_body_q(const AttnArgs& a, const PoolRsrc& rs, uint32_t row, uint32_t kvh, uint32_t limit,
+                              const PartView& pv, int lane) {
     constexpr int LPT = D / kQE;
     constexpr int TT = (kWave / LPT) * NL;
     const int ts = lane / LPT, dl = lane % LPT;
     const uint32_t G = a.group;
-    const int32_t ql = st.cu[seq + 1] - st.cu[seq];
-    const uint32_t limit = row_limit(st.ctx[seq], ql,
-                                     static_cast<int32_t>(row) - st.cu[seq], a.capacity);
-    const uint32_t t_begin = part * P;
-    const uint32_t t_end = min(t_begin + P, limit);
-    const PartView pv = load_part(a, seq, t_begin, t_end, lane);
+    const uint32_t t_begin = pv.t_begin, t_end = pv.t_end;
+    const uint32_t part = t_begin / a.part_size;
 
     float q[GMAX][kQE], acc[GMAX][kQE], m[GMAX], l[GMAX];
 #pragma unroll
@@ -790,6 +802,16 @@ __device__ void decode_item_q(const AttnArgs& a, const SeqTable& st, const PoolR
         }
         if (lane == 0) a.part_stats[slot] = make_float2(m[g], l[g]);
     }
+}
+
+template <int D, int GMAX, int KVT, int NL, int NB>
+__device__ void decode_item_q(const AttnArgs& a, const SeqTable& st, const PoolRsrc& rs, uint32_t row,
+                              uint32_t part, uint32_t P, uint32_t seq, uint32_t kvh, int lane) {
+    const int32_t ql = st.cu[seq + 1] - st.cu[seq];
+    const uint32_t limit = row_limit(st.ctx[seq], ql, static_cast<int32_t>(row) - st.cu[seq], a.capacity);
+    const uint32_t t_begin = part * P;
+    const PartView pv = load_part(a, seq, t_begin, min(t_begin + P, limit), lane);
+    decode_body_q<D, GMAX, KVT, NL, NB>(a, rs, row, kvh, limit, pv, lane);
 }
 
 // ---------------------------------------------------------------- chunk rows (MFMA)
@@ -1258,6 +1280,39 @@ __device__ void chunk_block(const AttnArgs& a, const SeqTable& st, const PoolRsr
     }
 }
 
+// Decode items from the caller's work list: one load per wave gives the item's row,
+// keys and block ids (no sequence table, no block-table round trip), then the same
+// item body as the table-driven path.
+template <int D, int GMAX, int KVT, bool BUF, int NL, int NB>
+__device__ void decode_work(const AttnArgs& a, const PoolRsrc& rs) {
+    const int lane = threadIdx.x & (kWave - 1);
+    const uint32_t wave = blockIdx.x * kWaves + threadIdx.x / kWave;
+    const uint32_t n_waves = gridDim.x * kWaves;
+    const uint32_t n = a.n_work * a.num_kv_heads;
+    for (uint32_t w = wave; w < n; w += n_waves) {
+        const uint32_t item = w / a.num_kv_heads, kvh = w % a.num_kv_heads;
+        const uint32_t word = a.work[static_cast<size_t>(item) * kWorkWords + lane];
+        const uint32_t row = __builtin_amdgcn_readlane(word, kWorkBlocks);
+        const uint32_t limit = __builtin_amdgcn_readlane(word, kWorkBlocks + 3);
+        PartView pv;
+        pv.t_begin = __builtin_amdgcn_readlane(word, kWorkBlocks + 1);
+        pv.t_end = __builtin_amdgcn_readlane(word, kWorkBlocks + 2);
+        pv.blk0 = block_of(a, pv.t_begin);
+        const uint32_t nblk = block_of(a, pv.t_end - 1) - pv.blk0 + 1;  // <= kWorkBlocks (host-checked)
+        uint32_t phys = static_cast<uint32_t>(lane) < nblk ? word : 0u;
+        if (phys >= a.num_blocks) {
+            raise_status(a.status, KANSO_DEV_BLOCK_OOB);
+            phys = 0;
+        }
+        pv.tab = static_cast<int>(phys);
+        if (pv.t_begin == 0 && kvh == 0 && lane == 0) a.row_np[row] = ceil_div(limit, a.part_size);
+        if constexpr (KVT != KANSO_KV_F32 && BUF && D >= kQE)
+            decode_body_q<D, GMAX, KVT, (GMAX <= 4 ? 8 : 4), 2>(a, rs, row, kvh, limit, pv, lane);
+        else
+            decode_body<D, GMAX, KVT, NL, NB, BUF>(a, rs, row, kvh, limit, pv, lane);
+    }
+}
+
 // ---------------------------------------------------------------- kernels
 
 // Rows with no key (an empty context, or more query rows than context) get zeros,
@@ -1292,6 +1347,12 @@ __global__ __launch_bounds__(kThreads, 2) void attn_main(AttnArgs a) {
         rs.v = make_rsrc(a.v_pool, a.pool_bytes);
         rs.ks = make_rsrc(a.k_scales, a.scale_bytes);
         rs.vs = make_rsrc(a.v_scales, a.scale_bytes);
+    }
+    if constexpr (GC == 0) {
+        if (a.work) {
+            decode_work<D, GMAX, KVT, BUF, NL, NB>(a, rs);
+            return;
+        }
     }
     uint32_t n_chunk_wg = 0;
     if constexpr (GC > 0) {
@@ -1514,7 +1575,8 @@ uint32_t host_row_limit(uint32_t ctx_len, uint32_t q_len, uint32_t i, uint32_t c
 int run_ragged(kanso_ctx* ctx, const kanso_ragged_attention_params* p, const float* q,
                const void* kp, const void* vp, const void* ks, const void* vs,
                const uint32_t* tables, const int32_t* cu, const uint32_t* ctx_lens, float* out,
-               hipStream_t stream, const char* who, bool out_tiled = false, void* fixed_scratch = nullptr) {
+               hipStream_t stream, const char* who, bool out_tiled = false, void* fixed_scratch = nullptr,
+               const uint32_t* work = nullptr, uint32_t n_work = 0) {
     const uint32_t S = p->num_seqs, H = p->num_heads, HKV = p->num_kv_heads, D = p->head_dim;
     const bool one_row_each = p->total_q == S && p->max_q_len == 1;
     if (!q || !kp || !vp || !tables || (!cu && !one_row_each) || !ctx_lens || !out) {
@@ -1623,6 +1685,8 @@ int run_ragged(kanso_ctx* ctx, const kanso_ragged_attention_params* p, const flo
     a.row_np = reinterpret_cast<uint32_t*>(base + off_np);
     a.out = out;
     a.out_nbk = out_tiled ? H * D / 32 : 0u;
+    a.work = nullptr;
+    a.n_work = 0;
     a.status = ctx->status;
     a.num_seqs = S;
     a.num_heads = H;
@@ -1656,6 +1720,17 @@ int run_ragged(kanso_ctx* ctx, const kanso_ragged_attention_params* p, const flo
     a.use_mfma = use_mfma_path(p, max_q) ? 1u : 0u;
     a.head_major = p->pool_layout == KANSO_POOL_HEAD_MAJOR ? 1u : 0u;
     Stage1Fn main_fn = pick_main_kv(p->kv_dtype, D, G, buf, a.use_mfma != 0);
+    if (work) {
+        // the work-list path: single-row sequences, the decode kernel with buffer
+        // loads, partitions whose block ids fit an item
+        if (!one_row_each || a.use_mfma || !buf || p->partition_size == 0 || P > kWorkBlocks * p->block_size ||
+            p->kv_dtype == KANSO_KV_FP8 || n_work == 0) {
+            set_error("%s: work list given for a batch it cannot serve", who);
+            return KANSO_E_INVALID_ARG;
+        }
+        a.work = work;
+        a.n_work = n_work;
+    }
     const bool wide_merge = max_parts > 16;
     Stage1Fn reduce = pick_reduce(D, wide_merge);
     if (!main_fn || !reduce) {
@@ -1681,17 +1756,23 @@ int run_ragged(kanso_ctx* ctx, const kanso_ragged_attention_params* p, const flo
 
 }  // namespace
 
+bool ragged_work_supported(const kanso_ragged_attention_params* p) {
+    return p->total_q == p->num_seqs && p->max_q_len == 1 && p->head_dim == 64 && p->kv_dtype != KANSO_KV_FP8 &&
+           p->partition_size != 0 && p->partition_size <= kWorkBlocks * p->block_size && pool_fits_rsrc(p) &&
+           p->pool_layout == KANSO_POOL_TOKEN_MAJOR;
+}
+
 int op_ragged_attention(kanso_ctx* ctx, const kanso_ragged_attention_params* p, const float* q, const void* k_pool,
                         const void* v_pool, const void* k_scales, const void* v_scales, const uint32_t* block_tables,
                         const int32_t* cu_seqlens, const uint32_t* context_lens, float* out, hipStream_t s,
-                        bool out_tiled) {
+                        bool out_tiled, const uint32_t* work, uint32_t n_work) {
     if (out_tiled && (p->num_heads * p->head_dim) % 32 != 0) {
         set_error("ragged attention: tiled output needs heads x head_dim (%u) to be a multiple of 32",
                   p->num_heads * p->head_dim);
         return KANSO_E_INVALID_SHAPE;
     }
     return run_ragged(ctx, p, q, k_pool, v_pool, k_scales, v_scales, block_tables, cu_seqlens, context_lens, out, s,
-                      "ragged attention", out_tiled);
+                      "ragged attention", out_tiled, nullptr, work, n_work);
 }
 
 int noalloc_scratch_init(void** ptr) {

@@ -226,7 +226,8 @@ float* norm_slot(kanso_model* m, uint32_t kind, uint32_t layer) {
     return nullptr;
 }
 
-int ensure_step_buffers(kanso_model* m, uint32_t T, uint32_t S, uint32_t tables, uint32_t arena) {
+int ensure_step_buffers(kanso_model* m, uint32_t T, uint32_t S, uint32_t tables, uint32_t arena,
+                        size_t work_bytes = 0) {
     const kanso_model_config& c = m->cfg;
     int rc;
     if (T > m->cap_tokens || S > m->cap_seqs) {
@@ -264,7 +265,8 @@ int ensure_step_buffers(kanso_model* m, uint32_t T, uint32_t S, uint32_t tables,
         m->cap_tables = want;
     }
     const size_t need = align_up(static_cast<size_t>(S) * sizeof(kanso_seq_plan), 256) +
-                        align_up(static_cast<size_t>(arena) * 4, 256) + align_up(static_cast<size_t>(S) * 4, 256);
+                        align_up(static_cast<size_t>(arena) * 4, 256) + align_up(static_cast<size_t>(S) * 4, 256) +
+                        work_bytes;
     if (need > m->stage_bytes) {
         const size_t want = align_up(need + need / 2, 1 << 16);
         KANSO_HIP_TRY(hipDeviceSynchronize());
@@ -367,49 +369,6 @@ int model_forward(kanso_model* m, const HostStep& step, float* logits, uint32_t*
         max_blocks = std::max(max_blocks, std::max((ctx + m->block_size - 1) / m->block_size, 1u));
     }
     const uint32_t R = all_rows ? T : S;  // rows through the lm_head
-    int rc = ensure_step_buffers(m, T, std::max(S, R), S * max_blocks,
-                                 static_cast<uint32_t>(step.token_arena.size() + step.table_arena.size()));
-    if (rc) return rc;
-    // Stage: plan | token arena + table arena | last rows.
-    char* h = static_cast<char*>(m->h_stage);
-    const size_t off_arena = align_up(S * sizeof(kanso_seq_plan), 256);
-    const size_t arena_n = step.token_arena.size() + step.table_arena.size();
-    const size_t off_last = off_arena + align_up(arena_n * 4, 256);
-    std::memcpy(h, step.plan.data(), S * sizeof(kanso_seq_plan));
-    std::memcpy(h + off_arena, step.token_arena.data(), step.token_arena.size() * 4);
-    std::memcpy(h + off_arena + step.token_arena.size() * 4, step.table_arena.data(), step.table_arena.size() * 4);
-    int32_t* last = reinterpret_cast<int32_t*>(h + off_last);
-    if (all_rows) {
-        for (uint32_t i = 0; i < T; ++i) last[i] = static_cast<int32_t>(i);
-    } else {
-        int32_t run = 0;
-        for (uint32_t i = 0; i < S; ++i) {
-            run += static_cast<int32_t>(step.plan[i].q_len);
-            last[i] = run - 1;
-        }
-    }
-    KANSO_HIP_TRY(hipMemcpyAsync(m->d_stage, h, off_last + R * 4ull, hipMemcpyHostToDevice, s));
-    char* d = static_cast<char*>(m->d_stage);
-    const auto* d_plan = reinterpret_cast<const kanso_seq_plan*>(d);
-    const auto* d_tok_arena = reinterpret_cast<const uint32_t*>(d + off_arena);
-    const auto* d_tab_arena = d_tok_arena + step.token_arena.size();
-    const auto* d_last = reinterpret_cast<const int32_t*>(d + off_last);
-
-    kanso_packed_step packed{m->cu, m->seq_of_query, m->positions, m->slots, m->tokens, m->tables, m->ctx_lens};
-    if ((rc = kanso_pack_step(m->ctx, d_plan, S, d_tok_arena, d_tab_arena, m->block_size, max_blocks, T, &packed,
-                              reinterpret_cast<kanso_stream_t>(s))))
-        return rc;
-    // hidden, attn and act are in the tiled activation order (act_tile_off): the
-    // products read them as contiguous 1 KB slices
-    // Granite multipliers: the reference multiplies by the f64 scale on f32 tensors,
-    // i.e. by the scale rounded to f32 (src/model.rs:424-430, 739-760)
-    const float emb_mul = c.embedding_scale != 0.f ? c.embedding_scale : 1.f;
-    const float res_mul = c.residual_scale != 0.f ? c.residual_scale : 1.f;
-    const float logit_mul = c.logit_scale != 0.f ? static_cast<float>(1.0 / static_cast<double>(c.logit_scale)) : 1.f;
-    if ((rc = op_embed(m->ctx, m->embed, c.vocab, c.hidden, m->tokens, T, m->hidden, s, true, emb_mul))) return rc;
-
-    kanso_qkv_params qp{T, c.hidden, c.num_heads, c.num_kv_heads, 64, c.max_position, c.eps, m->num_blocks,
-                        m->block_size};
     kanso_ragged_attention_params ap{};
     ap.num_seqs = S;
     ap.num_heads = c.num_heads;
@@ -435,6 +394,82 @@ int model_forward(kanso_model* m, const HostStep& step, float* logits, uint32_t*
         ap.partition_size = kanso_ragged_partition_size(m->ctx, &ap, ql.data(), cl.data());
         ap.chunk_partition_size = kanso_ragged_chunk_partition_size(m->ctx, &ap, ql.data(), cl.data());
     }
+    // A step of single-row sequences takes the attention's work-list path: the items
+    // (row, partition) with their block ids come from the host's plan in the same
+    // upload as the plan, so an attention wave's first load is its item and its
+    // second its keys (no sequence table, no block-table round trip).
+    const uint32_t cap = max_blocks * m->block_size;
+    const uint32_t P = ap.partition_size;
+    uint32_t n_items = 0;
+    const bool use_work = max_q == 1 && ragged_work_supported(&ap);
+    if (use_work)
+        for (const auto& p : step.plan) n_items += (std::min(p.start_pos + 1, cap) + P - 1) / P;
+    int rc = ensure_step_buffers(m, T, std::max(S, R), S * max_blocks,
+                                 static_cast<uint32_t>(step.token_arena.size() + step.table_arena.size()),
+                                 static_cast<size_t>(n_items) * kanso_ragged_work_item_words * 4);
+    if (rc) return rc;
+    // Stage: plan | token arena + table arena | last rows.
+    char* h = static_cast<char*>(m->h_stage);
+    const size_t off_arena = align_up(S * sizeof(kanso_seq_plan), 256);
+    const size_t arena_n = step.token_arena.size() + step.table_arena.size();
+    const size_t off_last = off_arena + align_up(arena_n * 4, 256);
+    std::memcpy(h, step.plan.data(), S * sizeof(kanso_seq_plan));
+    std::memcpy(h + off_arena, step.token_arena.data(), step.token_arena.size() * 4);
+    std::memcpy(h + off_arena + step.token_arena.size() * 4, step.table_arena.data(), step.table_arena.size() * 4);
+    int32_t* last = reinterpret_cast<int32_t*>(h + off_last);
+    if (all_rows) {
+        for (uint32_t i = 0; i < T; ++i) last[i] = static_cast<int32_t>(i);
+    } else {
+        int32_t run = 0;
+        for (uint32_t i = 0; i < S; ++i) {
+            run += static_cast<int32_t>(step.plan[i].q_len);
+            last[i] = run - 1;
+        }
+    }
+    const size_t off_work = align_up(off_last + R * 4ull, 256);
+    size_t stage_n = off_last + R * 4ull;
+    if (use_work) {
+        uint32_t* wk = reinterpret_cast<uint32_t*>(h + off_work);
+        const uint32_t W = kanso_ragged_work_item_words, B = W - 4;
+        for (uint32_t i = 0; i < S; ++i) {
+            const kanso_seq_plan& p = step.plan[i];
+            const uint32_t limit = std::min(p.start_pos + 1, cap);
+            const uint32_t* tab = step.table_arena.data() + p.table_offset;
+            for (uint32_t t0 = 0; t0 < limit; t0 += P, wk += W) {
+                const uint32_t t1 = std::min(t0 + P, limit);
+                const uint32_t b0 = t0 / m->block_size, nb = (t1 - 1) / m->block_size - b0 + 1;
+                for (uint32_t j = 0; j < B; ++j) wk[j] = j < nb && b0 + j < p.table_len ? tab[b0 + j] : 0u;
+                wk[B] = i;  // the row: one per sequence
+                wk[B + 1] = t0;
+                wk[B + 2] = t1;
+                wk[B + 3] = limit;
+            }
+        }
+        stage_n = off_work + static_cast<size_t>(n_items) * W * 4;
+    }
+    KANSO_HIP_TRY(hipMemcpyAsync(m->d_stage, h, stage_n, hipMemcpyHostToDevice, s));
+    char* d = static_cast<char*>(m->d_stage);
+    const auto* d_plan = reinterpret_cast<const kanso_seq_plan*>(d);
+    const auto* d_tok_arena = reinterpret_cast<const uint32_t*>(d + off_arena);
+    const auto* d_tab_arena = d_tok_arena + step.token_arena.size();
+    const auto* d_last = reinterpret_cast<const int32_t*>(d + off_last);
+    const auto* d_work = use_work ? reinterpret_cast<const uint32_t*>(d + off_work) : nullptr;
+
+    kanso_packed_step packed{m->cu, m->seq_of_query, m->positions, m->slots, m->tokens, m->tables, m->ctx_lens};
+    if ((rc = kanso_pack_step(m->ctx, d_plan, S, d_tok_arena, d_tab_arena, m->block_size, max_blocks, T, &packed,
+                              reinterpret_cast<kanso_stream_t>(s))))
+        return rc;
+    // hidden, attn and act are in the tiled activation order (act_tile_off): the
+    // products read them as contiguous 1 KB slices
+    // Granite multipliers: the reference multiplies by the f64 scale on f32 tensors,
+    // i.e. by the scale rounded to f32 (src/model.rs:424-430, 739-760)
+    const float emb_mul = c.embedding_scale != 0.f ? c.embedding_scale : 1.f;
+    const float res_mul = c.residual_scale != 0.f ? c.residual_scale : 1.f;
+    const float logit_mul = c.logit_scale != 0.f ? static_cast<float>(1.0 / static_cast<double>(c.logit_scale)) : 1.f;
+    if ((rc = op_embed(m->ctx, m->embed, c.vocab, c.hidden, m->tokens, T, m->hidden, s, true, emb_mul))) return rc;
+
+    kanso_qkv_params qp{T, c.hidden, c.num_heads, c.num_kv_heads, 64, c.max_position, c.eps, m->num_blocks,
+                        m->block_size};
     const uint32_t qd = c.num_heads * 64;
     const bool quant = m->kv_dtype != KANSO_KV_F32;
     // 1-byte pools: the QKV epilogue quantizes each K / V row into its pool slot
@@ -459,7 +494,7 @@ int model_forward(kanso_model* m, const HostStep& step, float* logits, uint32_t*
             return rc;
         }
         if ((rc = op_ragged_attention(m->ctx, &ap, m->q, kp, vp, ks, vs, m->tables, m->cu, m->ctx_lens, m->attn, s,
-                                      true)))
+                                      true, d_work, n_items)))
             return rc;
         if ((rc = op_gemm_residual(o4 ? L.o_q4k : L.o, m->attn, m->hidden, c.hidden, qd, T, s, true, o4, res_mul)))
             return rc;
