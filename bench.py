@@ -39,6 +39,7 @@ METRIC = "ragged paged-attn tokens/s + % HBM peak; batched decode tok/s at 1 MI3
 POOL_LAYOUT = 0  # KANSO_POOL_TOKEN_MAJOR unless --pool-layout head
 PARTITION = 0  # 0: kanso_ragged_partition_size per batch; -1: the library's choice; > 0: fixed
 CHUNK_PARTITION = 0  # > 0: a fixed chunk partition (else from the lengths, or the library's)
+WORK = True  # pass the decode work list built from the host-side plan, as the engine does
 
 
 def log(msg: str) -> None:
@@ -115,13 +116,25 @@ class AttnBench:
                 self.ctx, q_lens=b.q_lens, context_lens=b.context_lens, num_heads=b.num_heads,
                 num_kv_heads=b.num_kv_heads, head_dim=b.head_dim, block_size=b.block_size,
                 max_blocks=b.max_blocks, kv_dtype=self.kv_dtype, num_blocks=self.num_blocks)
+            # the decode work list from the same host-side plan (the engine builds it
+            # per step and uploads it with the plan); None where the batch cannot
+            # take one or a partition is not given
+            w = None
+            if WORK and d["P"]:
+                w = self.K.ragged_work(
+                    q_lens=b.q_lens, context_lens=b.context_lens, block_tables=b.block_tables,
+                    num_heads=b.num_heads, num_kv_heads=b.num_kv_heads, head_dim=b.head_dim,
+                    block_size=b.block_size, partition_size=d["P"], kv_dtype=self.kv_dtype,
+                    num_blocks=self.num_blocks, max_q_len=int(b.q_lens.max()), pool_layout=POOL_LAYOUT,
+                    chunk_partition_size=d["CP"])
+            d["work"] = None if w is None else self.torch.from_numpy(w.view(np.int32)).to("cuda:0")
         self.K.ragged_paged_attention(
             self.ctx, q=d["q"], k_pool=self.k, v_pool=self.v, k_scales=self.ks, v_scales=self.vs,
             block_tables=d["tables"], cu_seqlens=d["cu"], context_lens=d["lens"], out=d["out"],
             num_heads=b.num_heads, num_kv_heads=b.num_kv_heads, head_dim=b.head_dim,
             block_size=b.block_size, scale=b.scale, kv_dtype=self.kv_dtype,
             num_blocks=self.num_blocks, max_q_len=int(b.q_lens.max()),
-            pool_layout=POOL_LAYOUT, partition_size=d["P"], chunk_partition_size=d["CP"])
+            pool_layout=POOL_LAYOUT, partition_size=d["P"], chunk_partition_size=d["CP"], work=d["work"])
 
     def run(self, steps, warmup):
         torch = self.torch
@@ -725,6 +738,8 @@ def main():
     ap.add_argument("--partition", type=int, default=0,
                     help="split-K partition of the attention benchmarks: 0 = from the batch's "
                          "lengths (kanso_ragged_partition_size), -1 = the library's own choice")
+    ap.add_argument("--no-work", action="store_true",
+                    help="attention calls without the decode work list (the table-driven path)")
     ap.add_argument("--chunk-partition", type=int, default=0,
                     help="fixed partition of the MFMA chunk rows (a multiple of 32; 0 = the "
                          "library's rule)")
@@ -736,10 +751,11 @@ def main():
     ap.add_argument("--decode-only", action="store_true",
                     help="also time the headline batches' decode rows alone")
     args = ap.parse_args()
-    global POOL_LAYOUT, PARTITION, CHUNK_PARTITION
+    global POOL_LAYOUT, PARTITION, CHUNK_PARTITION, WORK
     POOL_LAYOUT = 1 if args.pool_layout == "head" else 0
     PARTITION = args.partition
     CHUNK_PARTITION = args.chunk_partition
+    WORK = not args.no_work
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print("bench.py measures one GPU: this build has no multi-GPU component (the path "
               "would shard by sequences, one engine and KV pool per GPU); run with --gpus 1",
@@ -800,12 +816,26 @@ def main():
 
     extras = {}
     extras["partitions"] = [d["P"] for d in hb.dev_batches]
+    extras["work_list"] = [d["work"] is not None for d in hb.dev_batches]
+    if WORK:
+        # the same batches through the table-driven path (no work list)
+        WORK = False
+        tp = AttnBench.__new__(AttnBench)
+        tp.__dict__.update(hb.__dict__)
+        tp.dev_batches = [{k: v for k, v in d.items() if k not in ("P", "work")} for d in hb.dev_batches]
+        rt = tp.run(args.steps, args.warmup)
+        WORK = True
+        extras["headline_table_path"] = dict(
+            tokens_per_s=round(rt["tokens_per_s"], 1), ms_per_step=round(rt["ms_per_step"], 5),
+            stage1_gbps=round(rt["stage1_gbps"], 1),
+            hbm_frac_stage1=round(rt["stage1_gbps"] * 1e9 / HBM_PEAK, 4))
+        log(f"config2, table path: {extras['headline_table_path']}")
     if not args.quick and PARTITION == 0:
         # the same batches with the library's own partition (no host lengths)
         PARTITION = -1
         lib = AttnBench.__new__(AttnBench)
         lib.__dict__.update(hb.__dict__)
-        lib.dev_batches = [{k: v for k, v in d.items() if k != "P"} for d in hb.dev_batches]
+        lib.dev_batches = [{k: v for k, v in d.items() if k not in ("P", "work")} for d in hb.dev_batches]
         rl = lib.run(args.steps, args.warmup)
         PARTITION = 0
         extras["headline_library_partition"] = dict(
@@ -945,6 +975,9 @@ def main():
             "rotation": "8 batches",
             "partition": "per batch from its host-side lengths (kanso_ragged_partition_size), "
                          "as the engine passes it from its plan",
+            "work_list": ("decode rows from the work list built on the host from the same plan "
+                          "(kanso_ragged_build_work, uploaded once per batch outside the timed "
+                          "region as the engine uploads it with each step's plan)") if WORK else None,
         },
         "roofline": {
             "bound": "hbm",

@@ -211,6 +211,34 @@ int kanso_ragged_paged_attention(kanso_ctx* ctx, const kanso_ragged_attention_pa
                                  const uint32_t* context_lens, float* out,
                                  kanso_stream_t stream);
 
+/* Decode work list of a planned batch. The caller that planned the step holds its
+ * query lengths, context lengths and block tables on the host (Engine::step's
+ * query_lens / context_lens / block tables, src/engine.rs:376-402); from them
+ * kanso_ragged_build_work writes one item of KANSO_RAGGED_WORK_ITEM_WORDS u32 per
+ * (row, partition) of every row outside the matrix-core chunk path: the
+ * partition's physical block ids, then the row, its first key, its end key and the
+ * row's key count. kanso_ragged_paged_attention_work then takes that list (uploaded
+ * to the device) instead of deriving the items from the sequence and block tables:
+ * an attention wave's first load is its item, its second its keys. Results are
+ * bit-identical to kanso_ragged_paged_attention's. p->partition_size must be set
+ * (kanso_ragged_partition_size), at most 60 blocks; INT8 / Q8_0 / F32 pools,
+ * token-major layout. kanso_ragged_work_items returns the item count, 0 when the
+ * batch cannot take a list (then call kanso_ragged_paged_attention). No
+ * counterpart in the reference (the Metal kernel derives its work from the grid).
+ * block_tables is the host copy of the [num_seqs][max_num_blocks_per_seq] table
+ * the attention call reads. Host-only; launch nothing. */
+#define KANSO_RAGGED_WORK_ITEM_WORDS 64u
+uint32_t kanso_ragged_work_items(const kanso_ragged_attention_params* p, const uint32_t* q_lens,
+                                 const uint32_t* context_lens);
+int kanso_ragged_build_work(const kanso_ragged_attention_params* p, const uint32_t* q_lens,
+                            const uint32_t* context_lens, const uint32_t* block_tables, uint32_t* work,
+                            uint32_t n_items);
+int kanso_ragged_paged_attention_work(kanso_ctx* ctx, const kanso_ragged_attention_params* p, const float* q,
+                                      const void* k_pool, const void* v_pool, const void* k_scales,
+                                      const void* v_scales, const uint32_t* block_tables,
+                                      const int32_t* cu_seqlens, const uint32_t* context_lens, float* out,
+                                      const uint32_t* work, uint32_t n_work, kanso_stream_t stream);
+
 /* kanso_ragged_paged_attention without any allocation: the same kernels, with
  * their split-K partials, statistics and per-row partition counts in a fixed
  * 64 MiB device array that each GPU holds for the life of the process (its

@@ -36,7 +36,7 @@ from ._capi import (KANSO_KV_F32, KANSO_KV_FP8, KANSO_KV_INT8, KANSO_KV_Q8_0, Pa
 __all__ = [
     "EngineError", "Context", "PagedAttentionParams", "paged_attention_num_partitions",
     "validate_paged_attention_params", "gpu_paged_attention_v2", "paged_attention_v2",
-    "ragged_paged_attention", "pack_step", "kv_append", "kv_reset_blocks", "gemv_q8_0",
+    "ragged_paged_attention", "ragged_work", "pack_step", "kv_append", "kv_reset_blocks", "gemv_q8_0",
     "gemv_q4_k", "KANSO_KV_F32", "KANSO_KV_INT8", "KANSO_KV_Q8_0", "KANSO_KV_FP8", "ragged_partition_size", "ragged_chunk_partition_size", "q8_0_packed_bytes",
     "q8_0_pack", "gemm_q8_0", "gemm_q8_0_residual", "embed_q8_0", "qkv_rope_append",
     "qkv_rope_append_quant",
@@ -206,20 +206,49 @@ def ragged_paged_attention(ctx: Context, *, q: torch.Tensor, k_pool: torch.Tenso
                            k_scales: torch.Tensor | None = None,
                            v_scales: torch.Tensor | None = None, num_blocks: int = 0,
                            max_q_len: int = 0, pool_layout: int = 0, partition_size: int = 0,
-                           chunk_partition_size: int = 0,
+                           chunk_partition_size: int = 0, work: torch.Tensor | None = None,
                            stream: torch.cuda.Stream | None = None) -> None:
     """Mixed prefill + decode attention over the paged pool (kanso_ragged_paged_attention).
-    cu_seqlens None: a decode batch, one query row per sequence."""
+    cu_seqlens None: a decode batch, one query row per sequence. work: a device copy of
+    ragged_work's list (kanso_ragged_paged_attention_work)."""
     num_seqs = cu_seqlens.numel() - 1 if cu_seqlens is not None else context_lens.numel()
     max_blocks = block_tables.numel() // max(num_seqs, 1)
     total_q = q.numel() // (num_heads * head_dim)
     p = RaggedAttentionParamsC(num_seqs, num_heads, num_kv_heads, head_dim, block_size, max_blocks,
                                scale, total_q, kv_dtype, num_blocks, max_q_len, pool_layout,
                                partition_size, chunk_partition_size)
-    _check(ctx._lib.kanso_ragged_paged_attention(
-        ctx.handle, C.byref(p), _ptr(q), _ptr(k_pool), _ptr(v_pool), _ptr(k_scales),
-        _ptr(v_scales), _ptr(block_tables), _ptr(cu_seqlens), _ptr(context_lens), _ptr(out),
-        _stream(stream)))
+    args = (ctx.handle, C.byref(p), _ptr(q), _ptr(k_pool), _ptr(v_pool), _ptr(k_scales),
+            _ptr(v_scales), _ptr(block_tables), _ptr(cu_seqlens), _ptr(context_lens), _ptr(out))
+    if work is None:
+        _check(ctx._lib.kanso_ragged_paged_attention(*args, _stream(stream)))
+    else:
+        _check(ctx._lib.kanso_ragged_paged_attention_work(
+            *args, _ptr(work), work.numel() // _capi.KANSO_RAGGED_WORK_ITEM_WORDS, _stream(stream)))
+
+
+def ragged_work(*, q_lens, context_lens, block_tables, num_heads: int, num_kv_heads: int,
+                head_dim: int, block_size: int, partition_size: int, kv_dtype: int = KANSO_KV_F32,
+                num_blocks: int = 0, max_q_len: int = 0, pool_layout: int = 0,
+                chunk_partition_size: int = 0) -> np.ndarray | None:
+    """The decode work list of a planned batch (kanso_ragged_build_work) from host
+    lengths and the host copy of the [S, max_blocks] block table; None when the batch
+    cannot take one (kanso_ragged_work_items == 0). Host-only."""
+    lib = _capi.load()
+    ql = np.ascontiguousarray(np.asarray(q_lens, dtype=np.uint32))
+    cl = np.ascontiguousarray(np.asarray(context_lens, dtype=np.uint32))
+    tabs = np.ascontiguousarray(np.asarray(block_tables, dtype=np.uint32).reshape(ql.size, -1))
+    p = RaggedAttentionParamsC(ql.size, num_heads, num_kv_heads, head_dim, block_size, tabs.shape[1],
+                               1.0, int(ql.sum()), kv_dtype, num_blocks, max_q_len, pool_layout,
+                               partition_size, chunk_partition_size)
+    n = int(lib.kanso_ragged_work_items(C.byref(p), ql.ctypes.data_as(C.c_void_p),
+                                        cl.ctypes.data_as(C.c_void_p)))
+    if n == 0:
+        return None
+    out = np.zeros(n * _capi.KANSO_RAGGED_WORK_ITEM_WORDS, np.uint32)
+    _check(lib.kanso_ragged_build_work(C.byref(p), ql.ctypes.data_as(C.c_void_p),
+                                       cl.ctypes.data_as(C.c_void_p), tabs.ctypes.data_as(C.c_void_p),
+                                       out.ctypes.data_as(C.c_void_p), n))
+    return out
 
 
 def _lengths_call(fn, q_lens, context_lens, num_heads, num_kv_heads, head_dim, block_size,

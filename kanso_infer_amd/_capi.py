@@ -34,6 +34,7 @@ KANSO_KV_F32 = 0
 KANSO_KV_INT8 = 1
 KANSO_KV_Q8_0 = 2
 KANSO_KV_FP8 = 3
+KANSO_RAGGED_WORK_ITEM_WORDS = 64  # kanso_hip.h
 
 KANSO_POOL_TOKEN_MAJOR = 0
 KANSO_POOL_HEAD_MAJOR = 1
@@ -154,6 +155,10 @@ SIGNATURES: dict[str, tuple] = {
     "kanso_ragged_chunk_partition_size": (C.c_uint32, [_P, C.POINTER(RaggedAttentionParamsC), _P, _P]),
     "kanso_ragged_paged_attention": (
         _I, [_P, C.POINTER(RaggedAttentionParamsC), _P, _P, _P, _P, _P, _P, _P, _P, _P, _P]),
+    "kanso_ragged_work_items": (C.c_uint32, [C.POINTER(RaggedAttentionParamsC), _P, _P]),
+    "kanso_ragged_build_work": (_I, [C.POINTER(RaggedAttentionParamsC), _P, _P, _P, _P, _U]),
+    "kanso_ragged_paged_attention_work": (
+        _I, [_P, C.POINTER(RaggedAttentionParamsC), _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _U, _P]),
     "kanso_ragged_paged_attention_noalloc": (
         _I, [_P, C.POINTER(RaggedAttentionParamsC), _P, _P, _P, _P, _P, _P, _P, _P, _P, _P]),
     "kanso_pack_step": (_I, [_P, _P, _U, _P, _P, _U, _U, _U, C.POINTER(PackedStepC), _P]),

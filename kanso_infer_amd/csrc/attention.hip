@@ -1284,10 +1284,10 @@ __device__ void chunk_block(const AttnArgs& a, const SeqTable& st, const PoolRsr
 // keys and block ids (no sequence table, no block-table round trip), then the same
 // item body as the table-driven path.
 template <int D, int GMAX, int KVT, bool BUF, int NL, int NB>
-__device__ void decode_work(const AttnArgs& a, const PoolRsrc& rs) {
+__device__ void decode_work(const AttnArgs& a, const PoolRsrc& rs, uint32_t first_wg) {
     const int lane = threadIdx.x & (kWave - 1);
-    const uint32_t wave = blockIdx.x * kWaves + threadIdx.x / kWave;
-    const uint32_t n_waves = gridDim.x * kWaves;
+    const uint32_t wave = (blockIdx.x - first_wg) * kWaves + threadIdx.x / kWave;
+    const uint32_t n_waves = (gridDim.x - first_wg) * kWaves;
     const uint32_t n = a.n_work * a.num_kv_heads;
     for (uint32_t w = wave; w < n; w += n_waves) {
         const uint32_t item = w / a.num_kv_heads, kvh = w % a.num_kv_heads;
@@ -1350,7 +1350,7 @@ __global__ __launch_bounds__(kThreads, 2) void attn_main(AttnArgs a) {
     }
     if constexpr (GC == 0) {
         if (a.work) {
-            decode_work<D, GMAX, KVT, BUF, NL, NB>(a, rs);
+            decode_work<D, GMAX, KVT, BUF, NL, NB>(a, rs, 0);
             return;
         }
     }
@@ -1383,6 +1383,10 @@ __global__ __launch_bounds__(kThreads, 2) void attn_main(AttnArgs a) {
                     __syncthreads();  // the next item's prologue reuses the stages
                 }
                 if (n_chunk_wg) return;  // chunk workgroup: done
+            }
+            if (a.work) {  // decode rows from the caller's list: no decode tables
+                decode_work<D, GMAX, KVT, BUF, NL, NB>(a, rs, n_chunk_wg);
+                return;
             }
             __syncthreads();  // the decode tables below overwrite the chunk tables
         }
@@ -1721,10 +1725,9 @@ int run_ragged(kanso_ctx* ctx, const kanso_ragged_attention_params* p, const flo
     a.head_major = p->pool_layout == KANSO_POOL_HEAD_MAJOR ? 1u : 0u;
     Stage1Fn main_fn = pick_main_kv(p->kv_dtype, D, G, buf, a.use_mfma != 0);
     if (work) {
-        // the work-list path: single-row sequences, the decode kernel with buffer
-        // loads, partitions whose block ids fit an item
-        if (!one_row_each || a.use_mfma || !buf || p->partition_size == 0 || P > kWorkBlocks * p->block_size ||
-            p->kv_dtype == KANSO_KV_FP8 || n_work == 0) {
+        // the work-list path (kanso_ragged_build_work): decode rows from the list,
+        // MFMA chunk rows (if any) from the sequence tables
+        if (!ragged_work_supported(p) || n_work == 0) {
             set_error("%s: work list given for a batch it cannot serve", who);
             return KANSO_E_INVALID_ARG;
         }
@@ -1757,9 +1760,56 @@ int run_ragged(kanso_ctx* ctx, const kanso_ragged_attention_params* p, const flo
 }  // namespace
 
 bool ragged_work_supported(const kanso_ragged_attention_params* p) {
-    return p->total_q == p->num_seqs && p->max_q_len == 1 && p->head_dim == 64 && p->kv_dtype != KANSO_KV_FP8 &&
-           p->partition_size != 0 && p->partition_size <= kWorkBlocks * p->block_size && pool_fits_rsrc(p) &&
-           p->pool_layout == KANSO_POOL_TOKEN_MAJOR;
+    return p->kv_dtype != KANSO_KV_FP8 && p->partition_size != 0 && p->partition_size % 32 == 0 &&
+           p->partition_size <= std::min(992u, kWorkBlocks * p->block_size) && p->block_size != 0 &&
+           pool_fits_rsrc(p) && p->pool_layout == KANSO_POOL_TOKEN_MAJOR && p->num_kv_heads != 0 &&
+           p->num_heads % p->num_kv_heads == 0;
+}
+
+// The decode items of a batch (every row outside the MFMA chunk path, per partition)
+// in row order, or 0 when the batch cannot take a work list (a row without keys,
+// or parameters the list path does not serve). Fills `work` when given.
+uint64_t ragged_work(const kanso_ragged_attention_params* p, const uint32_t* q_lens, const uint32_t* context_lens,
+                     const uint32_t* block_tables, uint32_t* work) {
+    if (!ragged_work_supported(p)) return 0;
+    const uint32_t S = p->num_seqs, P = p->partition_size, bs = p->block_size;
+    const uint64_t cap64 = static_cast<uint64_t>(p->max_num_blocks_per_seq) * bs;
+    const uint32_t cap = static_cast<uint32_t>(std::min<uint64_t>(cap64, 0xffffffffu));
+    uint64_t T = 0;
+    uint32_t max_q = 0;
+    for (uint32_t s = 0; s < S; ++s) {
+        T += q_lens[s];
+        max_q = std::max(max_q, q_lens[s]);
+    }
+    if (T != p->total_q || T == 0) return 0;
+    const bool mfma = use_mfma_path(p, p->max_q_len ? p->max_q_len : max_q);
+    uint64_t n = 0;
+    uint32_t row = 0;
+    for (uint32_t s = 0; s < S; ++s) {
+        const uint32_t ql = q_lens[s], c = context_lens[s];
+        if (mfma && ql > 1) {
+            if (host_row_limit(c, ql, 0, cap) == 0) return 0;  // rows without keys: table path
+            row += ql;
+            continue;
+        }
+        for (uint32_t i = 0; i < ql; ++i, ++row) {
+            const uint32_t limit = host_row_limit(c, ql, i, cap);
+            if (limit == 0) return 0;
+            for (uint32_t t0 = 0; t0 < limit; t0 += P, ++n) {
+                if (!work) continue;
+                uint32_t* w = work + n * kWorkWords;
+                const uint32_t t1 = std::min(t0 + P, limit);
+                const uint32_t b0 = t0 / bs, nb = (t1 - 1) / bs - b0 + 1;
+                const uint32_t* tab = block_tables + static_cast<size_t>(s) * p->max_num_blocks_per_seq;
+                for (uint32_t j = 0; j < kWorkBlocks; ++j) w[j] = j < nb ? tab[b0 + j] : 0u;
+                w[kWorkBlocks] = row;
+                w[kWorkBlocks + 1] = t0;
+                w[kWorkBlocks + 2] = t1;
+                w[kWorkBlocks + 3] = limit;
+            }
+        }
+    }
+    return n;
 }
 
 int op_ragged_attention(kanso_ctx* ctx, const kanso_ragged_attention_params* p, const float* q, const void* k_pool,
@@ -1884,6 +1934,47 @@ uint32_t kanso_ragged_chunk_partition_size(const kanso_ctx* ctx, const kanso_rag
         if (n_chunk <= resident) return cp;
     }
     return p_max;
+}
+
+uint32_t kanso_ragged_work_items(const kanso_ragged_attention_params* p, const uint32_t* q_lens,
+                                 const uint32_t* context_lens) {
+    if (!p || !q_lens || !context_lens || p->num_seqs == 0) return 0;
+    const uint64_t n = ragged_work(p, q_lens, context_lens, nullptr, nullptr);
+    return n <= 0xffffffffu ? static_cast<uint32_t>(n) : 0u;
+}
+
+int kanso_ragged_build_work(const kanso_ragged_attention_params* p, const uint32_t* q_lens,
+                            const uint32_t* context_lens, const uint32_t* block_tables, uint32_t* work,
+                            uint32_t n_items) {
+    if (!p || !q_lens || !context_lens || !block_tables || !work || p->num_seqs == 0) {
+        set_error("kanso_ragged_build_work: null argument");
+        return KANSO_E_INVALID_ARG;
+    }
+    const uint64_t n = ragged_work(p, q_lens, context_lens, nullptr, nullptr);
+    if (n == 0 || n != n_items) {
+        set_error("kanso_ragged_build_work: the batch has %llu work items, the buffer %u",
+                  static_cast<unsigned long long>(n), n_items);
+        return KANSO_E_INVALID_SHAPE;
+    }
+    ragged_work(p, q_lens, context_lens, block_tables, work);
+    return KANSO_OK;
+}
+
+int kanso_ragged_paged_attention_work(kanso_ctx* ctx, const kanso_ragged_attention_params* p, const float* q,
+                                      const void* k_pool, const void* v_pool, const void* k_scales,
+                                      const void* v_scales, const uint32_t* block_tables,
+                                      const int32_t* cu_seqlens, const uint32_t* context_lens, float* out,
+                                      const uint32_t* work, uint32_t n_work, kanso_stream_t stream) {
+    if (!ctx) {
+        set_error("kanso_ragged_paged_attention_work: null context");
+        return KANSO_E_INVALID_ARG;
+    }
+    if (!work || n_work == 0) {
+        set_error("kanso_ragged_paged_attention_work: empty work list");
+        return KANSO_E_INVALID_ARG;
+    }
+    return run_ragged(ctx, p, q, k_pool, v_pool, k_scales, v_scales, block_tables, cu_seqlens, context_lens, out,
+                      as_stream(stream), "kanso_ragged_paged_attention_work", false, nullptr, work, n_work);
 }
 
 int kanso_validate_paged_attention_params(const kanso_paged_attention_params* p) {

@@ -382,28 +382,22 @@ int model_forward(kanso_model* m, const HostStep& step, float* logits, uint32_t*
     ap.kv_dtype = m->kv_dtype;
     ap.num_blocks = m->num_blocks;
     ap.max_q_len = max_q;
-    {
-        // The split-K partition from the step's planned lengths (the attention library
-        // alone only sees the table capacity). Measured on config 5: 10.96 k tok/s with
-        // the capacity-based choice, 11.2 k with the planned lengths.
-        std::vector<uint32_t> ql(S), cl(S);
-        for (uint32_t i = 0; i < S; ++i) {
-            ql[i] = step.plan[i].q_len;
-            cl[i] = step.plan[i].start_pos + step.plan[i].q_len;
-        }
-        ap.partition_size = kanso_ragged_partition_size(m->ctx, &ap, ql.data(), cl.data());
-        ap.chunk_partition_size = kanso_ragged_chunk_partition_size(m->ctx, &ap, ql.data(), cl.data());
+    // The split-K partition from the step's planned lengths (the attention library
+    // alone only sees the table capacity). Measured on config 5: 10.96 k tok/s with
+    // the capacity-based choice, 11.2 k with the planned lengths.
+    std::vector<uint32_t> ql(S), cl(S);
+    for (uint32_t i = 0; i < S; ++i) {
+        ql[i] = step.plan[i].q_len;
+        cl[i] = step.plan[i].start_pos + step.plan[i].q_len;
     }
-    // A step of single-row sequences takes the attention's work-list path: the items
-    // (row, partition) with their block ids come from the host's plan in the same
-    // upload as the plan, so an attention wave's first load is its item and its
-    // second its keys (no sequence table, no block-table round trip).
-    const uint32_t cap = max_blocks * m->block_size;
-    const uint32_t P = ap.partition_size;
-    uint32_t n_items = 0;
-    const bool use_work = max_q == 1 && ragged_work_supported(&ap);
-    if (use_work)
-        for (const auto& p : step.plan) n_items += (std::min(p.start_pos + 1, cap) + P - 1) / P;
+    ap.partition_size = kanso_ragged_partition_size(m->ctx, &ap, ql.data(), cl.data());
+    ap.chunk_partition_size = kanso_ragged_chunk_partition_size(m->ctx, &ap, ql.data(), cl.data());
+    // The attention's decode rows take the work-list path (kanso_ragged_build_work):
+    // the items (row, partition) with their block ids come from the host's plan in
+    // the same upload as the plan, so an attention wave's first load is its item and
+    // its second its keys (no sequence table, no block-table round trip).
+    const uint32_t n_items = kanso_ragged_work_items(&ap, ql.data(), cl.data());
+    const bool use_work = n_items != 0;
     int rc = ensure_step_buffers(m, T, std::max(S, R), S * max_blocks,
                                  static_cast<uint32_t>(step.token_arena.size() + step.table_arena.size()),
                                  static_cast<size_t>(n_items) * kanso_ragged_work_item_words * 4);
@@ -429,23 +423,19 @@ int model_forward(kanso_model* m, const HostStep& step, float* logits, uint32_t*
     const size_t off_work = align_up(off_last + R * 4ull, 256);
     size_t stage_n = off_last + R * 4ull;
     if (use_work) {
-        uint32_t* wk = reinterpret_cast<uint32_t*>(h + off_work);
-        const uint32_t W = kanso_ragged_work_item_words, B = W - 4;
+        // the step's tables padded to [S][max_blocks] as the device holds them
+        // (PaddedDecodeTables: the last needed block repeats)
+        std::vector<uint32_t> tabs(static_cast<size_t>(S) * max_blocks, 0u);
         for (uint32_t i = 0; i < S; ++i) {
             const kanso_seq_plan& p = step.plan[i];
-            const uint32_t limit = std::min(p.start_pos + 1, cap);
-            const uint32_t* tab = step.table_arena.data() + p.table_offset;
-            for (uint32_t t0 = 0; t0 < limit; t0 += P, wk += W) {
-                const uint32_t t1 = std::min(t0 + P, limit);
-                const uint32_t b0 = t0 / m->block_size, nb = (t1 - 1) / m->block_size - b0 + 1;
-                for (uint32_t j = 0; j < B; ++j) wk[j] = j < nb && b0 + j < p.table_len ? tab[b0 + j] : 0u;
-                wk[B] = i;  // the row: one per sequence
-                wk[B + 1] = t0;
-                wk[B + 2] = t1;
-                wk[B + 3] = limit;
-            }
+            const uint32_t* t = step.table_arena.data() + p.table_offset;
+            for (uint32_t j = 0; j < max_blocks; ++j)
+                tabs[static_cast<size_t>(i) * max_blocks + j] = p.table_len ? t[std::min(j, p.table_len - 1)] : 0u;
         }
-        stage_n = off_work + static_cast<size_t>(n_items) * W * 4;
+        if ((rc = kanso_ragged_build_work(&ap, ql.data(), cl.data(), tabs.data(),
+                                          reinterpret_cast<uint32_t*>(h + off_work), n_items)))
+            return rc;
+        stage_n = off_work + static_cast<size_t>(n_items) * kanso_ragged_work_item_words * 4;
     }
     KANSO_HIP_TRY(hipMemcpyAsync(m->d_stage, h, stage_n, hipMemcpyHostToDevice, s));
     char* d = static_cast<char*>(m->d_stage);

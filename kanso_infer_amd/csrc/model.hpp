@@ -35,7 +35,7 @@ int op_ragged_attention(kanso_ctx* ctx, const kanso_ragged_attention_params* p, 
                         const void* v_pool, const void* k_scales, const void* v_scales, const uint32_t* block_tables,
                         const int32_t* cu_seqlens, const uint32_t* context_lens, float* out, hipStream_t s,
                         bool out_tiled, const uint32_t* work = nullptr, uint32_t n_work = 0);
-constexpr uint32_t kanso_ragged_work_item_words = 64;  // 60 block ids + row, first key, end key, key count
+constexpr uint32_t kanso_ragged_work_item_words = KANSO_RAGGED_WORK_ITEM_WORDS;  // 60 block ids + 4 header words
 bool ragged_work_supported(const kanso_ragged_attention_params* p);
 
 // One step as the scheduler hands it over: the compact plan plus the token and

@@ -1,6 +1,8 @@
 """The C-ABI library loads and exports every symbol include/kanso_hip.h declares
 (no compute calls: this runs without a GPU)."""
 import re
+
+import numpy as np
 from pathlib import Path
 
 import pytest
@@ -38,3 +40,33 @@ def test_no_fallback_when_library_missing(monkeypatch, tmp_path):
     monkeypatch.setenv("KANSO_HIP_LIB", str(tmp_path / "missing.so"))
     with pytest.raises(RuntimeError):
         _capi.load()
+
+
+def test_work_list_layout():
+    """kanso_ragged_build_work on the host: one 64-word item per (row, partition) of
+    every row outside the matrix-core chunk path, block ids first (the partition's
+    table slice), then row, first key, end key and the row's key count; a row
+    without keys or an FP8 pool gives no list."""
+    import kanso_infer_amd as K
+    q_lens = np.array([1, 1, 1], np.uint32)
+    ctx = np.array([40, 100, 1], np.uint32)
+    bs, P = 16, 32
+    tables = np.arange(3 * 8, dtype=np.uint32).reshape(3, 8) + 1000
+    geo = dict(num_heads=15, num_kv_heads=5, head_dim=64, block_size=bs, partition_size=P,
+               num_blocks=4096)
+    w = K.ragged_work(q_lens=q_lens, context_lens=ctx, block_tables=tables, **geo)
+    items = w.reshape(-1, 64)
+    want = []
+    for s, c in enumerate(ctx):
+        for t0 in range(0, int(c), P):
+            t1 = min(t0 + P, int(c))
+            blocks = list(tables[s, t0 // bs:(t1 - 1) // bs + 1])
+            want.append((blocks, s, t0, t1, int(c)))
+    assert items.shape[0] == len(want) == 2 + 4 + 1
+    for it, (blocks, row, t0, t1, lim) in zip(items, want):
+        assert list(it[:len(blocks)]) == blocks and not it[len(blocks):60].any()
+        assert list(it[60:]) == [row, t0, t1, lim]
+    assert K.ragged_work(q_lens=q_lens, context_lens=np.array([40, 0, 1], np.uint32),
+                         block_tables=tables, **geo) is None
+    assert K.ragged_work(q_lens=q_lens, context_lens=ctx, block_tables=tables, kv_dtype=K.KANSO_KV_FP8,
+                         **geo) is None

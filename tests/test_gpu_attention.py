@@ -345,3 +345,43 @@ def test_partition_from_host_lengths(ctx, variant):
     assert_close(got, want, what=f"{variant} P {P}")
     assert K.ragged_partition_size(ctx, q_lens=[], context_lens=[], num_heads=15, num_kv_heads=5,
                                    head_dim=64, block_size=16, max_blocks=4) == 0
+
+
+@pytest.mark.parametrize("case", ["small_mixed", "decode_only", "config2_small_pool", "int8", "q8_0"])
+def test_work_list_equals_table_path(ctx, case):
+    """kanso_ragged_paged_attention_work with the host-built decode work list gives the
+    table-driven call's output bit for bit (same item arithmetic, only the way a
+    wave finds its item differs), for mixed and decode-only batches and 1-byte pools."""
+    kv = {"int8": oracle.KV_INT8, "q8_0": oracle.KV_Q8_0}.get(case, oracle.KV_F32)
+    if case == "decode_only":
+        b = workloads.config1_decode(seed_offset=6)
+    elif case == "config2_small_pool":
+        b = workloads.config2_mixed(num_blocks=10000, seed_offset=2)
+    elif case in ("int8", "q8_0"):
+        b = workloads.config3_quant_decode(seed_offset=1)
+    else:
+        b = workloads.small_mixed(7)
+    kp, vp, ks, vs = fill_pool(b, kv, 21)
+    q = np.random.default_rng(22).standard_normal(
+        b.total_q * b.num_heads * b.head_dim).astype(np.float32)
+    geo = dict(num_heads=b.num_heads, num_kv_heads=b.num_kv_heads, head_dim=b.head_dim,
+               block_size=b.block_size)
+    P = K.ragged_partition_size(ctx, q_lens=b.q_lens, context_lens=b.context_lens,
+                                max_blocks=b.max_blocks, kv_dtype=kv, num_blocks=b.num_blocks, **geo)
+    work = K.ragged_work(q_lens=b.q_lens, context_lens=b.context_lens, block_tables=b.block_tables,
+                         partition_size=P, kv_dtype=kv, num_blocks=b.num_blocks,
+                         max_q_len=int(b.q_lens.max()), **geo)
+    assert work is not None
+
+    def call(w):
+        out = torch.empty(b.total_q * b.num_heads * b.head_dim, device="cuda:0")
+        K.ragged_paged_attention(
+            ctx, q=dev(q), k_pool=dev(kp), v_pool=dev(vp), k_scales=None if ks is None else dev(ks),
+            v_scales=None if vs is None else dev(vs), block_tables=dev(b.block_tables.ravel()),
+            cu_seqlens=dev(b.cu_seqlens), context_lens=dev(b.context_lens.astype(np.uint32)), out=out,
+            scale=b.scale, kv_dtype=kv, num_blocks=b.num_blocks, max_q_len=int(b.q_lens.max()),
+            partition_size=P, work=None if w is None else dev(w), **geo)
+        ctx.check_device_status()
+        return host(out)
+
+    np.testing.assert_array_equal(call(work), call(None))
