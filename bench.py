@@ -817,7 +817,7 @@ def main():
     extras = {}
     extras["partitions"] = [d["P"] for d in hb.dev_batches]
     extras["work_list"] = [d["work"] is not None for d in hb.dev_batches]
-    if WORK:
+    if WORK and not args.quick:
         # the same batches through the table-driven path (no work list)
         WORK = False
         tp = AttnBench.__new__(AttnBench)
