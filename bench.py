@@ -127,14 +127,16 @@ class AttnBench:
                     block_size=b.block_size, partition_size=d["P"], kv_dtype=self.kv_dtype,
                     num_blocks=self.num_blocks, max_q_len=int(b.q_lens.max()), pool_layout=POOL_LAYOUT,
                     chunk_partition_size=d["CP"])
-            d["work"] = None if w is None else self.torch.from_numpy(w.view(np.int32)).to("cuda:0")
+            d["work"] = None if w is None else self.torch.from_numpy(w[0].view(np.int32)).to("cuda:0")
+            d["work_chunk"] = 0 if w is None else w[1]
         self.K.ragged_paged_attention(
             self.ctx, q=d["q"], k_pool=self.k, v_pool=self.v, k_scales=self.ks, v_scales=self.vs,
             block_tables=d["tables"], cu_seqlens=d["cu"], context_lens=d["lens"], out=d["out"],
             num_heads=b.num_heads, num_kv_heads=b.num_kv_heads, head_dim=b.head_dim,
             block_size=b.block_size, scale=b.scale, kv_dtype=self.kv_dtype,
             num_blocks=self.num_blocks, max_q_len=int(b.q_lens.max()),
-            pool_layout=POOL_LAYOUT, partition_size=d["P"], chunk_partition_size=d["CP"], work=d["work"])
+            pool_layout=POOL_LAYOUT, partition_size=d["P"], chunk_partition_size=d["CP"], work=d["work"],
+            work_chunk_items=d["work_chunk"])
 
     def run(self, steps, warmup):
         torch = self.torch
@@ -822,7 +824,7 @@ def main():
         WORK = False
         tp = AttnBench.__new__(AttnBench)
         tp.__dict__.update(hb.__dict__)
-        tp.dev_batches = [{k: v for k, v in d.items() if k not in ("P", "work")} for d in hb.dev_batches]
+        tp.dev_batches = [{k: v for k, v in d.items() if k not in ("P", "work", "work_chunk")} for d in hb.dev_batches]
         rt = tp.run(args.steps, args.warmup)
         WORK = True
         extras["headline_table_path"] = dict(
@@ -835,7 +837,7 @@ def main():
         PARTITION = -1
         lib = AttnBench.__new__(AttnBench)
         lib.__dict__.update(hb.__dict__)
-        lib.dev_batches = [{k: v for k, v in d.items() if k not in ("P", "work")} for d in hb.dev_batches]
+        lib.dev_batches = [{k: v for k, v in d.items() if k not in ("P", "work", "work_chunk")} for d in hb.dev_batches]
         rl = lib.run(args.steps, args.warmup)
         PARTITION = 0
         extras["headline_library_partition"] = dict(
@@ -975,7 +977,7 @@ def main():
             "rotation": "8 batches",
             "partition": "per batch from its host-side lengths (kanso_ragged_partition_size), "
                          "as the engine passes it from its plan",
-            "work_list": ("decode rows from the work list built on the host from the same plan "
+            "work_list": ("rows from the work list built on the host from the same plan "
                           "(kanso_ragged_build_work, uploaded once per batch outside the timed "
                           "region as the engine uploads it with each step's plan)") if WORK else None,
         },

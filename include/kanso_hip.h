@@ -211,25 +211,28 @@ int kanso_ragged_paged_attention(kanso_ctx* ctx, const kanso_ragged_attention_pa
                                  const uint32_t* context_lens, float* out,
                                  kanso_stream_t stream);
 
-/* Decode work list of a planned batch. The caller that planned the step holds its
- * query lengths, context lengths and block tables on the host (Engine::step's
+/* Work list of a planned batch. The caller that planned the step holds its query
+ * lengths, context lengths and block tables on the host (Engine::step's
  * query_lens / context_lens / block tables, src/engine.rs:376-402); from them
- * kanso_ragged_build_work writes one item of KANSO_RAGGED_WORK_ITEM_WORDS u32 per
- * (row, partition) of every row outside the matrix-core chunk path: the
- * partition's physical block ids, then the row, its first key, its end key and the
- * row's key count. kanso_ragged_paged_attention_work then takes that list (uploaded
- * to the device) instead of deriving the items from the sequence and block tables:
- * an attention wave's first load is its item, its second its keys. Results are
- * bit-identical to kanso_ragged_paged_attention's. p->partition_size must be set
- * (kanso_ragged_partition_size), at most 60 blocks; INT8 / Q8_0 / F32 pools,
- * token-major layout. kanso_ragged_work_items returns the item count, 0 when the
- * batch cannot take a list (then call kanso_ragged_paged_attention). No
- * counterpart in the reference (the Metal kernel derives its work from the grid).
- * block_tables is the host copy of the [num_seqs][max_num_blocks_per_seq] table
- * the attention call reads. Host-only; launch nothing. */
+ * kanso_ragged_build_work writes items of KANSO_RAGGED_WORK_ITEM_WORDS u32: first one
+ * per (row, partition) of every row outside the matrix-core chunk path (the
+ * partition's physical block ids, then row, first key, end key, the row's key
+ * count), then one per (64-row block, chunk partition) of the sequences on that path
+ * (block ids, then first row, rows, key position of the first row, partition).
+ * kanso_ragged_paged_attention_work takes that list (uploaded to the device) instead
+ * of deriving the items from the sequence and block tables: a wave's first load is
+ * its item, its second its keys. Results are bit-identical to
+ * kanso_ragged_paged_attention's. p->partition_size must be set
+ * (kanso_ragged_partition_size); partitions of at most 60 blocks; F32 / INT8 / Q8_0
+ * pools, token-major layout; every row must have a key. kanso_ragged_work_items
+ * returns the item count (and the chunk items among them), 0 when the batch cannot
+ * take a list (then call kanso_ragged_paged_attention). No counterpart in the
+ * reference (the Metal kernel derives its work from the grid). block_tables is the
+ * host copy of the [num_seqs][max_num_blocks_per_seq] table the attention call
+ * reads. The first two are host-only and launch nothing. */
 #define KANSO_RAGGED_WORK_ITEM_WORDS 64u
 uint32_t kanso_ragged_work_items(const kanso_ragged_attention_params* p, const uint32_t* q_lens,
-                                 const uint32_t* context_lens);
+                                 const uint32_t* context_lens, uint32_t* n_chunk_items);
 int kanso_ragged_build_work(const kanso_ragged_attention_params* p, const uint32_t* q_lens,
                             const uint32_t* context_lens, const uint32_t* block_tables, uint32_t* work,
                             uint32_t n_items);
@@ -237,7 +240,8 @@ int kanso_ragged_paged_attention_work(kanso_ctx* ctx, const kanso_ragged_attenti
                                       const void* k_pool, const void* v_pool, const void* k_scales,
                                       const void* v_scales, const uint32_t* block_tables,
                                       const int32_t* cu_seqlens, const uint32_t* context_lens, float* out,
-                                      const uint32_t* work, uint32_t n_work, kanso_stream_t stream);
+                                      const uint32_t* work, uint32_t n_items, uint32_t n_chunk_items,
+                                      kanso_stream_t stream);
 
 /* kanso_ragged_paged_attention without any allocation: the same kernels, with
  * their split-K partials, statistics and per-row partition counts in a fixed

@@ -207,10 +207,11 @@ def ragged_paged_attention(ctx: Context, *, q: torch.Tensor, k_pool: torch.Tenso
                            v_scales: torch.Tensor | None = None, num_blocks: int = 0,
                            max_q_len: int = 0, pool_layout: int = 0, partition_size: int = 0,
                            chunk_partition_size: int = 0, work: torch.Tensor | None = None,
+                           work_chunk_items: int = 0,
                            stream: torch.cuda.Stream | None = None) -> None:
     """Mixed prefill + decode attention over the paged pool (kanso_ragged_paged_attention).
     cu_seqlens None: a decode batch, one query row per sequence. work: a device copy of
-    ragged_work's list (kanso_ragged_paged_attention_work)."""
+    ragged_work's list, work_chunk_items its chunk items (kanso_ragged_paged_attention_work)."""
     num_seqs = cu_seqlens.numel() - 1 if cu_seqlens is not None else context_lens.numel()
     max_blocks = block_tables.numel() // max(num_seqs, 1)
     total_q = q.numel() // (num_heads * head_dim)
@@ -223,16 +224,18 @@ def ragged_paged_attention(ctx: Context, *, q: torch.Tensor, k_pool: torch.Tenso
         _check(ctx._lib.kanso_ragged_paged_attention(*args, _stream(stream)))
     else:
         _check(ctx._lib.kanso_ragged_paged_attention_work(
-            *args, _ptr(work), work.numel() // _capi.KANSO_RAGGED_WORK_ITEM_WORDS, _stream(stream)))
+            *args, _ptr(work), work.numel() // _capi.KANSO_RAGGED_WORK_ITEM_WORDS, work_chunk_items,
+            _stream(stream)))
 
 
 def ragged_work(*, q_lens, context_lens, block_tables, num_heads: int, num_kv_heads: int,
                 head_dim: int, block_size: int, partition_size: int, kv_dtype: int = KANSO_KV_F32,
                 num_blocks: int = 0, max_q_len: int = 0, pool_layout: int = 0,
-                chunk_partition_size: int = 0) -> np.ndarray | None:
-    """The decode work list of a planned batch (kanso_ragged_build_work) from host
-    lengths and the host copy of the [S, max_blocks] block table; None when the batch
-    cannot take one (kanso_ragged_work_items == 0). Host-only."""
+                chunk_partition_size: int = 0) -> tuple[np.ndarray, int] | None:
+    """The work list of a planned batch (kanso_ragged_build_work) from host lengths and
+    the host copy of the [S, max_blocks] block table, and the number of chunk items
+    at its end; None when the batch cannot take one (kanso_ragged_work_items == 0).
+    Host-only."""
     lib = _capi.load()
     ql = np.ascontiguousarray(np.asarray(q_lens, dtype=np.uint32))
     cl = np.ascontiguousarray(np.asarray(context_lens, dtype=np.uint32))
@@ -240,15 +243,16 @@ def ragged_work(*, q_lens, context_lens, block_tables, num_heads: int, num_kv_he
     p = RaggedAttentionParamsC(ql.size, num_heads, num_kv_heads, head_dim, block_size, tabs.shape[1],
                                1.0, int(ql.sum()), kv_dtype, num_blocks, max_q_len, pool_layout,
                                partition_size, chunk_partition_size)
+    nc = C.c_uint32(0)
     n = int(lib.kanso_ragged_work_items(C.byref(p), ql.ctypes.data_as(C.c_void_p),
-                                        cl.ctypes.data_as(C.c_void_p)))
+                                        cl.ctypes.data_as(C.c_void_p), C.byref(nc)))
     if n == 0:
         return None
     out = np.zeros(n * _capi.KANSO_RAGGED_WORK_ITEM_WORDS, np.uint32)
     _check(lib.kanso_ragged_build_work(C.byref(p), ql.ctypes.data_as(C.c_void_p),
                                        cl.ctypes.data_as(C.c_void_p), tabs.ctypes.data_as(C.c_void_p),
                                        out.ctypes.data_as(C.c_void_p), n))
-    return out
+    return out, int(nc.value)
 
 
 def _lengths_call(fn, q_lens, context_lens, num_heads, num_kv_heads, head_dim, block_size,

@@ -155,10 +155,10 @@ SIGNATURES: dict[str, tuple] = {
     "kanso_ragged_chunk_partition_size": (C.c_uint32, [_P, C.POINTER(RaggedAttentionParamsC), _P, _P]),
     "kanso_ragged_paged_attention": (
         _I, [_P, C.POINTER(RaggedAttentionParamsC), _P, _P, _P, _P, _P, _P, _P, _P, _P, _P]),
-    "kanso_ragged_work_items": (C.c_uint32, [C.POINTER(RaggedAttentionParamsC), _P, _P]),
+    "kanso_ragged_work_items": (C.c_uint32, [C.POINTER(RaggedAttentionParamsC), _P, _P, _P]),
     "kanso_ragged_build_work": (_I, [C.POINTER(RaggedAttentionParamsC), _P, _P, _P, _P, _U]),
     "kanso_ragged_paged_attention_work": (
-        _I, [_P, C.POINTER(RaggedAttentionParamsC), _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _U, _P]),
+        _I, [_P, C.POINTER(RaggedAttentionParamsC), _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _U, _U, _P]),
     "kanso_ragged_paged_attention_noalloc": (
         _I, [_P, C.POINTER(RaggedAttentionParamsC), _P, _P, _P, _P, _P, _P, _P, _P, _P, _P]),
     "kanso_pack_step": (_I, [_P, _P, _U, _P, _P, _U, _U, _U, C.POINTER(PackedStepC), _P]),

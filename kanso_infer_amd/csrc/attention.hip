@@ -82,13 +82,15 @@ struct AttnArgs {
     uint32_t pool_bytes, scale_bytes;  // per pool tensor, for buffer resources (< 4 GiB)
     float scale_log2;
     uint32_t out_nbk;  // 0: out is row-major [T][H][D]; else the tiled activation order, K / 32
-    // Optional decode work list (a batch of single-row sequences whose caller planned
-    // the step): n_work items of kWorkWords words, item i = (row, partition) with
-    // words 0 .. kWorkBlocks-1 the partition's physical block ids and the last four
-    // row, first key, end key, the row's key count. Null: items come from the
-    // sequence tables.
+    // Optional work list built by the caller that planned the step: n_work decode
+    // items of kWorkWords words (row, partition: words 0 .. kWorkBlocks-1 the
+    // partition's physical block ids, the last four row, first key, end key, the
+    // row's key count), then n_work_chunk chunk items (64-row block, partition: the
+    // block ids, then first row, rows, key position of the first row, partition).
+    // Null: items come from the sequence tables.
     const uint32_t* work;
-    uint32_t n_work;
+    uint32_t n_work;        // decode items (first in the list)
+    uint32_t n_work_chunk;  // MFMA chunk items after them: 64 rows x partition each
 };
 
 constexpr uint32_t kWorkWords = kanso_ragged_work_item_words;
@@ -411,6 +413,7 @@ __device__ __forceinline__ float comp(const float4& v, int i) {
 struct PartView {
     uint32_t t_begin, t_end, blk0;
     int tab;
+    uint32_t kvh = 0;  // the item's KV head (chunk items)
 };
 
 __device__ __forceinline__ uint32_t block_of(const AttnArgs& a, uint32_t t) {
@@ -1193,23 +1196,19 @@ __device__ __forceinline__ void chunk_compute(const AttnArgs& a, const ChunkStag
 // One workgroup item: 64 query rows (wave w: rows 16w .. 16w + 15 of the block) of
 // one sequence, one key partition, one KV head.
 template <int G, int KVT>
-__device__ void chunk_block(const AttnArgs& a, const SeqTable& st, const PoolRsrc& rs, ChunkStage (&stage)[2],
-                            uint32_t row0,
-                            uint32_t part, int nrows_blk, uint32_t seq, uint32_t kvh) {
+__device__ void chunk_body(const AttnArgs& a, const PoolRsrc& rs, ChunkStage (&stage)[2], uint32_t row0,
+                           uint32_t part, int nrows_blk, int32_t pos0, const PartView& pv) {
+    // pos0: key position of the block's first row (ctx - q_len + its index in the
+    // sequence); row j of the block attends keys 0 ..= pos0 + j (row_limit)
     constexpr int D = 64;
     const int lane = threadIdx.x & (kWave - 1), wv = threadIdx.x / kWave;
-    const int32_t ql = st.cu[seq + 1] - st.cu[seq];
-    const int32_t ctx = st.ctx[seq];
-    const int32_t li0 = static_cast<int32_t>(row0) - st.cu[seq];
+    const uint32_t kvh = pv.kvh;
     const int nrows = min(kChunkWaveRows, nrows_blk - kChunkWaveRows * wv);  // this wave's rows (may be <= 0)
     const int qi = lane & 15;
     const bool qlive = qi < nrows;
     const uint32_t wrow0 = row0 + kChunkWaveRows * wv;
-    const uint32_t lim = qlive ? row_limit(ctx, ql, li0 + kChunkWaveRows * wv + qi, a.capacity) : 0;
-    const uint32_t lim_max = row_limit(ctx, ql, li0 + nrows_blk - 1, a.capacity);  // last row of the block
-    const uint32_t t_begin = part * a.chunk_part;
-    const uint32_t t_end = min(t_begin + a.chunk_part, lim_max);
-    const PartView pv = load_part(a, seq, t_begin, t_end, lane);
+    const uint32_t lim = qlive ? row_limit(pos0 + 1, 1, kChunkWaveRows * wv + qi, a.capacity) : 0;
+    const uint32_t t_begin = pv.t_begin, t_end = pv.t_end;
 
     Bf16Split qs[G][2];  // Q[query qi][d = 32 sd + 8 kq + j] as bf16 hi / lo (B operand of S^T)
     floatx4 o[G][4];
@@ -1278,6 +1277,19 @@ __device__ void chunk_block(const AttnArgs& a, const SeqTable& st, const PoolRsr
             if (!single && qq == 0) a.part_stats[head * a.max_parts + part] = make_float2(m[g], l[g]);
         }
     }
+}
+
+template <int G, int KVT>
+__device__ void chunk_block(const AttnArgs& a, const SeqTable& st, const PoolRsrc& rs, ChunkStage (&stage)[2],
+                            uint32_t row0, uint32_t part, int nrows_blk, uint32_t seq, uint32_t kvh) {
+    const int lane = threadIdx.x & (kWave - 1);
+    const int32_t ql = st.cu[seq + 1] - st.cu[seq];
+    const int32_t pos0 = st.ctx[seq] - ql + (static_cast<int32_t>(row0) - st.cu[seq]);
+    const uint32_t lim_max = row_limit(pos0 + 1, 1, nrows_blk - 1, a.capacity);  // last row of the block
+    const uint32_t t_begin = part * a.chunk_part;
+    PartView pv = load_part(a, seq, t_begin, min(t_begin + a.chunk_part, lim_max), lane);
+    pv.kvh = kvh;
+    chunk_body<G, KVT>(a, rs, stage, row0, part, nrows_blk, pos0, pv);
 }
 
 // Decode items from the caller's work list: one load per wave gives the item's row,
@@ -1357,6 +1369,44 @@ __global__ __launch_bounds__(kThreads, 2) void attn_main(AttnArgs a) {
     uint32_t n_chunk_wg = 0;
     if constexpr (GC > 0) {
         __shared__ ChunkStage stage[2];
+        if (a.use_mfma && a.work) {  // chunk and decode items from the caller's list
+            const uint32_t n_chunk = a.n_work_chunk * a.num_kv_heads;
+            n_chunk_wg = n_chunk < gridDim.x ? n_chunk : 0u;
+            const uint32_t stride = n_chunk_wg ? n_chunk_wg : gridDim.x;
+            if (n_chunk_wg == 0 || blockIdx.x < n_chunk_wg) {
+                const int lane = threadIdx.x & (kWave - 1);
+                for (uint32_t w = blockIdx.x; w < n_chunk; w += stride) {
+                    const uint32_t item = w / a.num_kv_heads;
+                    const uint32_t word =
+                        a.work[static_cast<size_t>(a.n_work + item) * kWorkWords + static_cast<uint32_t>(lane)];
+                    const uint32_t row0 = __builtin_amdgcn_readlane(word, kWorkBlocks);
+                    const int nrows = static_cast<int>(__builtin_amdgcn_readlane(word, kWorkBlocks + 1));
+                    const int32_t pos0 = static_cast<int32_t>(__builtin_amdgcn_readlane(word, kWorkBlocks + 2));
+                    const uint32_t part = __builtin_amdgcn_readlane(word, kWorkBlocks + 3);
+                    PartView pv;
+                    pv.kvh = w % a.num_kv_heads;
+                    pv.t_begin = part * a.chunk_part;
+                    pv.t_end = min(pv.t_begin + a.chunk_part, row_limit(pos0 + 1, 1, nrows - 1, a.capacity));
+                    pv.blk0 = block_of(a, pv.t_begin);
+                    const uint32_t nblk = block_of(a, pv.t_end - 1) - pv.blk0 + 1;  // <= kWorkBlocks (host-checked)
+                    uint32_t phys = static_cast<uint32_t>(lane) < nblk ? word : 0u;
+                    if (phys >= a.num_blocks) {
+                        raise_status(a.status, KANSO_DEV_BLOCK_OOB);
+                        phys = 0;
+                    }
+                    pv.tab = static_cast<int>(phys);
+                    if (part == 0 && pv.kvh == 0 && static_cast<int>(threadIdx.x) < nrows)
+                        a.row_np[row0 + threadIdx.x] =
+                            ceil_div(row_limit(pos0 + 1, 1, static_cast<int32_t>(threadIdx.x), a.capacity),
+                                     a.chunk_part);
+                    chunk_body<GC, KVT>(a, rs, stage, row0, part, nrows, pos0, pv);
+                    __syncthreads();  // the next item's prologue reuses the stages
+                }
+                if (n_chunk_wg) return;  // chunk workgroup: done
+            }
+            decode_work<D, GMAX, KVT, BUF, NL, NB>(a, rs, n_chunk_wg);
+            return;
+        }
         if (a.use_mfma) {
             load_seq_table<true>(a, st);
             const uint32_t n_chunk = st.pre[a.num_seqs] * a.num_kv_heads;
@@ -1383,10 +1433,6 @@ __global__ __launch_bounds__(kThreads, 2) void attn_main(AttnArgs a) {
                     __syncthreads();  // the next item's prologue reuses the stages
                 }
                 if (n_chunk_wg) return;  // chunk workgroup: done
-            }
-            if (a.work) {  // decode rows from the caller's list: no decode tables
-                decode_work<D, GMAX, KVT, BUF, NL, NB>(a, rs, n_chunk_wg);
-                return;
             }
             __syncthreads();  // the decode tables below overwrite the chunk tables
         }
@@ -1580,7 +1626,7 @@ int run_ragged(kanso_ctx* ctx, const kanso_ragged_attention_params* p, const flo
                const void* kp, const void* vp, const void* ks, const void* vs,
                const uint32_t* tables, const int32_t* cu, const uint32_t* ctx_lens, float* out,
                hipStream_t stream, const char* who, bool out_tiled = false, void* fixed_scratch = nullptr,
-               const uint32_t* work = nullptr, uint32_t n_work = 0) {
+               const uint32_t* work = nullptr, uint32_t n_work = 0, uint32_t n_work_chunk = 0) {
     const uint32_t S = p->num_seqs, H = p->num_heads, HKV = p->num_kv_heads, D = p->head_dim;
     const bool one_row_each = p->total_q == S && p->max_q_len == 1;
     if (!q || !kp || !vp || !tables || (!cu && !one_row_each) || !ctx_lens || !out) {
@@ -1691,6 +1737,7 @@ int run_ragged(kanso_ctx* ctx, const kanso_ragged_attention_params* p, const flo
     a.out_nbk = out_tiled ? H * D / 32 : 0u;
     a.work = nullptr;
     a.n_work = 0;
+    a.n_work_chunk = 0;
     a.status = ctx->status;
     a.num_seqs = S;
     a.num_heads = H;
@@ -1727,12 +1774,14 @@ int run_ragged(kanso_ctx* ctx, const kanso_ragged_attention_params* p, const flo
     if (work) {
         // the work-list path (kanso_ragged_build_work): decode rows from the list,
         // MFMA chunk rows (if any) from the sequence tables
-        if (!ragged_work_supported(p) || n_work == 0) {
+        if (!ragged_work_supported(p) || n_work + n_work_chunk == 0 || (n_work_chunk && !a.use_mfma) ||
+            CP > kWorkBlocks * p->block_size) {
             set_error("%s: work list given for a batch it cannot serve", who);
             return KANSO_E_INVALID_ARG;
         }
         a.work = work;
         a.n_work = n_work;
+        a.n_work_chunk = n_work_chunk;
     }
     const bool wide_merge = max_parts > 16;
     Stage1Fn reduce = pick_reduce(D, wide_merge);
@@ -1766,12 +1815,15 @@ bool ragged_work_supported(const kanso_ragged_attention_params* p) {
            p->num_heads % p->num_kv_heads == 0;
 }
 
-// The decode items of a batch (every row outside the MFMA chunk path, per partition)
-// in row order, or 0 when the batch cannot take a work list (a row without keys,
-// or parameters the list path does not serve). Fills `work` when given.
-uint64_t ragged_work(const kanso_ragged_attention_params* p, const uint32_t* q_lens, const uint32_t* context_lens,
-                     const uint32_t* block_tables, uint32_t* work) {
-    if (!ragged_work_supported(p)) return 0;
+// The work list of a batch: decode items (every row outside the MFMA chunk path, per
+// partition) in row order, then chunk items (each 64-row block of a multi-row
+// sequence on the MFMA path, per chunk partition). Returns false when the batch
+// cannot take a list (a row without keys, or parameters the list path does not
+// serve); fills `work` when given, and the two counts.
+bool ragged_work(const kanso_ragged_attention_params* p, const uint32_t* q_lens, const uint32_t* context_lens,
+                 const uint32_t* block_tables, uint32_t* work, uint64_t* n_decode, uint64_t* n_chunk) {
+    *n_decode = *n_chunk = 0;
+    if (!ragged_work_supported(p)) return false;
     const uint32_t S = p->num_seqs, P = p->partition_size, bs = p->block_size;
     const uint64_t cap64 = static_cast<uint64_t>(p->max_num_blocks_per_seq) * bs;
     const uint32_t cap = static_cast<uint32_t>(std::min<uint64_t>(cap64, 0xffffffffu));
@@ -1781,48 +1833,74 @@ uint64_t ragged_work(const kanso_ragged_attention_params* p, const uint32_t* q_l
         T += q_lens[s];
         max_q = std::max(max_q, q_lens[s]);
     }
-    if (T != p->total_q || T == 0) return 0;
+    if (T != p->total_q || T == 0) return false;
     const bool mfma = use_mfma_path(p, p->max_q_len ? p->max_q_len : max_q);
-    uint64_t n = 0;
-    uint32_t row = 0;
-    for (uint32_t s = 0; s < S; ++s) {
-        const uint32_t ql = q_lens[s], c = context_lens[s];
-        if (mfma && ql > 1) {
-            if (host_row_limit(c, ql, 0, cap) == 0) return 0;  // rows without keys: table path
-            row += ql;
-            continue;
-        }
-        for (uint32_t i = 0; i < ql; ++i, ++row) {
-            const uint32_t limit = host_row_limit(c, ql, i, cap);
-            if (limit == 0) return 0;
-            for (uint32_t t0 = 0; t0 < limit; t0 += P, ++n) {
-                if (!work) continue;
-                uint32_t* w = work + n * kWorkWords;
-                const uint32_t t1 = std::min(t0 + P, limit);
-                const uint32_t b0 = t0 / bs, nb = (t1 - 1) / bs - b0 + 1;
-                const uint32_t* tab = block_tables + static_cast<size_t>(s) * p->max_num_blocks_per_seq;
-                for (uint32_t j = 0; j < kWorkBlocks; ++j) w[j] = j < nb ? tab[b0 + j] : 0u;
-                w[kWorkBlocks] = row;
-                w[kWorkBlocks + 1] = t0;
-                w[kWorkBlocks + 2] = t1;
-                w[kWorkBlocks + 3] = limit;
+    const uint32_t CP = p->chunk_partition_size ? p->chunk_partition_size : chunk_partition(P, bs);
+    if (mfma && CP > kWorkBlocks * bs) return false;
+    // the item's block ids: keys [t0, t1) of sequence s
+    const auto blocks = [&](uint32_t* w, uint32_t s, uint32_t t0, uint32_t t1) {
+        const uint32_t b0 = t0 / bs, nb = (t1 - 1) / bs - b0 + 1;
+        const uint32_t* tab = block_tables + static_cast<size_t>(s) * p->max_num_blocks_per_seq;
+        for (uint32_t j = 0; j < kWorkBlocks; ++j) w[j] = j < nb ? tab[b0 + j] : 0u;
+    };
+    uint64_t nd = 0, nc = 0;
+    for (int pass = 0; pass < (work ? 2 : 1); ++pass) {
+        uint64_t di = 0, ci = 0;  // items written so far of each kind
+        uint32_t row = 0;
+        for (uint32_t s = 0; s < S; ++s) {
+            const uint32_t ql = q_lens[s], c = context_lens[s];
+            if (mfma && ql > 1) {
+                for (uint32_t i0 = 0; i0 < ql; i0 += kChunkBlockRows) {
+                    const uint32_t nrows = std::min<uint32_t>(kChunkBlockRows, ql - i0);
+                    if (host_row_limit(c, ql, i0, cap) == 0) return false;  // rows without keys: table path
+                    const uint32_t lim_max = host_row_limit(c, ql, i0 + nrows - 1, cap);
+                    for (uint32_t t0 = 0, part = 0; t0 < lim_max; t0 += CP, ++part, ++ci) {
+                        if (pass == 0) continue;
+                        uint32_t* w = work + (nd + ci) * kWorkWords;
+                        blocks(w, s, t0, std::min(t0 + CP, lim_max));
+                        w[kWorkBlocks] = row + i0;
+                        w[kWorkBlocks + 1] = nrows;
+                        w[kWorkBlocks + 2] = c - ql + i0;  // key position of the block's first row
+                        w[kWorkBlocks + 3] = part;
+                    }
+                }
+                row += ql;
+                continue;
+            }
+            for (uint32_t i = 0; i < ql; ++i, ++row) {
+                const uint32_t limit = host_row_limit(c, ql, i, cap);
+                if (limit == 0) return false;
+                for (uint32_t t0 = 0; t0 < limit; t0 += P, ++di) {
+                    if (pass == 0) continue;
+                    uint32_t* w = work + di * kWorkWords;
+                    const uint32_t t1 = std::min(t0 + P, limit);
+                    blocks(w, s, t0, t1);
+                    w[kWorkBlocks] = row;
+                    w[kWorkBlocks + 1] = t0;
+                    w[kWorkBlocks + 2] = t1;
+                    w[kWorkBlocks + 3] = limit;
+                }
             }
         }
+        nd = di;
+        nc = ci;
     }
-    return n;
+    *n_decode = nd;
+    *n_chunk = nc;
+    return nd + nc > 0;
 }
 
 int op_ragged_attention(kanso_ctx* ctx, const kanso_ragged_attention_params* p, const float* q, const void* k_pool,
                         const void* v_pool, const void* k_scales, const void* v_scales, const uint32_t* block_tables,
                         const int32_t* cu_seqlens, const uint32_t* context_lens, float* out, hipStream_t s,
-                        bool out_tiled, const uint32_t* work, uint32_t n_work) {
+                        bool out_tiled, const uint32_t* work, uint32_t n_work, uint32_t n_work_chunk) {
     if (out_tiled && (p->num_heads * p->head_dim) % 32 != 0) {
         set_error("ragged attention: tiled output needs heads x head_dim (%u) to be a multiple of 32",
                   p->num_heads * p->head_dim);
         return KANSO_E_INVALID_SHAPE;
     }
     return run_ragged(ctx, p, q, k_pool, v_pool, k_scales, v_scales, block_tables, cu_seqlens, context_lens, out, s,
-                      "ragged attention", out_tiled, nullptr, work, n_work);
+                      "ragged attention", out_tiled, nullptr, work, n_work, n_work_chunk);
 }
 
 int noalloc_scratch_init(void** ptr) {
@@ -1937,10 +2015,13 @@ uint32_t kanso_ragged_chunk_partition_size(const kanso_ctx* ctx, const kanso_rag
 }
 
 uint32_t kanso_ragged_work_items(const kanso_ragged_attention_params* p, const uint32_t* q_lens,
-                                 const uint32_t* context_lens) {
+                                 const uint32_t* context_lens, uint32_t* n_chunk_items) {
+    if (n_chunk_items) *n_chunk_items = 0;
     if (!p || !q_lens || !context_lens || p->num_seqs == 0) return 0;
-    const uint64_t n = ragged_work(p, q_lens, context_lens, nullptr, nullptr);
-    return n <= 0xffffffffu ? static_cast<uint32_t>(n) : 0u;
+    uint64_t nd = 0, nc = 0;
+    if (!ragged_work(p, q_lens, context_lens, nullptr, nullptr, &nd, &nc) || nd + nc > 0xffffffffu) return 0;
+    if (n_chunk_items) *n_chunk_items = static_cast<uint32_t>(nc);
+    return static_cast<uint32_t>(nd + nc);
 }
 
 int kanso_ragged_build_work(const kanso_ragged_attention_params* p, const uint32_t* q_lens,
@@ -1950,13 +2031,13 @@ int kanso_ragged_build_work(const kanso_ragged_attention_params* p, const uint32
         set_error("kanso_ragged_build_work: null argument");
         return KANSO_E_INVALID_ARG;
     }
-    const uint64_t n = ragged_work(p, q_lens, context_lens, nullptr, nullptr);
-    if (n == 0 || n != n_items) {
+    uint64_t nd = 0, nc = 0;
+    if (!ragged_work(p, q_lens, context_lens, nullptr, nullptr, &nd, &nc) || nd + nc != n_items) {
         set_error("kanso_ragged_build_work: the batch has %llu work items, the buffer %u",
-                  static_cast<unsigned long long>(n), n_items);
+                  static_cast<unsigned long long>(nd + nc), n_items);
         return KANSO_E_INVALID_SHAPE;
     }
-    ragged_work(p, q_lens, context_lens, block_tables, work);
+    ragged_work(p, q_lens, context_lens, block_tables, work, &nd, &nc);
     return KANSO_OK;
 }
 
@@ -1964,17 +2045,20 @@ int kanso_ragged_paged_attention_work(kanso_ctx* ctx, const kanso_ragged_attenti
                                       const void* k_pool, const void* v_pool, const void* k_scales,
                                       const void* v_scales, const uint32_t* block_tables,
                                       const int32_t* cu_seqlens, const uint32_t* context_lens, float* out,
-                                      const uint32_t* work, uint32_t n_work, kanso_stream_t stream) {
+                                      const uint32_t* work, uint32_t n_items, uint32_t n_chunk_items,
+                                      kanso_stream_t stream) {
     if (!ctx) {
         set_error("kanso_ragged_paged_attention_work: null context");
         return KANSO_E_INVALID_ARG;
     }
-    if (!work || n_work == 0) {
-        set_error("kanso_ragged_paged_attention_work: empty work list");
+    if (!work || n_items == 0 || n_chunk_items > n_items) {
+        set_error("kanso_ragged_paged_attention_work: empty work list or %u chunk items of %u", n_chunk_items,
+                  n_items);
         return KANSO_E_INVALID_ARG;
     }
     return run_ragged(ctx, p, q, k_pool, v_pool, k_scales, v_scales, block_tables, cu_seqlens, context_lens, out,
-                      as_stream(stream), "kanso_ragged_paged_attention_work", false, nullptr, work, n_work);
+                      as_stream(stream), "kanso_ragged_paged_attention_work", false, nullptr, work,
+                      n_items - n_chunk_items, n_chunk_items);
 }
 
 int kanso_validate_paged_attention_params(const kanso_paged_attention_params* p) {

@@ -392,11 +392,12 @@ int model_forward(kanso_model* m, const HostStep& step, float* logits, uint32_t*
     }
     ap.partition_size = kanso_ragged_partition_size(m->ctx, &ap, ql.data(), cl.data());
     ap.chunk_partition_size = kanso_ragged_chunk_partition_size(m->ctx, &ap, ql.data(), cl.data());
-    // The attention's decode rows take the work-list path (kanso_ragged_build_work):
-    // the items (row, partition) with their block ids come from the host's plan in
-    // the same upload as the plan, so an attention wave's first load is its item and
-    // its second its keys (no sequence table, no block-table round trip).
-    const uint32_t n_items = kanso_ragged_work_items(&ap, ql.data(), cl.data());
+    // The attention takes the work-list path (kanso_ragged_build_work): the items
+    // with their block ids come from the host's plan in the same upload as the plan,
+    // so an attention wave's first load is its item and its second its keys (no
+    // sequence table, no block-table round trip).
+    uint32_t n_chunk_items = 0;
+    const uint32_t n_items = kanso_ragged_work_items(&ap, ql.data(), cl.data(), &n_chunk_items);
     const bool use_work = n_items != 0;
     int rc = ensure_step_buffers(m, T, std::max(S, R), S * max_blocks,
                                  static_cast<uint32_t>(step.token_arena.size() + step.table_arena.size()),
@@ -484,7 +485,7 @@ int model_forward(kanso_model* m, const HostStep& step, float* logits, uint32_t*
             return rc;
         }
         if ((rc = op_ragged_attention(m->ctx, &ap, m->q, kp, vp, ks, vs, m->tables, m->cu, m->ctx_lens, m->attn, s,
-                                      true, d_work, n_items)))
+                                      true, d_work, n_items - n_chunk_items, n_chunk_items)))
             return rc;
         if ((rc = op_gemm_residual(o4 ? L.o_q4k : L.o, m->attn, m->hidden, c.hidden, qd, T, s, true, o4, res_mul)))
             return rc;

@@ -28,13 +28,13 @@ int op_lm_head_argmax(kanso_ctx* ctx, const void* w, const float* x, const int32
                       hipStream_t s, bool tiled, float logit_mul);
 // The ragged attention with its output in the tiled activation order (the O
 // projection's input) when out_tiled is set (attention.hip).
-// work / n_work: an optional decode work list (kanso_ragged_work_item_words words per
-// item, built by the caller for a batch of single-row sequences when
-// ragged_work_supported holds).
+// work: an optional work list (kanso_ragged_build_work): n_work decode items, then
+// n_work_chunk chunk items, kanso_ragged_work_item_words words each.
 int op_ragged_attention(kanso_ctx* ctx, const kanso_ragged_attention_params* p, const float* q, const void* k_pool,
                         const void* v_pool, const void* k_scales, const void* v_scales, const uint32_t* block_tables,
                         const int32_t* cu_seqlens, const uint32_t* context_lens, float* out, hipStream_t s,
-                        bool out_tiled, const uint32_t* work = nullptr, uint32_t n_work = 0);
+                        bool out_tiled, const uint32_t* work = nullptr, uint32_t n_work = 0,
+                        uint32_t n_work_chunk = 0);
 constexpr uint32_t kanso_ragged_work_item_words = KANSO_RAGGED_WORK_ITEM_WORDS;  // 60 block ids + 4 header words
 bool ragged_work_supported(const kanso_ragged_attention_params* p);
 

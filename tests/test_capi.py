@@ -54,7 +54,8 @@ def test_work_list_layout():
     tables = np.arange(3 * 8, dtype=np.uint32).reshape(3, 8) + 1000
     geo = dict(num_heads=15, num_kv_heads=5, head_dim=64, block_size=bs, partition_size=P,
                num_blocks=4096)
-    w = K.ragged_work(q_lens=q_lens, context_lens=ctx, block_tables=tables, **geo)
+    w, n_chunk = K.ragged_work(q_lens=q_lens, context_lens=ctx, block_tables=tables, **geo)
+    assert n_chunk == 0
     items = w.reshape(-1, 64)
     want = []
     for s, c in enumerate(ctx):
@@ -70,3 +71,29 @@ def test_work_list_layout():
                          block_tables=tables, **geo) is None
     assert K.ragged_work(q_lens=q_lens, context_lens=ctx, block_tables=tables, kv_dtype=K.KANSO_KV_FP8,
                          **geo) is None
+
+
+def test_work_list_chunk_items():
+    """A mixed batch: decode items first, then one chunk item per (64-row block,
+    chunk partition) of the multi-row sequence: block ids of the partition, then
+    first row, rows, key position of the first row, partition."""
+    import kanso_infer_amd as K
+    q_lens = np.array([1, 100, 1], np.uint32)   # a 100-row chunk between two decodes
+    ctx = np.array([50, 700, 20], np.uint32)     # the chunk's rows sit at keys 600 .. 699
+    bs, P, CP = 16, 32, 512
+    tables = np.arange(3 * 48, dtype=np.uint32).reshape(3, 48) + 7
+    w, n_chunk = K.ragged_work(q_lens=q_lens, context_lens=ctx, block_tables=tables, num_heads=15,
+                               num_kv_heads=5, head_dim=64, block_size=bs, partition_size=P,
+                               num_blocks=4096, max_q_len=100, chunk_partition_size=CP)
+    items = w.reshape(-1, 64)
+    n_dec = 2 + 1  # rows of 50 and 20 keys at 32-key partitions
+    assert items.shape[0] == n_dec + n_chunk
+    assert [list(it[60:]) for it in items[:n_dec]] == [[0, 0, 32, 50], [0, 32, 50, 50], [101, 0, 20, 20]]
+    # chunk blocks: rows 0-63 (keys up to 600 + 63 + 1 = 664: partitions 0, 1) and rows 64-99
+    # (keys up to 700: partitions 0, 1)
+    want = [(1, 64, 600, 0), (1, 64, 600, 1), (65, 36, 664, 0), (65, 36, 664, 1)]
+    assert [tuple(int(x) for x in it[60:]) for it in items[n_dec:]] == want
+    first = items[n_dec]
+    assert list(first[:32]) == list(tables[1, :32]) and not first[32:60].any()
+    second = items[n_dec + 1]  # keys 512 .. 663: blocks 32 .. 41
+    assert list(second[:10]) == list(tables[1, 32:42]) and not second[10:60].any()

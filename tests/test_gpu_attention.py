@@ -349,9 +349,10 @@ def test_partition_from_host_lengths(ctx, variant):
 
 @pytest.mark.parametrize("case", ["small_mixed", "decode_only", "config2_small_pool", "int8", "q8_0"])
 def test_work_list_equals_table_path(ctx, case):
-    """kanso_ragged_paged_attention_work with the host-built decode work list gives the
-    table-driven call's output bit for bit (same item arithmetic, only the way a
-    wave finds its item differs), for mixed and decode-only batches and 1-byte pools."""
+    """kanso_ragged_paged_attention_work with the host-built work list (decode and
+    chunk items) gives the table-driven call's output bit for bit (same item
+    arithmetic, only the way a wave finds its item differs), for mixed and
+    decode-only batches and 1-byte pools."""
     kv = {"int8": oracle.KV_INT8, "q8_0": oracle.KV_Q8_0}.get(case, oracle.KV_F32)
     if case == "decode_only":
         b = workloads.config1_decode(seed_offset=6)
@@ -372,6 +373,8 @@ def test_work_list_equals_table_path(ctx, case):
                          partition_size=P, kv_dtype=kv, num_blocks=b.num_blocks,
                          max_q_len=int(b.q_lens.max()), **geo)
     assert work is not None
+    work, n_chunk = work
+    assert (n_chunk > 0) == (case in ("small_mixed", "config2_small_pool"))
 
     def call(w):
         out = torch.empty(b.total_q * b.num_heads * b.head_dim, device="cuda:0")
@@ -380,7 +383,7 @@ def test_work_list_equals_table_path(ctx, case):
             v_scales=None if vs is None else dev(vs), block_tables=dev(b.block_tables.ravel()),
             cu_seqlens=dev(b.cu_seqlens), context_lens=dev(b.context_lens.astype(np.uint32)), out=out,
             scale=b.scale, kv_dtype=kv, num_blocks=b.num_blocks, max_q_len=int(b.q_lens.max()),
-            partition_size=P, work=None if w is None else dev(w), **geo)
+            partition_size=P, work=None if w is None else dev(w), work_chunk_items=n_chunk, **geo)
         ctx.check_device_status()
         return host(out)
 
