@@ -94,6 +94,7 @@ struct AttnArgs {
 };
 
 constexpr uint32_t kWorkWords = kanso_ragged_work_item_words;
+constexpr uint32_t kXcds = 8;  // MI355X: workgroup b of a launch runs on XCD b % 8
 constexpr uint32_t kWorkBlocks = kWorkWords - 4;
 
 // Output of query row `head / H`, head `head % H`, dims d .. (up to 4 consecutive
@@ -1370,13 +1371,21 @@ __global__ __launch_bounds__(kThreads, 2) void attn_main(AttnArgs a) {
     if constexpr (GC > 0) {
         __shared__ ChunkStage stage[2];
         if (a.use_mfma && a.work) {  // chunk and decode items from the caller's list
+            // Chunk work index L = kv_head * items + item, the list holding the row
+            // blocks of one (sequence, partition) next to each other; with a
+            // workgroup per item, the workgroups of XCD x (workgroup b runs on XCD
+            // b % 8) take the contiguous run of L from x * per, so the row blocks that
+            // read the same keys share an L2 rather than each fetching them from HBM.
             const uint32_t n_chunk = a.n_work_chunk * a.num_kv_heads;
-            n_chunk_wg = n_chunk < gridDim.x ? n_chunk : 0u;
+            const uint32_t per = (n_chunk + kXcds - 1) / kXcds;
+            n_chunk_wg = per * kXcds < gridDim.x ? per * kXcds : 0u;
             const uint32_t stride = n_chunk_wg ? n_chunk_wg : gridDim.x;
             if (n_chunk_wg == 0 || blockIdx.x < n_chunk_wg) {
                 const int lane = threadIdx.x & (kWave - 1);
-                for (uint32_t w = blockIdx.x; w < n_chunk; w += stride) {
-                    const uint32_t item = w / a.num_kv_heads;
+                for (uint32_t b = blockIdx.x; b < (n_chunk_wg ? n_chunk_wg : n_chunk); b += stride) {
+                    const uint32_t w = n_chunk_wg ? (b % kXcds) * per + b / kXcds : b;
+                    if (w >= n_chunk) continue;  // the round-up's idle workgroups
+                    const uint32_t item = w % a.n_work_chunk, kvh_w = w / a.n_work_chunk;
                     const uint32_t word =
                         a.work[static_cast<size_t>(a.n_work + item) * kWorkWords + static_cast<uint32_t>(lane)];
                     const uint32_t row0 = __builtin_amdgcn_readlane(word, kWorkBlocks);
@@ -1384,7 +1393,7 @@ __global__ __launch_bounds__(kThreads, 2) void attn_main(AttnArgs a) {
                     const int32_t pos0 = static_cast<int32_t>(__builtin_amdgcn_readlane(word, kWorkBlocks + 2));
                     const uint32_t part = __builtin_amdgcn_readlane(word, kWorkBlocks + 3);
                     PartView pv;
-                    pv.kvh = w % a.num_kv_heads;
+                    pv.kvh = kvh_w;
                     pv.t_begin = part * a.chunk_part;
                     pv.t_end = min(pv.t_begin + a.chunk_part, row_limit(pos0 + 1, 1, nrows - 1, a.capacity));
                     pv.blk0 = block_of(a, pv.t_begin);
@@ -1850,20 +1859,25 @@ bool ragged_work(const kanso_ragged_attention_params* p, const uint32_t* q_lens,
         for (uint32_t s = 0; s < S; ++s) {
             const uint32_t ql = q_lens[s], c = context_lens[s];
             if (mfma && ql > 1) {
-                for (uint32_t i0 = 0; i0 < ql; i0 += kChunkBlockRows) {
-                    const uint32_t nrows = std::min<uint32_t>(kChunkBlockRows, ql - i0);
-                    if (host_row_limit(c, ql, i0, cap) == 0) return false;  // rows without keys: table path
-                    const uint32_t lim_max = host_row_limit(c, ql, i0 + nrows - 1, cap);
-                    for (uint32_t t0 = 0, part = 0; t0 < lim_max; t0 += CP, ++part, ++ci) {
-                        if (pass == 0) continue;
-                        uint32_t* w = work + (nd + ci) * kWorkWords;
-                        blocks(w, s, t0, std::min(t0 + CP, lim_max));
-                        w[kWorkBlocks] = row + i0;
-                        w[kWorkBlocks + 1] = nrows;
-                        w[kWorkBlocks + 2] = c - ql + i0;  // key position of the block's first row
-                        w[kWorkBlocks + 3] = part;
+                if (host_row_limit(c, ql, 0, cap) == 0) return false;  // rows without keys: table path
+                // partition-major: the row blocks that read the same keys are adjacent
+                const uint32_t np_max = (host_row_limit(c, ql, ql - 1, cap) + CP - 1) / CP;
+                for (uint32_t part = 0; part < np_max; ++part)
+                    for (uint32_t i0 = 0; i0 < ql; i0 += kChunkBlockRows) {
+                        const uint32_t nrows = std::min<uint32_t>(kChunkBlockRows, ql - i0);
+                        const uint32_t lim_max = host_row_limit(c, ql, i0 + nrows - 1, cap);
+                        const uint32_t t0 = part * CP;
+                        if (t0 >= lim_max) continue;  // this block's rows end before the partition
+                        if (pass == 1) {
+                            uint32_t* w = work + (nd + ci) * kWorkWords;
+                            blocks(w, s, t0, std::min(t0 + CP, lim_max));
+                            w[kWorkBlocks] = row + i0;
+                            w[kWorkBlocks + 1] = nrows;
+                            w[kWorkBlocks + 2] = c - ql + i0;  // key position of the block's first row
+                            w[kWorkBlocks + 3] = part;
+                        }
+                        ++ci;
                     }
-                }
                 row += ql;
                 continue;
             }

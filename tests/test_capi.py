@@ -91,9 +91,9 @@ def test_work_list_chunk_items():
     assert [list(it[60:]) for it in items[:n_dec]] == [[0, 0, 32, 50], [0, 32, 50, 50], [101, 0, 20, 20]]
     # chunk blocks: rows 0-63 (keys up to 600 + 63 + 1 = 664: partitions 0, 1) and rows 64-99
     # (keys up to 700: partitions 0, 1)
-    want = [(1, 64, 600, 0), (1, 64, 600, 1), (65, 36, 664, 0), (65, 36, 664, 1)]
+    want = [(1, 64, 600, 0), (65, 36, 664, 0), (1, 64, 600, 1), (65, 36, 664, 1)]  # partition-major
     assert [tuple(int(x) for x in it[60:]) for it in items[n_dec:]] == want
     first = items[n_dec]
     assert list(first[:32]) == list(tables[1, :32]) and not first[32:60].any()
-    second = items[n_dec + 1]  # keys 512 .. 663: blocks 32 .. 41
+    second = items[n_dec + 2]  # rows 0-63, keys 512 .. 663: blocks 32 .. 41
     assert list(second[:10]) == list(tables[1, 32:42]) and not second[10:60].any()
