@@ -64,7 +64,9 @@ enum {
     KANSO_DEV_SLOT_OOB = 1u << 4,         /* slot >= num_blocks*block_size (kind.rs:130-137) */
     KANSO_DEV_BLOCK_OOB = 1u << 5,        /* physical block id >= num_blocks                 */
     KANSO_DEV_POSITION_OOB = 1u << 6,     /* position beyond the RoPE table                  */
-    KANSO_DEV_TOKEN_OOB = 1u << 7         /* token id >= vocab size                          */
+    KANSO_DEV_TOKEN_OOB = 1u << 7,        /* token id >= vocab size                          */
+    KANSO_DEV_PARTS_OOB = 1u << 8         /* a row's partition count beyond the partials'    */
+                                          /* capacity (a work list missing a row's items)    */
 };
 
 /* KV pool element types.
@@ -229,7 +231,11 @@ int kanso_ragged_paged_attention(kanso_ctx* ctx, const kanso_ragged_attention_pa
  * take a list (then call kanso_ragged_paged_attention). No counterpart in the
  * reference (the Metal kernel derives its work from the grid). block_tables is the
  * host copy of the [num_seqs][max_num_blocks_per_seq] table the attention call
- * reads. The first two are host-only and launch nothing. */
+ * reads. The first two are host-only and launch nothing. The list must be the one
+ * kanso_ragged_build_work wrote for these lengths: a list that leaves out a row's
+ * items leaves that row's output unwritten, and when its stale partition count
+ * exceeds the call's partials the merge skips the row and raises
+ * KANSO_DEV_PARTS_OOB. */
 #define KANSO_RAGGED_WORK_ITEM_WORDS 64u
 uint32_t kanso_ragged_work_items(const kanso_ragged_attention_params* p, const uint32_t* q_lens,
                                  const uint32_t* context_lens, uint32_t* n_chunk_items);

@@ -29,6 +29,7 @@ KANSO_DEV_SLOT_OOB = 1 << 4
 KANSO_DEV_BLOCK_OOB = 1 << 5
 KANSO_DEV_POSITION_OOB = 1 << 6
 KANSO_DEV_TOKEN_OOB = 1 << 7
+KANSO_DEV_PARTS_OOB = 1 << 8
 
 KANSO_KV_F32 = 0
 KANSO_KV_INT8 = 1

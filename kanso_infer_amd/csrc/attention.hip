@@ -1490,7 +1490,14 @@ __global__ __launch_bounds__(kThreads) void attn_reduce(AttnArgs a) {
     const uint32_t n_work = a.total_q * a.num_heads;
     for (uint32_t w = blockIdx.x * kGroups + threadIdx.x / LPG; w < n_work; w += n_groups) {
         const uint32_t row = w / a.num_heads, h = w % a.num_heads;
-        const uint32_t np = a.row_np[row];  // written by the main kernel for every row
+        // written by the main kernel for every row the call's items cover; a work list
+        // without a row's items leaves a stale count, which must not index past the
+        // row's partials
+        uint32_t np = a.row_np[row];
+        if (np > a.max_parts) {
+            if (h == 0) raise_status(a.status, KANSO_DEV_PARTS_OOB);
+            np = 0;
+        }
         if (np > 1) merge_partials<D, LPG>(a, static_cast<size_t>(row) * a.num_heads + h, np, lane);
     }
 }

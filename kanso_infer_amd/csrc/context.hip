@@ -178,6 +178,7 @@ int kanso_check_device_status(kanso_ctx* ctx, kanso_stream_t stream, uint32_t* f
         if (host & KANSO_DEV_BLOCK_OOB) msg += " physical block id outside the pool;";
         if (host & KANSO_DEV_POSITION_OOB) msg += " position beyond the RoPE table;";
         if (host & KANSO_DEV_TOKEN_OOB) msg += " token id beyond the vocabulary;";
+        if (host & KANSO_DEV_PARTS_OOB) msg += " partition count beyond the partials (work list without a row's items);";
         set_error("%s", msg.c_str());
         return KANSO_E_DEVICE_CHECK;
     }
